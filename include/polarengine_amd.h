@@ -1,0 +1,158 @@
+/*
+ * polarengine_amd.h -- C ABI of the MI355X (gfx950) PolarEngine quantized-linear
+ * library, libpolarengine_amd.so.
+ *
+ * Every entry point takes raw device pointers, sizes and a HIP stream
+ * (hipStream_t passed as void*, NULL = the null stream), launches
+ * asynchronously on that stream, allocates nothing, never synchronises the
+ * host, and returns an int status (PE_OK = 0). Outputs and workspaces are
+ * owned by the caller. Entry points are re-entrant; concurrent calls on one
+ * workspace race.
+ *
+ * Runtime weight layout (one quantized linear, N = out_f, Kp = in_f padded to
+ * a multiple of 128, nb = Kp / 128), as registered by the reference's
+ * PolarQuantLinearMethod.create_weights / process_weights_after_loading
+ * (polarengine_vllm/linear_method.py:119-135, 243-248):
+ *   bits 5..8 : codes int8  [N, Kp]         one code per byte (unsigned value)
+ *   bits 2..4 : codes uint8 [N, Kp/2]       half-block nibbles,
+ *               byte[n, 64*b + i] = code[n, 128*b + 64 + i] << 4 | code[n, 128*b + i]
+ *               (polarengine_vllm/packing.py:22-60)
+ *   norms     : float16 [N, nb]             per-block L2 norms
+ *   ct_scaled : float32 [2**bits]           Lloyd-Max centroids / sqrt(128)
+ *
+ * Transformed-activation layout "pair f16" (PE_XTF_PAIR_F16), produced by
+ * pe_fwht128 and consumed by the *_xtf entry points:
+ *   half2 xtf[M][nb][64], xtf[m][b][i] = (H x_m,b)[i], (H x_m,b)[i + 64]
+ * i.e. the two activations that one nibble byte multiplies sit in one dword.
+ */
+#ifndef POLARENGINE_AMD_H
+#define POLARENGINE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------- */
+enum {
+  PE_OK = 0,
+  PE_ERR_NULL = 1,      /* a required pointer is NULL                         */
+  PE_ERR_DIMS = 2,      /* bad size (K % 128, <= 0, above a kernel limit)     */
+  PE_ERR_BITS = 3,      /* unsupported bit width / n_levels / packing combo   */
+  PE_ERR_ALIGN = 4,     /* pointer not 16-byte aligned                        */
+  PE_ERR_DTYPE = 5,     /* unsupported dtype or layout code                   */
+  PE_ERR_WORKSPACE = 6, /* workspace NULL or smaller than the size query      */
+  PE_ERR_LAUNCH = 7,    /* hipGetLastError reported a launch failure          */
+  PE_ERR_DEVICE = 8     /* device query failed                                */
+};
+
+/* ---- dtype / layout codes ---------------------------------------------- */
+enum { PE_DTYPE_F16 = 0, PE_DTYPE_BF16 = 1, PE_DTYPE_F32 = 2 };
+enum {
+  PE_XTF_F32 = 0,      /* natural layout, float32 [rows, cols]              */
+  PE_XTF_F16 = 1,      /* natural layout, float16 [rows, cols]              */
+  PE_XTF_PAIR_F16 = 2  /* pair layout, see header comment                   */
+};
+
+/* Human-readable text for a status code (static storage). */
+const char* pe_status_string(int status);
+
+/* ABI version of this header; bumps on any signature change. */
+int pe_abi_version(void);
+
+/*
+ * Blockwise normalised Walsh-Hadamard transform over contiguous 128-blocks of
+ * each row: y[r, 128b:128b+128] = x[r, 128b:128b+128] @ H128.
+ * Replaces kernels/fwht.py:77-108 (fwht_matmul, x.reshape(-1,128) @ H) and the
+ * pybind fwht / fwht_ of kernels/cuda/fwht_cuda.cu:93-141. x_dtype is
+ * PE_DTYPE_F16/BF16/F32 with row stride ldx (elements); y_layout is a
+ * PE_XTF_* code (row stride = cols for the natural layouts). x == y is
+ * allowed for F32 -> PE_XTF_F32 (the in-place fwht_).
+ */
+int pe_fwht128(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t ldx,
+               void* y, int y_layout, void* stream);
+
+/*
+ * Reference native GEMV on int8 codes (bits 5..8, or unpacked 2..4):
+ * out[n] = sum_b norms[n,b] * sum_k ct_scaled[codes[n,128b+k]] * x_tf[128b+k].
+ * Replaces polar_gemv (kernels/polar_gemv.py:181-216; pybind
+ * kernels/cuda/polar_gemv_cuda.cu:261-307). x_tf is float32 [in_f_padded]
+ * (already transformed), out is float32 [out_f]. block_size must be 128;
+ * n_levels = len(ct_scaled) in [4, 256].
+ */
+int pe_polar_gemv(const int8_t* codes, const float* x_tf, const uint16_t* norms_f16,
+                  const float* ct_scaled, int n_levels, float* out, int out_f,
+                  int in_f_padded, int n_blocks, int block_size, void* stream);
+
+/*
+ * Same on half-block nibble codes (bits 2..4). Replaces polar_gemv_packed
+ * (kernels/polar_gemv.py:219-256; polar_gemv_cuda.cu:309-349) and the split-K
+ * variants polar_gemv[_packed]_splitk (kernels/polar_gemv_splitk.py:421-569),
+ * which compute the same function. in_f_half = n_blocks * 64.
+ */
+int pe_polar_gemv_packed(const uint8_t* packed, const float* x_tf, const uint16_t* norms_f16,
+                         const float* ct_scaled, int n_levels, float* out, int out_f,
+                         int in_f_half, int n_blocks, int block_size, void* stream);
+
+/*
+ * Batched form: out[M, out_f] (float32) = x_tf[M, in_f_padded] (float32,
+ * transformed) against the codes. packed = 1 for nibble codes. Replaces
+ * polar_matmul / polar_gemm[_packed] (kernels/polar_gemm.py:311-534).
+ * Needs a workspace of pe_polar_matmul_workspace_size(M, in_f_padded) bytes.
+ */
+size_t pe_polar_matmul_workspace_size(int64_t M, int in_f_padded);
+int pe_polar_matmul(const void* codes, int packed, const float* x_tf, int64_t M,
+                    const uint16_t* norms_f16, const float* ct_scaled, int n_levels,
+                    float* out, int out_f, int in_f_padded, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/*
+ * The quantized linear forward of PolarQuantLinearMethod.apply
+ * (polarengine_vllm/linear_method.py:157-222): pad -> FWHT -> quantized
+ * GEMV/GEMM (fp32 accumulate) -> cast -> + bias.
+ *   x      : [M, in_f] in x_dtype (PE_DTYPE_F16), row stride ldx
+ *   codes  : runtime layout for (bits, packed)
+ *   bias   : NULL or [out_f] in x_dtype
+ *   y      : [M, out_f] in x_dtype, row stride out_f
+ * Needs pe_linear_workspace_size(...) bytes of workspace (0 is valid when the
+ * query returns 0).
+ */
+size_t pe_linear_workspace_size(int64_t M, int in_f, int out_f, int bits, int packed);
+int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f, int64_t ldx,
+                      const void* codes, int bits, int packed, const uint16_t* norms_f16,
+                      const float* ct_scaled, int n_levels, const void* bias, void* y,
+                      int out_f, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Same, starting from an already-transformed activation in the pair-f16
+ * layout (the FWHTCache hit of linear_method.py:190-197, shared by Q/K/V).
+ * in_f_padded = 128 * nb of x_tf.
+ */
+size_t pe_linear_xtf_workspace_size(int64_t M, int in_f_padded, int out_f, int bits, int packed);
+int pe_linear_forward_xtf(const void* x_tf_pair, int64_t M, int in_f_padded,
+                          const void* codes, int bits, int packed, const uint16_t* norms_f16,
+                          const float* ct_scaled, int n_levels, const void* bias, int out_dtype,
+                          void* y, int out_f, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/*
+ * Nibble packing of int8 codes in [0, 15] (bit-exact): replaces
+ * pack_codes_int4 (kernels/polar_gemv.py:263-283), called by
+ * process_weights_after_loading (linear_method.py:243-248).
+ * codes int8 [rows, K] -> packed uint8 [rows, K/2]; K % 128 == 0.
+ */
+int pe_pack_nibble(const int8_t* codes, uint8_t* packed, int64_t rows, int64_t K, void* stream);
+
+/*
+ * On-disk Q5 (LSB-first, 8 codes in 5 bytes) to int8 codes, bit-exact:
+ * replaces unpack_codes_q5 (packing.py:163-209) as used by the loader
+ * (loader.py:412-417). packed uint8 [rows, K*5/8] -> codes int8 [rows, K].
+ */
+int pe_unpack_q5(const uint8_t* packed, int8_t* codes, int64_t rows, int64_t K, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* POLARENGINE_AMD_H */

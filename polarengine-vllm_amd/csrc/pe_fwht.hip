@@ -1,0 +1,116 @@
+// Blockwise FWHT-128 for gfx950.
+//
+// Replaces the reference's fwht_matmul (kernels/fwht.py:77-108), which runs
+// x.reshape(-1, 128) @ H as one fp32 SGEMM (128x the additions of a
+// butterfly), and the unwired CUDA butterfly (kernels/cuda/fwht_cuda.cu:35-86).
+// Here a 16-lane group owns one 128-block: 8 values per lane, 3 in-lane
+// stages and 4 cross-lane stages (lane xor 1/2/4/8), one 16-byte load and one
+// 16/32-byte store per lane. HBM-bound: 2*2 bytes per element for f16 in and
+// pair-f16 out.
+
+#include "pe_internal.h"
+
+namespace pe {
+
+template <int XDT, int YL, bool XFORM = true>
+__global__ __launch_bounds__(256) void fwht128_kernel(const void* x, void* y, int64_t rows,
+                                                      int nbc, int64_t ldx) {
+  const int64_t total = rows * (int64_t)nbc;
+  int64_t bid = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int q = threadIdx.x & 15;
+  const bool live = bid < total;
+  if (!live) bid = total - 1;  // keep the 16-lane group converged; store is masked
+  const int64_t r = bid / nbc;
+  const int cb = (int)(bid - r * nbc);
+  constexpr int esz = XDT == PE_DTYPE_F32 ? 4 : 2;
+  const char* src = reinterpret_cast<const char*>(x) + ((r * ldx) + (int64_t)cb * kBlock + q * 8) * esz;
+  float v[8];
+  load8<XDT>(src, v);
+  if constexpr (XFORM) fwht128_group16(v, q);
+
+  if constexpr (YL == PE_XTF_PAIR_F16) {
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = __shfl_xor(v[i], 8, 64);
+    if (!live) return;
+    uint4 w;
+    int p0;
+    if (q < 8) {
+      p0 = 8 * q;
+      w.x = pack_h2(v[0], o[0]); w.y = pack_h2(v[1], o[1]);
+      w.z = pack_h2(v[2], o[2]); w.w = pack_h2(v[3], o[3]);
+    } else {
+      p0 = 8 * (q - 8) + 4;
+      w.x = pack_h2(o[4], v[4]); w.y = pack_h2(o[5], v[5]);
+      w.z = pack_h2(o[6], v[6]); w.w = pack_h2(o[7], v[7]);
+    }
+    uint32_t* dst = reinterpret_cast<uint32_t*>(y) + (bid * 64 + p0);
+    *reinterpret_cast<uint4*>(dst) = w;
+  } else if constexpr (YL == PE_XTF_F32) {
+    if (!live) return;
+    float* dst = reinterpret_cast<float*>(y) + (r * (int64_t)nbc * kBlock + (int64_t)cb * kBlock + q * 8);
+    reinterpret_cast<float4*>(dst)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(dst)[1] = make_float4(v[4], v[5], v[6], v[7]);
+  } else {
+    if (!live) return;
+    uint16_t* dst = reinterpret_cast<uint16_t*>(y) + (r * (int64_t)nbc * kBlock + (int64_t)cb * kBlock + q * 8);
+    uint4 w;
+    w.x = pack_h2(v[0], v[1]); w.y = pack_h2(v[2], v[3]);
+    w.z = pack_h2(v[4], v[5]); w.w = pack_h2(v[6], v[7]);
+    *reinterpret_cast<uint4*>(dst) = w;
+  }
+}
+
+template <int XDT>
+static int launch_fwht(const void* x, int64_t rows, int nbc, int64_t ldx, void* y, int yl,
+                       hipStream_t st) {
+  const int64_t groups = rows * (int64_t)nbc;
+  const dim3 grid((unsigned)((groups + 15) / 16)), block(256);
+  switch (yl) {
+    case PE_XTF_F32: fwht128_kernel<XDT, PE_XTF_F32><<<grid, block, 0, st>>>(x, y, rows, nbc, ldx); break;
+    case PE_XTF_F16: fwht128_kernel<XDT, PE_XTF_F16><<<grid, block, 0, st>>>(x, y, rows, nbc, ldx); break;
+    case PE_XTF_PAIR_F16: fwht128_kernel<XDT, PE_XTF_PAIR_F16><<<grid, block, 0, st>>>(x, y, rows, nbc, ldx); break;
+    default: return PE_ERR_DTYPE;
+  }
+  return launch_status();
+}
+
+int fwht128(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t ldx, void* y,
+            int y_layout, hipStream_t st) {
+  if (!x || !y) return PE_ERR_NULL;
+  if (rows < 0 || cols <= 0 || cols % kBlock || ldx < cols) return PE_ERR_DIMS;
+  if (rows == 0) return PE_OK;
+  // grid = ceil(rows*nb/16) workgroups of 256 lanes; keep the lane count < 2^32.
+  if (cols / kBlock > (int64_t)INT32_MAX || rows * (cols / kBlock) > (int64_t(1) << 26)) return PE_ERR_DIMS;
+  if (!aligned16(x) || !aligned16(y)) return PE_ERR_ALIGN;
+  const int esz = x_dtype == PE_DTYPE_F32 ? 4 : 2;
+  if ((ldx * esz) % 16) return PE_ERR_ALIGN;
+  const int nbc = (int)(cols / kBlock);
+  switch (x_dtype) {
+    case PE_DTYPE_F16: return launch_fwht<PE_DTYPE_F16>(x, rows, nbc, ldx, y, y_layout, st);
+    case PE_DTYPE_BF16: return launch_fwht<PE_DTYPE_BF16>(x, rows, nbc, ldx, y, y_layout, st);
+    case PE_DTYPE_F32: return launch_fwht<PE_DTYPE_F32>(x, rows, nbc, ldx, y, y_layout, st);
+    default: return PE_ERR_DTYPE;
+  }
+}
+
+// Already-transformed fp32 activations (natural layout) -> pair f16, no
+// transform: the input of the reference API's batched polar_matmul.
+int repack_pair(const float* x, int64_t rows, int64_t cols, void* y, hipStream_t st) {
+  if (!x || !y) return PE_ERR_NULL;
+  if (rows < 0 || cols <= 0 || cols % kBlock || rows * (cols / kBlock) > (int64_t(1) << 26)) return PE_ERR_DIMS;
+  if (!aligned16(x) || !aligned16(y)) return PE_ERR_ALIGN;
+  if (rows == 0) return PE_OK;
+  const int nbc = (int)(cols / kBlock);
+  const int64_t groups = rows * (int64_t)nbc;
+  fwht128_kernel<PE_DTYPE_F32, PE_XTF_PAIR_F16, false>
+      <<<dim3((unsigned)((groups + 15) / 16)), dim3(256), 0, st>>>(x, y, rows, nbc, cols);
+  return launch_status();
+}
+
+}  // namespace pe
+
+extern "C" int pe_fwht128(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t ldx,
+                          void* y, int y_layout, void* stream) {
+  return pe::fwht128(x, x_dtype, rows, cols, ldx, y, y_layout, reinterpret_cast<hipStream_t>(stream));
+}

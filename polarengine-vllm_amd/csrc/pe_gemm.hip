@@ -1,0 +1,303 @@
+// Prefill GEMM for gfx950: Y[M, N] = X_tf[M, K] . W~[N, K]^T with
+// W~[n, k] = ct[code[n, k]] * norm[n, k / 128], fp16 operands on MFMA
+// (v_mfma_f32_32x32x16_f16), fp32 accumulate.
+//
+// Replaces polar_gemm / polar_gemm_packed (kernels/polar_gemm.py:81-171,
+// 211-418), which gather ct per tile and run tl.dot on fp32 tiles.
+//
+// Structure (one 256-lane workgroup = 2 x 2 waves, wave tile 32*TMW x 32*TNW):
+//  * K advances in half-blocks of 64 activations = 32 pairs; pair p of a
+//    128-block is (x[p], x[p + 64]), the two positions one nibble byte codes;
+//  * the activation tile (BM rows x 32 pairs, pair-f16) is staged global ->
+//    registers -> LDS, double-buffered, rows padded to 144 B so the
+//    ds_read_b128 of 8 consecutive rows hit distinct banks;
+//  * the weight operand never touches LDS as data: every wave loads its own
+//    codes (one dwordx4 per row per half-block for nibbles) one half-block
+//    ahead, and dequantizes in registers through the per-lane LDS codebook
+//    table (one v_perm + one ds_read_b32 per code byte) and a v_pk_mul_f16 by
+//    the block norm;
+//  * k-order inside an MFMA is the pair order: lane half h of slab t carries
+//    pairs 16h + 4t + j, j = 0..3, as (lo, hi) halves, identically for A and B.
+//  * workgroup ids are remapped so that each XCD (ids round-robin over 8)
+//    walks a contiguous range of tiles (M-tile fastest) and shares A/B in its
+//    own L2.
+
+#include "pe_internal.h"
+
+namespace pe {
+
+constexpr int kAStride = 144;  // bytes per A-tile row in LDS (128 + 16 pad)
+
+template <int OM>
+__device__ __forceinline__ void store_out(void* y, int64_t ldy, int m, int n, float v,
+                                          const uint16_t* bias) {
+  if constexpr (OM == 0) {
+    reinterpret_cast<float*>(y)[(int64_t)m * ldy + n] = v;
+  } else {
+    _Float16 h = (_Float16)v;
+    if (bias) h = (_Float16)((float)h + h2f(bias[n]));
+    reinterpret_cast<_Float16*>(y)[(int64_t)m * ldy + n] = h;
+  }
+}
+
+// Fill the per-lane codebook table. Nibble: half2(ct[lo], ct[hi]) per byte
+// value; int8: fp16 bits of ct[e] in the low half of the slot.
+template <bool NIB>
+__device__ __forceinline__ void fill_table_f16(uint32_t* tbl, const float* ct, int n_levels,
+                                               int entries, int tid, int nthreads) {
+  const int lane = tid & 63;
+  for (int e = tid >> 6; e < entries; e += nthreads >> 6) {
+    uint32_t val;
+    if constexpr (NIB) {
+      const int lo = e & 15, hi = e >> 4;
+      val = pack_h2(lo < n_levels ? ct[lo] : 0.f, hi < n_levels ? ct[hi] : 0.f);
+    } else {
+      val = (uint32_t)f2h_bits(ct[e]);
+    }
+    tbl[e * 64 + lane] = val;
+  }
+}
+
+// Dequantize one slab worth of B for one MFMA n-tile: 4 pair dwords.
+template <bool NIB>
+__device__ __forceinline__ half8v dequant_slab(const char* tbl, uint32_t wlo, uint32_t whi,
+                                               uint32_t lane4, half2v nrm2) {
+  uint32_t p[4];
+  if constexpr (NIB) {
+    p[0] = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<0>(wlo, lane4));
+    p[1] = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<1>(wlo, lane4));
+    p[2] = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<2>(wlo, lane4));
+    p[3] = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<3>(wlo, lane4));
+  } else {
+    const uint32_t a0 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<0>(wlo, lane4));
+    const uint32_t a1 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<1>(wlo, lane4));
+    const uint32_t a2 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<2>(wlo, lane4));
+    const uint32_t a3 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<3>(wlo, lane4));
+    const uint32_t b0 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<0>(whi, lane4));
+    const uint32_t b1 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<1>(whi, lane4));
+    const uint32_t b2 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<2>(whi, lane4));
+    const uint32_t b3 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<3>(whi, lane4));
+    // (lo16 of a, lo16 of b): bytes a0,a1,b0,b1 -> selector 0x05040100 over {b, a}
+    p[0] = __builtin_amdgcn_perm(b0, a0, 0x05040100u);
+    p[1] = __builtin_amdgcn_perm(b1, a1, 0x05040100u);
+    p[2] = __builtin_amdgcn_perm(b2, a2, 0x05040100u);
+    p[3] = __builtin_amdgcn_perm(b3, a3, 0x05040100u);
+  }
+  half8v r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const half2v v = as_h2(p[j]) * nrm2;
+    r[2 * j] = v[0];
+    r[2 * j + 1] = v[1];
+  }
+  return r;
+}
+
+template <bool NIB, int TMW, int TNW, int OM>
+__global__ __launch_bounds__(256) void gemm_kernel(
+    const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
+    const float* __restrict__ ct, int n_levels, uint32_t code_mask, int tbl_entries,
+    const uint32_t* __restrict__ xp, void* __restrict__ y, const uint16_t* __restrict__ bias,
+    int M, int N, int nb, int64_t ldy, int tiles_m, int tiles_total) {
+  constexpr int BM = 2 * TMW * 32;
+  constexpr int BN = 2 * TNW * 32;
+  constexpr int kAPerThread = BM * 8 / 256;  // uint4 of A per thread per half-block
+  extern __shared__ uint4 smem4[];
+  char* smem = reinterpret_cast<char*>(smem4);
+  char* tbl = smem;
+  char* abuf = smem + tbl_entries * 256;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int h = lane >> 5, l32 = lane & 31;
+  const uint32_t lane4 = (uint32_t)lane << 2;
+
+  // XCD-aware tile order: ids are dealt round-robin to 8 XCDs; give each XCD a
+  // contiguous range of logical tiles.
+  int wid = blockIdx.x;
+  if ((tiles_total & 7) == 0) wid = (wid & 7) * (tiles_total >> 3) + (wid >> 3);
+  const int tm = wid % tiles_m, tn = wid / tiles_m;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  fill_table_f16<NIB>(reinterpret_cast<uint32_t*>(tbl), ct, n_levels, tbl_entries, tid, 256);
+
+  // ---- A loader: thread t moves uint4 q = t + 256 i (row q >> 3, 16-byte col q & 7)
+  const int64_t xrow_u32 = (int64_t)nb * 64;  // uint32 per x_tf row
+  const uint32_t* a_src[kAPerThread];
+  int a_dst[kAPerThread];
+#pragma unroll
+  for (int i = 0; i < kAPerThread; ++i) {
+    const int q = tid + 256 * i;
+    const int r = q >> 3, c = q & 7;
+    int m = m0 + r;
+    if (m >= M) m = M - 1;  // clamped rows feed discarded outputs only
+    a_src[i] = xp + (int64_t)m * xrow_u32 + c * 4;
+    a_dst[i] = r * kAStride + c * 16;
+  }
+
+  // ---- B rows of this wave
+  const int row_bytes = NIB ? nb * 64 : nb * kBlock;
+  const uint8_t* b_row[TNW];
+  const uint16_t* n_row[TNW];
+#pragma unroll
+  for (int j = 0; j < TNW; ++j) {
+    int n = n0 + wn * TNW * 32 + j * 32 + l32;
+    if (n >= N) n = N - 1;
+    b_row[j] = codes + (int64_t)n * row_bytes + 16 * h;
+    n_row[j] = norms + (int64_t)n * nb;
+  }
+
+  const int nkt = 2 * nb;  // half-block K-tiles
+  uint4 a_reg[kAPerThread];
+  uint4 c_lo[TNW], c_hi[TNW];
+  uint16_t nrm_bits[TNW];
+
+  auto load_a = [&](int kt) {
+    const int b = kt >> 1, half = kt & 1;
+    const int off = b * 64 + half * 32;
+#pragma unroll
+    for (int i = 0; i < kAPerThread; ++i)
+      a_reg[i] = *reinterpret_cast<const uint4*>(a_src[i] + off);
+  };
+  auto store_a = [&](int buf) {
+    char* dst = abuf + buf * (BM * kAStride);
+#pragma unroll
+    for (int i = 0; i < kAPerThread; ++i) *reinterpret_cast<uint4*>(dst + a_dst[i]) = a_reg[i];
+  };
+  auto load_b = [&](int kt) {
+    const int b = kt >> 1, half = kt & 1;
+#pragma unroll
+    for (int j = 0; j < TNW; ++j) {
+      if constexpr (NIB) {
+        c_lo[j] = ld_nt16((b_row[j] + b * 64 + half * 32));
+      } else {
+        c_lo[j] = ld_nt16((b_row[j] + b * kBlock + half * 32));
+        c_hi[j] = ld_nt16((b_row[j] + b * kBlock + 64 + half * 32));
+      }
+      nrm_bits[j] = n_row[j][b];
+    }
+  };
+
+  float16v acc[TMW][TNW];
+#pragma unroll
+  for (int i = 0; i < TMW; ++i)
+#pragma unroll
+    for (int j = 0; j < TNW; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  load_a(0);
+  load_b(0);
+  store_a(0);
+  __syncthreads();
+
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int cur = kt & 1;
+    // current B operands out of the prefetch registers
+    uint4 cl[TNW], ch[TNW];
+    half2v nrm2[TNW];
+#pragma unroll
+    for (int j = 0; j < TNW; ++j) {
+      cl[j] = c_lo[j];
+      if constexpr (!NIB) ch[j] = c_hi[j];
+      const _Float16 nh = __builtin_bit_cast(_Float16, nrm_bits[j]);
+      nrm2[j] = half2v{nh, nh};
+    }
+    if (kt + 1 < nkt) {
+      load_a(kt + 1);
+      load_b(kt + 1);
+    }
+    const char* abase = abuf + cur * (BM * kAStride) + (wm * TMW * 32 + l32) * kAStride + 64 * h;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      half8v af[TMW];
+#pragma unroll
+      for (int i = 0; i < TMW; ++i)
+        af[i] = __builtin_bit_cast(half8v, *reinterpret_cast<const uint4*>(abase + i * 32 * kAStride + 16 * t));
+#pragma unroll
+      for (int j = 0; j < TNW; ++j) {
+        const uint32_t wl = (t == 0 ? cl[j].x : t == 1 ? cl[j].y : t == 2 ? cl[j].z : cl[j].w) & code_mask;
+        uint32_t wh = 0;
+        if constexpr (!NIB) wh = (t == 0 ? ch[j].x : t == 1 ? ch[j].y : t == 2 ? ch[j].z : ch[j].w) & code_mask;
+        const half8v bf = dequant_slab<NIB>(tbl, wl, wh, lane4, nrm2[j]);
+#pragma unroll
+        for (int i = 0; i < TMW; ++i)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf, acc[i][j], 0, 0, 0);
+      }
+    }
+    if (kt + 1 < nkt) store_a(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: acc[i][j][e] -> row 8*(e/4) + 4*h + e%4, col l32
+#pragma unroll
+  for (int i = 0; i < TMW; ++i) {
+#pragma unroll
+    for (int j = 0; j < TNW; ++j) {
+      const int n = n0 + wn * TNW * 32 + j * 32 + l32;
+      if (n >= N) continue;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = m0 + wm * TMW * 32 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+        if (m < M) store_out<OM>(y, ldy, m, n, acc[i][j][e], bias);
+      }
+    }
+  }
+}
+
+template <bool NIB, int TMW, int TNW, int OM>
+static int launch_gemm_t(const GemmArgs& a, hipStream_t st) {
+  constexpr int BM = 2 * TMW * 32, BN = 2 * TNW * 32;
+  auto kern = gemm_kernel<NIB, TMW, TNW, OM>;
+  const int entries = table_entries(NIB, a.n_levels);
+  const size_t lds = (size_t)entries * 256 + 2 * (size_t)BM * kAStride;
+  if (lds > 160 * 1024) return PE_ERR_DIMS;
+  static const bool attr_ok = [&] {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+  }();
+  (void)attr_ok;
+  const int tiles_m = (a.M + BM - 1) / BM;
+  const int tiles_n = (a.N + BN - 1) / BN;
+  const int64_t total = (int64_t)tiles_m * tiles_n;
+  if (total > INT32_MAX) return PE_ERR_DIMS;
+  const uint8_t mb = NIB ? (uint8_t)((a.n_levels - 1) * 0x11) : (uint8_t)(a.n_levels - 1);
+  kern<<<dim3((unsigned)total), dim3(256), lds, st>>>(
+      a.codes, a.norms, a.ct, a.n_levels, 0x01010101u * mb, entries,
+      reinterpret_cast<const uint32_t*>(a.xp), a.y, a.bias, a.M, a.N, a.nb, a.ldy, tiles_m,
+      (int)total);
+  return launch_status();
+}
+
+template <bool NIB, int OM>
+static int launch_gemm_shape(const GemmArgs& a, hipStream_t st) {
+  // tile shape by M: 256 x 256 for large M, narrower M tiles for small M
+  if (a.M > 128) return launch_gemm_t<NIB, 4, 4, OM>(a, st);
+  if (a.M > 64) return launch_gemm_t<NIB, 2, 4, OM>(a, st);
+  return launch_gemm_t<NIB, 1, 4, OM>(a, st);
+}
+
+int gemm(bool nibble, int omode, const GemmArgs& a, hipStream_t st) {
+  if (nibble) return omode == 0 ? launch_gemm_shape<true, 0>(a, st) : launch_gemm_shape<true, 1>(a, st);
+  return omode == 0 ? launch_gemm_shape<false, 0>(a, st) : launch_gemm_shape<false, 1>(a, st);
+}
+
+// Matmul on a pair-f16 x_tf, used by the linear entry points for M > 1.
+size_t mm_xtf_workspace(bool nibble, int64_t M, int N, int nb) {
+  (void)nibble; (void)M; (void)N; (void)nb;
+  return 0;
+}
+
+int mm_xtf(bool nibble, const void* codes, const uint16_t* norms, const float* ct, int n_levels,
+           const void* x_pair, int64_t M, int N, int nb, void* y, int out_mode, int64_t ldy,
+           const uint16_t* bias, void* ws, size_t ws_bytes, hipStream_t st) {
+  (void)ws; (void)ws_bytes;
+  if (M > INT32_MAX) return PE_ERR_DIMS;
+  GemmArgs a{reinterpret_cast<const uint8_t*>(codes), norms, ct, n_levels, x_pair, y, bias,
+             (int)M, N, nb, ldy};
+  return gemm(nibble, out_mode, a, st);
+}
+
+}  // namespace pe

@@ -1,0 +1,330 @@
+// Decode GEMV (M = 1) for gfx950: y[n] = sum_b norm[n,b] * <ct[codes[n,b,:]], x_tf[b,:]>.
+//
+// Replaces the reference's M = 1 kernels: polar_gemv / polar_gemv_packed
+// (kernels/polar_gemv.py:48-174), the split-K pair that polar_matmul routes
+// M = 1 to (kernels/polar_gemv_splitk.py:82-182, 257-328; dispatch
+// kernels/polar_gemm.py:485-504) and the unwired CUDA kernels
+// (kernels/cuda/polar_gemv_cuda.cu:52-254).
+//
+// Design (HBM-bound; 16 bytes of codes per lane per row):
+//  * persistent grid; a wave streams whole rows: lane l reads the 16-byte
+//    chunks l, l+64, ... of the row with one global_load_dwordx4 each, so one
+//    wave instruction covers 1 KB of contiguous codes;
+//  * the lane's slice of the transformed activation stays in registers for
+//    the whole kernel (16 half2 pairs per nibble chunk, 16 floats per int8
+//    chunk), staged once per workgroup through LDS -- by an in-kernel
+//    FWHT-128 of the raw fp16 activation (fused prologue) or from a given
+//    x_tf;
+//  * nibble codes: one LDS lookup per byte returns half2(ct[lo], ct[hi]),
+//    consumed by one v_dot2_f32_f16 against the pair (x[p], x[p+64]);
+//    int8 codes: one fp32 lookup + one FMA per code (the reference's fp32
+//    arithmetic);
+//  * the LDS table is replicated per lane (entry e of lane l at
+//    (e << 8) | (l << 2)) so lookups never conflict and the address is one
+//    v_perm_b32 of the code byte;
+//  * per-block fp16 norm applied in fp32 to the lane's chunk partial;
+//    a wave reduction finishes each row; no split-K, no second pass.
+
+#include "pe_internal.h"
+
+namespace pe {
+
+constexpr int kGemvThreads = 512;
+
+// Stage one transformed 128-block held by a 16-lane group (8 values per lane,
+// positions 8q..8q+7) into the kernel's LDS activation layout.
+template <bool NIB>
+__device__ __forceinline__ void stage_block(char* xs, int b, int q, const float v[8]) {
+  if constexpr (NIB) {
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = __shfl_xor(v[i], 8, 64);
+    uint4 w;
+    int p0;
+    if (q < 8) {
+      p0 = 8 * q;
+      w.x = pack_h2(v[0], o[0]); w.y = pack_h2(v[1], o[1]);
+      w.z = pack_h2(v[2], o[2]); w.w = pack_h2(v[3], o[3]);
+    } else {
+      p0 = 8 * (q - 8) + 4;
+      w.x = pack_h2(o[4], v[4]); w.y = pack_h2(o[5], v[5]);
+      w.z = pack_h2(o[6], v[6]); w.w = pack_h2(o[7], v[7]);
+    }
+    *reinterpret_cast<uint4*>(xs + (b * 64 + p0) * 4) = w;
+  } else {
+    float4* d = reinterpret_cast<float4*>(xs + (b * kBlock + 8 * q) * 4);
+    d[0] = make_float4(v[0], v[1], v[2], v[3]);
+    d[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+
+template <bool NIB, int S, int U, int XM, int OM>
+__global__ __launch_bounds__(kGemvThreads) void gemv1_kernel(
+    const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
+    const float* __restrict__ ct, int n_levels, uint32_t code_mask, int tbl_entries,
+    const void* __restrict__ x, void* __restrict__ y, const uint16_t* __restrict__ bias,
+    int N, int nb) {
+  extern __shared__ uint4 smem4[];
+  char* smem = reinterpret_cast<char*>(smem4);
+  uint32_t* tbl = reinterpret_cast<uint32_t*>(smem);
+  char* xs = smem + tbl_entries * 256;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  constexpr int kWaves = kGemvThreads / 64;
+  const int row_bytes = NIB ? nb * 64 : nb * kBlock;
+  const int C = row_bytes >> 4;  // 16-byte chunks per row
+
+  // ---- 1. codebook table, one copy per lane -------------------------------
+  for (int e = wave; e < tbl_entries; e += kWaves) {
+    uint32_t val;
+    if constexpr (NIB) {
+      const int lo = e & 15, hi = e >> 4;
+      const float a = lo < n_levels ? ct[lo] : 0.f;
+      const float c = hi < n_levels ? ct[hi] : 0.f;
+      val = pack_h2(a, c);
+    } else {
+      val = __float_as_uint(ct[e]);
+    }
+    tbl[e * 64 + lane] = val;
+  }
+
+  // ---- 2. transformed activation into LDS ----------------------------------
+  {
+    const int g = tid >> 4, q = tid & 15;
+    constexpr int kGroups = kGemvThreads / 16;
+    if constexpr (XM == XM_RAW_F16 || XM == XM_XTF_F32) {
+      for (int b = g; b < nb; b += kGroups) {
+        float v[8];
+        if constexpr (XM == XM_RAW_F16) {
+          load8<PE_DTYPE_F16>(reinterpret_cast<const uint16_t*>(x) + b * kBlock + q * 8, v);
+          fwht128_group16(v, q);
+        } else {
+          load8<PE_DTYPE_F32>(reinterpret_cast<const float*>(x) + b * kBlock + q * 8, v);
+        }
+        stage_block<NIB>(xs, b, q, v);
+      }
+    } else {  // pair f16 input: nb * 64 half2
+      const uint4* src = reinterpret_cast<const uint4*>(x);
+      if constexpr (NIB) {
+        for (int i = tid; i < nb * 16; i += kGemvThreads)
+          reinterpret_cast<uint4*>(xs)[i] = src[i];
+      } else {
+        // pairs p..p+3 of block b -> x[p..p+3] and x[p+64..p+67]
+        for (int i = tid; i < nb * 16; i += kGemvThreads) {
+          const uint4 w = src[i];
+          const int b = i >> 4, p = (i & 15) * 4;
+          const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+          float lo[4], hi[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            lo[j] = h2f((uint16_t)(ws[j] & 0xffff));
+            hi[j] = h2f((uint16_t)(ws[j] >> 16));
+          }
+          float* d = reinterpret_cast<float*>(xs) + b * kBlock + p;
+          *reinterpret_cast<float4*>(d) = make_float4(lo[0], lo[1], lo[2], lo[3]);
+          *reinterpret_cast<float4*>(d + 64) = make_float4(hi[0], hi[1], hi[2], hi[3]);
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- 3. this lane's activation slice into registers -----------------------
+  // nibble chunk c: block c>>2, pairs 16*(c&3) .. +15; int8 chunk c: block
+  // c>>3, positions 16*(c&7) .. +15.
+  uint32_t xr[S][16];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int c = s * 64 + lane;
+    if (c < C) {
+      const int off = NIB ? ((c >> 2) * 64 + (c & 3) * 16) * 4 : ((c >> 3) * kBlock + (c & 7) * 16) * 4;
+      const uint4* p = reinterpret_cast<const uint4*>(xs + off);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint4 w = p[j];
+        xr[s][4 * j] = w.x; xr[s][4 * j + 1] = w.y; xr[s][4 * j + 2] = w.z; xr[s][4 * j + 3] = w.w;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) xr[s][j] = 0u;
+    }
+  }
+
+  // ---- 4. stream rows --------------------------------------------------------
+  const uint32_t lane4 = (uint32_t)lane << 2;
+  const int gw = blockIdx.x * kWaves + wave;
+  const int tw = gridDim.x * kWaves;
+  const int nshift = NIB ? 2 : 3;  // chunk -> block
+
+  // rows gw, gw + tw, gw + 2 tw, ... (balanced to +-1 row per wave), U at a time
+  for (int k0 = 0; gw + k0 * tw < N; k0 += U) {
+    uint4 d[U][S];
+    float nrm[U][S];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int n = gw + (k0 + u) * tw;
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const int c = s * 64 + lane;
+        if (n < N && c < C) {
+          d[u][s] = ld_nt16((codes + (size_t)n * row_bytes) + c);
+          nrm[u][s] = h2f(norms[(size_t)n * nb + (c >> nshift)]);
+        } else {
+          d[u][s] = make_uint4(0, 0, 0, 0);
+          nrm[u][s] = 0.f;
+        }
+      }
+    }
+    float acc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float a = 0.f;
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const uint32_t ws[4] = {d[u][s].x & code_mask, d[u][s].y & code_mask,
+                                d[u][s].z & code_mask, d[u][s].w & code_mask};
+        float part = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t a0 = tbl_addr<0>(ws[j], lane4);
+          const uint32_t a1 = tbl_addr<1>(ws[j], lane4);
+          const uint32_t a2 = tbl_addr<2>(ws[j], lane4);
+          const uint32_t a3 = tbl_addr<3>(ws[j], lane4);
+          const uint32_t t0 = *reinterpret_cast<const uint32_t*>(smem + a0);
+          const uint32_t t1 = *reinterpret_cast<const uint32_t*>(smem + a1);
+          const uint32_t t2 = *reinterpret_cast<const uint32_t*>(smem + a2);
+          const uint32_t t3 = *reinterpret_cast<const uint32_t*>(smem + a3);
+          if constexpr (NIB) {
+            part = __builtin_amdgcn_fdot2(as_h2(t0), as_h2(xr[s][4 * j + 0]), part, false);
+            part = __builtin_amdgcn_fdot2(as_h2(t1), as_h2(xr[s][4 * j + 1]), part, false);
+            part = __builtin_amdgcn_fdot2(as_h2(t2), as_h2(xr[s][4 * j + 2]), part, false);
+            part = __builtin_amdgcn_fdot2(as_h2(t3), as_h2(xr[s][4 * j + 3]), part, false);
+          } else {
+            part = fmaf(__uint_as_float(t0), __uint_as_float(xr[s][4 * j + 0]), part);
+            part = fmaf(__uint_as_float(t1), __uint_as_float(xr[s][4 * j + 1]), part);
+            part = fmaf(__uint_as_float(t2), __uint_as_float(xr[s][4 * j + 2]), part);
+            part = fmaf(__uint_as_float(t3), __uint_as_float(xr[s][4 * j + 3]), part);
+          }
+        }
+        a = fmaf(part, nrm[u][s], a);
+      }
+      acc[u] = a;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc[u] = wave_sum(acc[u]);
+    if (lane < U) {
+      float r = acc[0];
+#pragma unroll
+      for (int u = 1; u < U; ++u)
+        if (lane == u) r = acc[u];
+      const int n = gw + (k0 + lane) * tw;
+      if (n < N) {
+        if constexpr (OM == OM_F32) {
+          reinterpret_cast<float*>(y)[n] = r;
+        } else {
+          // reference order: fp32 result -> .half() -> + bias.half() (fp16 add)
+          _Float16 h = (_Float16)r;
+          if (bias) h = (_Float16)((float)h + h2f(bias[n]));
+          reinterpret_cast<_Float16*>(y)[n] = h;
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host launch
+// ---------------------------------------------------------------------------
+
+template <bool NIB, int S, int XM, int OM>
+static int launch_gemv1_s(const Gemv1Args& a, hipStream_t st) {
+  constexpr int U = S <= 2 ? 4 : (S <= 6 ? 2 : 1);
+  auto kern = gemv1_kernel<NIB, S, U, XM, OM>;
+  const int entries = table_entries(NIB, a.n_levels);
+  const size_t lds = (size_t)entries * 256 + (size_t)a.nb * (NIB ? 256 : 512);
+  if (lds > 160 * 1024) return PE_ERR_DIMS;
+  static const bool attr_ok = [&] {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+  }();
+  (void)attr_ok;
+  const int per_cu = lds <= 80 * 1024 ? 2 : 1;
+  // enough waves for one row each, capped at what stays resident
+  constexpr int kWaves = kGemvThreads / 64;
+  int grid = (a.N + kWaves - 1) / kWaves;
+  const int cap = num_cus() * per_cu;
+  if (grid > cap) grid = cap;
+  const uint8_t mb = NIB ? (uint8_t)((a.n_levels - 1) * 0x11) : (uint8_t)(a.n_levels - 1);
+  const uint32_t mask = 0x01010101u * mb;
+  kern<<<dim3(grid), dim3(kGemvThreads), lds, st>>>(a.codes, a.norms, a.ct, a.n_levels, mask,
+                                                   entries, a.x, a.y, a.bias, a.N, a.nb);
+  return launch_status();
+}
+
+template <bool NIB, int XM, int OM>
+static int launch_gemv1(const Gemv1Args& a, hipStream_t st) {
+  const int C = (NIB ? a.nb * 64 : a.nb * kBlock) / 16;
+  if (C <= 64) return launch_gemv1_s<NIB, 1, XM, OM>(a, st);
+  if (C <= 128) return launch_gemv1_s<NIB, 2, XM, OM>(a, st);
+  if (C <= 192) return launch_gemv1_s<NIB, 3, XM, OM>(a, st);
+  if (C <= 256) return launch_gemv1_s<NIB, 4, XM, OM>(a, st);
+  if (C <= 384) return launch_gemv1_s<NIB, 6, XM, OM>(a, st);
+  if (C <= 512) return launch_gemv1_s<NIB, 8, XM, OM>(a, st);
+  return PE_ERR_DIMS;
+}
+
+// Largest K (padded) the register-resident M = 1 kernel takes.
+int gemv1_max_kp(bool nibble) { return nibble ? 512 * 32 : 512 * 16; }
+
+int gemv1(bool nibble, int xmode, int omode, const Gemv1Args& a, hipStream_t st) {
+  if (nibble) {
+    if (xmode == XM_XTF_F32 && omode == OM_F32) return launch_gemv1<true, XM_XTF_F32, OM_F32>(a, st);
+    if (xmode == XM_RAW_F16 && omode == OM_F16) return launch_gemv1<true, XM_RAW_F16, OM_F16>(a, st);
+    if (xmode == XM_PAIR_F16 && omode == OM_F16) return launch_gemv1<true, XM_PAIR_F16, OM_F16>(a, st);
+  } else {
+    if (xmode == XM_XTF_F32 && omode == OM_F32) return launch_gemv1<false, XM_XTF_F32, OM_F32>(a, st);
+    if (xmode == XM_RAW_F16 && omode == OM_F16) return launch_gemv1<false, XM_RAW_F16, OM_F16>(a, st);
+    if (xmode == XM_PAIR_F16 && omode == OM_F16) return launch_gemv1<false, XM_PAIR_F16, OM_F16>(a, st);
+  }
+  return PE_ERR_DTYPE;
+}
+
+static int check_levels(bool nibble, int n_levels) {
+  if (nibble) return (n_levels >= 2 && n_levels <= 16 && (n_levels & (n_levels - 1)) == 0) ? PE_OK : PE_ERR_BITS;
+  return (n_levels >= 2 && n_levels <= 256 && (n_levels & (n_levels - 1)) == 0) ? PE_OK : PE_ERR_BITS;
+}
+
+int polar_gemv_ref(bool nibble, const void* codes, const float* x_tf, const uint16_t* norms,
+                   const float* ct, int n_levels, float* out, int out_f, int kp, int n_blocks,
+                   int block_size, hipStream_t st) {
+  if (!codes || !x_tf || !norms || !ct || !out) return PE_ERR_NULL;
+  if (block_size != kBlock) return PE_ERR_DIMS;
+  if (out_f <= 0 || n_blocks <= 0 || kp != n_blocks * kBlock) return PE_ERR_DIMS;
+  if (int rc = check_levels(nibble, n_levels)) return rc;
+  if (!aligned16(codes) || !aligned16(x_tf)) return PE_ERR_ALIGN;
+  if (kp > gemv1_max_kp(nibble)) return PE_ERR_DIMS;
+  Gemv1Args a{reinterpret_cast<const uint8_t*>(codes), norms, ct, n_levels, x_tf, out, nullptr,
+              out_f, n_blocks};
+  return gemv1(nibble, XM_XTF_F32, OM_F32, a, st);
+}
+
+}  // namespace pe
+
+extern "C" int pe_polar_gemv(const int8_t* codes, const float* x_tf, const uint16_t* norms_f16,
+                             const float* ct_scaled, int n_levels, float* out, int out_f,
+                             int in_f_padded, int n_blocks, int block_size, void* stream) {
+  return pe::polar_gemv_ref(false, codes, x_tf, norms_f16, ct_scaled, n_levels, out, out_f,
+                            in_f_padded, n_blocks, block_size, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int pe_polar_gemv_packed(const uint8_t* packed, const float* x_tf,
+                                    const uint16_t* norms_f16, const float* ct_scaled,
+                                    int n_levels, float* out, int out_f, int in_f_half,
+                                    int n_blocks, int block_size, void* stream) {
+  if (in_f_half != n_blocks * 64) return PE_ERR_DIMS;
+  return pe::polar_gemv_ref(true, packed, x_tf, norms_f16, ct_scaled, n_levels, out, out_f,
+                            n_blocks * pe::kBlock, n_blocks, block_size,
+                            reinterpret_cast<hipStream_t>(stream));
+}

@@ -1,0 +1,55 @@
+// Internal (C++) interfaces shared by the translation units of the library.
+#pragma once
+
+#include "pe_common.h"
+
+namespace pe {
+
+// activation source of the M = 1 GEMV
+enum { XM_RAW_F16 = 0, XM_XTF_F32 = 1, XM_PAIR_F16 = 2 };
+// output element type of GEMV/GEMM epilogues
+enum { OM_F32 = 0, OM_F16 = 1 };
+
+struct Gemv1Args {
+  const uint8_t* codes;
+  const uint16_t* norms;
+  const float* ct;
+  int n_levels;
+  const void* x;
+  void* y;
+  const uint16_t* bias;
+  int N;
+  int nb;
+};
+
+struct GemmArgs {
+  const uint8_t* codes;
+  const uint16_t* norms;
+  const float* ct;
+  int n_levels;
+  const void* xp;  // pair-f16 x_tf [M][nb][64]
+  void* y;
+  const uint16_t* bias;
+  int M, N, nb;
+  int64_t ldy;
+};
+
+// pe_gemv.hip
+int gemv1(bool nibble, int xmode, int omode, const Gemv1Args& a, hipStream_t st);
+int gemv1_max_kp(bool nibble);
+
+// pe_gemm.hip
+int gemm(bool nibble, int omode, const GemmArgs& a, hipStream_t st);
+size_t mm_xtf_workspace(bool nibble, int64_t M, int N, int nb);
+int mm_xtf(bool nibble, const void* codes, const uint16_t* norms, const float* ct, int n_levels,
+           const void* x_pair, int64_t M, int N, int nb, void* y, int out_mode, int64_t ldy,
+           const uint16_t* bias, void* ws, size_t ws_bytes, hipStream_t st);
+
+// pe_fwht.hip
+int fwht128(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t ldx, void* y,
+            int y_layout, hipStream_t st);
+int repack_pair(const float* x, int64_t rows, int64_t cols, void* y, hipStream_t st);
+
+inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace pe

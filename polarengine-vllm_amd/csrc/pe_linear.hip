@@ -1,0 +1,133 @@
+// Dispatch of the quantized linear forward (PolarQuantLinearMethod.apply,
+// polarengine_vllm/linear_method.py:157-222) and of the batched reference API
+// (polar_matmul, kernels/polar_gemm.py:425-534).
+//
+// Routing by M (rows of the activation):
+//   M == 1            -> gemv1: register-resident M=1 decode GEMV, FWHT fused
+//                        into its prologue (one launch per linear);
+//   2 <= M <= kSmallM -> FWHT-128 to pair-f16 x_tf, then the small-M MFMA
+//                        kernel (16x16x32 f16, K split across waves);
+//   M >  kSmallM      -> FWHT-128 to pair-f16 x_tf, then the prefill GEMM
+//                        (32x32x16 f16 MFMA, LDS A tiles, dequantized B).
+// The reference routes M = 1 to split-K GEMV and every M > 1 to its Triton
+// GEMM; results are the same function either way.
+
+#include "pe_internal.h"
+
+namespace pe {
+
+static int check_format(int bits, int packed, int n_levels, bool* nibble) {
+  if (bits < 2 || bits > 8) return PE_ERR_BITS;
+  if (packed && bits > 4) return PE_ERR_BITS;
+  if (n_levels != (1 << bits)) return PE_ERR_BITS;
+  *nibble = packed != 0;
+  return PE_OK;
+}
+
+
+}  // namespace pe
+
+using namespace pe;
+
+extern "C" size_t pe_linear_xtf_workspace_size(int64_t M, int in_f_padded, int out_f, int bits,
+                                               int packed) {
+  if (M <= 1 || in_f_padded <= 0 || out_f <= 0) return 0;
+  return mm_xtf_workspace(packed != 0 && bits <= 4, M, out_f, in_f_padded / kBlock);
+}
+
+extern "C" size_t pe_linear_workspace_size(int64_t M, int in_f, int out_f, int bits, int packed) {
+  if (M <= 1 || in_f <= 0 || out_f <= 0) return 0;
+  const int kp = (in_f + kBlock - 1) / kBlock * kBlock;
+  // pair-f16 x_tf, then whatever the matmul needs
+  return round_up((size_t)M * kp * 2, 256) +
+         pe_linear_xtf_workspace_size(M, kp, out_f, bits, packed);
+}
+
+extern "C" int pe_linear_forward_xtf(const void* x_tf_pair, int64_t M, int in_f_padded,
+                                     const void* codes, int bits, int packed,
+                                     const uint16_t* norms_f16, const float* ct_scaled,
+                                     int n_levels, const void* bias, int out_dtype, void* y,
+                                     int out_f, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (!x_tf_pair || !codes || !norms_f16 || !ct_scaled || !y) return PE_ERR_NULL;
+  if (M < 0 || out_f <= 0 || in_f_padded <= 0 || in_f_padded % kBlock) return PE_ERR_DIMS;
+  if (out_dtype != PE_DTYPE_F16) return PE_ERR_DTYPE;
+  bool nib = false;
+  if (int rc = check_format(bits, packed, n_levels, &nib)) return rc;
+  if (!aligned16(x_tf_pair) || !aligned16(codes)) return PE_ERR_ALIGN;
+  if (M == 0) return PE_OK;
+  const int nb = in_f_padded / kBlock;
+  if (M == 1 && in_f_padded <= gemv1_max_kp(nib)) {
+    Gemv1Args a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels,
+                x_tf_pair, y, reinterpret_cast<const uint16_t*>(bias), out_f, nb};
+    return gemv1(nib, XM_PAIR_F16, OM_F16, a, st);
+  }
+  return mm_xtf(nib, codes, norms_f16, ct_scaled, n_levels, x_tf_pair, M, out_f, nb, y, OM_F16,
+                out_f, reinterpret_cast<const uint16_t*>(bias), workspace, workspace_bytes, st);
+}
+
+extern "C" int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f, int64_t ldx,
+                                 const void* codes, int bits, int packed,
+                                 const uint16_t* norms_f16, const float* ct_scaled, int n_levels,
+                                 const void* bias, void* y, int out_f, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (!x || !codes || !norms_f16 || !ct_scaled || !y) return PE_ERR_NULL;
+  if (M < 0 || in_f <= 0 || out_f <= 0 || ldx < in_f) return PE_ERR_DIMS;
+  if (x_dtype != PE_DTYPE_F16) return PE_ERR_DTYPE;
+  // The kernels read 128-wide blocks of x: in_f must already be a multiple of
+  // 128 (the Python layer pads otherwise, as linear_method.py:194-195 does).
+  if (in_f % kBlock) return PE_ERR_DIMS;
+  bool nib = false;
+  if (int rc = check_format(bits, packed, n_levels, &nib)) return rc;
+  if (!aligned16(x) || !aligned16(codes) || (ldx * 2) % 16) return PE_ERR_ALIGN;
+  if (M == 0) return PE_OK;
+  const int nb = in_f / kBlock;
+  if (M == 1 && in_f <= gemv1_max_kp(nib)) {
+    Gemv1Args a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels, x, y,
+                reinterpret_cast<const uint16_t*>(bias), out_f, nb};
+    return gemv1(nib, XM_RAW_F16, OM_F16, a, st);
+  }
+  const size_t need = pe_linear_workspace_size(M, in_f, out_f, bits, packed);
+  if (!workspace || workspace_bytes < need) return PE_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return PE_ERR_ALIGN;
+  char* ws = reinterpret_cast<char*>(workspace);
+  const size_t xtf_bytes = round_up((size_t)M * in_f * 2, 256);
+  if (int rc = fwht128(x, x_dtype, M, in_f, ldx, ws, PE_XTF_PAIR_F16, st)) return rc;
+  return mm_xtf(nib, codes, norms_f16, ct_scaled, n_levels, ws, M, out_f, nb, y, OM_F16, out_f,
+                reinterpret_cast<const uint16_t*>(bias), ws + xtf_bytes, workspace_bytes - xtf_bytes,
+                st);
+}
+
+extern "C" size_t pe_polar_matmul_workspace_size(int64_t M, int in_f_padded) {
+  if (M <= 1 || in_f_padded <= 0) return 0;
+  // the already-transformed fp32 x_tf repacked to pair f16
+  return round_up((size_t)M * in_f_padded * 2, 256);
+}
+
+extern "C" int pe_polar_matmul(const void* codes, int packed, const float* x_tf, int64_t M,
+                               const uint16_t* norms_f16, const float* ct_scaled, int n_levels,
+                               float* out, int out_f, int in_f_padded, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (!codes || !x_tf || !norms_f16 || !ct_scaled || !out) return PE_ERR_NULL;
+  if (M < 0 || out_f <= 0 || in_f_padded <= 0 || in_f_padded % kBlock) return PE_ERR_DIMS;
+  const bool nib = packed != 0;
+  if (n_levels < 2 || n_levels > (nib ? 16 : 256) || (n_levels & (n_levels - 1))) return PE_ERR_BITS;
+  if (!aligned16(codes) || !aligned16(x_tf)) return PE_ERR_ALIGN;
+  if (M == 0) return PE_OK;
+  const int nb = in_f_padded / kBlock;
+  if (M == 1 && in_f_padded <= gemv1_max_kp(nib)) {
+    Gemv1Args a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels, x_tf,
+                out, nullptr, out_f, nb};
+    return gemv1(nib, XM_XTF_F32, OM_F32, a, st);
+  }
+  const size_t need = round_up((size_t)M * in_f_padded * 2, 256);
+  if (!workspace || workspace_bytes < need) return PE_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return PE_ERR_ALIGN;
+  if (int rc = repack_pair(x_tf, M, in_f_padded, workspace, st)) return rc;
+  char* ws = reinterpret_cast<char*>(workspace);
+  return mm_xtf(nib, codes, norms_f16, ct_scaled, n_levels, ws, M, out_f, nb, out, OM_F32, out_f,
+                nullptr, ws + need, workspace_bytes - need, st);
+}

@@ -1,0 +1,118 @@
+"""ctypes binding of libpolarengine_amd.so (the C ABI in include/polarengine_amd.h).
+
+The library is the only compute path of this package: there is no CPU or
+PyTorch fallback. If the shared object is missing, every kernel entry point
+raises ``RuntimeError`` naming the build command.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get(
+    "POLARENGINE_AMD_LIB",
+    os.path.join(os.path.dirname(_HERE), "lib", "libpolarengine_amd.so"),
+)
+
+PE_OK = 0
+PE_DTYPE_F16, PE_DTYPE_BF16, PE_DTYPE_F32 = 0, 1, 2
+PE_XTF_F32, PE_XTF_F16, PE_XTF_PAIR_F16 = 0, 1, 2
+
+_c_int, _c_i64, _c_sz, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
+
+# name -> (restype, argtypes); mirrors include/polarengine_amd.h
+_SIGNATURES = {
+    "pe_status_string": (ctypes.c_char_p, [_c_int]),
+    "pe_abi_version": (_c_int, []),
+    "pe_fwht128": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_int, _vp]),
+    "pe_polar_gemv": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
+    "pe_polar_gemv_packed": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
+    "pe_polar_matmul_workspace_size": (_c_sz, [_c_i64, _c_int]),
+    "pe_polar_matmul": (_c_int, [_vp, _c_int, _vp, _c_i64, _vp, _vp, _c_int, _vp, _c_int, _c_int,
+                                 _vp, _c_sz, _vp]),
+    "pe_linear_workspace_size": (_c_sz, [_c_i64, _c_int, _c_int, _c_int, _c_int]),
+    "pe_linear_forward": (_c_int, [_vp, _c_int, _c_i64, _c_int, _c_i64, _vp, _c_int, _c_int, _vp,
+                                   _vp, _c_int, _vp, _vp, _c_int, _vp, _c_sz, _vp]),
+    "pe_linear_xtf_workspace_size": (_c_sz, [_c_i64, _c_int, _c_int, _c_int, _c_int]),
+    "pe_linear_forward_xtf": (_c_int, [_vp, _c_i64, _c_int, _vp, _c_int, _c_int, _vp, _vp, _c_int,
+                                       _vp, _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
+    "pe_pack_nibble": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
+    "pe_unpack_q5": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load the shared library once; raise if it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"PolarEngine HIP library not found at {LIB_PATH}; build it with "
+                "`python polarengine-vllm_amd/build_lib.py` (gfx950)")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def exported_symbols():
+    return list(_SIGNATURES)
+
+
+def check(rc: int, what: str) -> None:
+    if rc != PE_OK:
+        msg = lib().pe_status_string(rc).decode()
+        raise RuntimeError(f"{what} failed: status {rc} ({msg})")
+
+
+def stream_ptr(device: torch.device) -> int:
+    """The raw hipStream_t of torch's current stream on ``device``."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_device(*tensors: torch.Tensor) -> torch.device:
+    """All tensors must live on one GPU; there is no CPU path."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "PolarEngine kernels run on the GPU only (got a tensor on "
+                f"{t.device}); there is no CPU fallback")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} vs {t.device}")
+    if dev is None:
+        raise RuntimeError("no tensor given")
+    return dev
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+_WS_CACHE: dict = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Per-device, per-stream growable workspace (uint8), reused across calls."""
+    if nbytes <= 0:
+        return None
+    key = (device, torch.cuda.current_stream(device).cuda_stream)
+    buf = _WS_CACHE.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WS_CACHE[key] = buf
+    return buf

@@ -1,0 +1,160 @@
+"""PolarQuant linear method for vLLM (reference: polarengine_vllm/linear_method.py).
+
+Same buffers and interface as the reference (``create_weights``, ``apply``,
+``process_weights_after_loading``), with the forward running on the gfx950
+HIP library:
+
+* M = 1 (decode): one launch of ``pe_linear_forward`` -- the FWHT-128 of x
+  is fused into the GEMV prologue;
+* M > 1: ``pe_fwht128`` once into the pair-f16 layout (cached for Q/K/V and
+  gate/up reading the same hidden state), then ``pe_linear_forward_xtf``
+  (MFMA GEMM) per projection;
+* bias and the fp16 output cast are fused into the kernel epilogue.
+
+Differences from the reference, on purpose:
+* the FWHT cache is process-wide (the reference's lives per method instance,
+  linear_method.py:85, so separate q/k/v modules never shared it) and keyed
+  safely (see kernels.fwht.FWHTCache);
+* activations must be float16 (the kernels' operand type); the output dtype
+  is float16 as in the reference (linear_method.py:219).
+"""
+
+from __future__ import annotations
+
+import logging
+import math
+from typing import Any, Dict, Optional
+
+import torch
+import torch.nn.functional as F
+
+from polarengine_vllm import _lib
+from polarengine_vllm.kernels.fwht import GLOBAL_FWHT_CACHE, FWHTCache, fwht_pairs
+from polarengine_vllm.utils import get_centroids
+
+try:
+    from vllm.model_executor.utils import set_weight_attrs  # type: ignore
+except Exception:  # vLLM absent: plain attribute setter
+
+    def set_weight_attrs(weight: torch.Tensor, attrs: Dict[str, Any]) -> None:
+        for key, value in attrs.items():
+            setattr(weight, key, value)
+
+logger = logging.getLogger(__name__)
+
+# M above which the transformed activation is materialised and shared
+# (below it the GEMV fuses the transform and sharing saves nothing).
+_SHARE_FWHT_MIN_M = 2
+
+
+class PolarQuantLinearMethod:
+    """vLLM linear method for PolarQuant layers (codes + fp16 norms + ct_scaled)."""
+
+    def __init__(self, block_size: int = 128, bits: int = 4,
+                 layer_meta: Optional[Dict[str, Any]] = None) -> None:
+        if block_size != 128:
+            raise ValueError("the gfx950 kernels implement block_size 128")
+        self.block_size = block_size
+        self.bits = bits
+        self.layer_meta = layer_meta or {}
+        self._fwht_cache = GLOBAL_FWHT_CACHE
+
+    # ------------------------------------------------------------------
+    def create_weights(self, layer: torch.nn.Module, input_size_per_partition: int,
+                       output_partition_sizes: list, input_size: int, output_size: int,
+                       params_dtype: torch.dtype, **extra_weight_attrs: Any) -> None:
+        """Register ``codes`` int8 [out_f, Kp], ``norms`` fp16 [out_f, nb] and
+        ``ct_scaled`` fp32 [2**bits] (reference: linear_method.py:91-151)."""
+        bs = self.block_size
+        in_f = input_size
+        out_f = sum(output_partition_sizes)
+        kp = (in_f + bs - 1) // bs * bs
+        nb = kp // bs
+        layer.register_buffer("codes", torch.zeros(out_f, kp, dtype=torch.int8))
+        layer.register_buffer("norms", torch.zeros(out_f, nb, dtype=torch.float16))
+        layer.register_buffer("ct_scaled", (get_centroids(self.bits) / math.sqrt(bs)).clone())
+        layer.in_f = in_f
+        layer.out_f = out_f
+        layer.in_f_padded = kp
+        layer.n_blocks = nb
+        layer.bits = self.bits
+        layer.block_size = bs
+        layer.packed = False
+        set_weight_attrs(layer.codes, {"input_dim": 1, "output_dim": 0})
+        set_weight_attrs(layer.norms, {"input_dim": 1, "output_dim": 0})
+
+    # ------------------------------------------------------------------
+    def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
+        """Move ct to the codes' device; nibble-pack bits <= 4 on the GPU
+        (``pe_pack_nibble``) and free the int8 codes
+        (reference: linear_method.py:228-258)."""
+        device = layer.codes.device
+        layer.ct_scaled = layer.ct_scaled.to(device=device, dtype=torch.float32).contiguous()
+        if layer.norms.dtype != torch.float16:
+            layer.norms = layer.norms.to(torch.float16)
+        layer.norms = layer.norms.contiguous()
+        if layer.bits <= 4 and not getattr(layer, "packed", False):
+            from polarengine_vllm.packing import pack_codes_half_block
+            layer.codes_packed = pack_codes_half_block(layer.codes.contiguous(), layer.block_size)
+            layer.in_f_half = layer.n_blocks * (layer.block_size // 2)
+            layer.packed = True
+            del layer.codes
+            logger.debug("packed codes to nibbles: out_f=%d in_f_half=%d bits=%d",
+                         layer.out_f, layer.in_f_half, layer.bits)
+
+    # ------------------------------------------------------------------
+    def apply(self, layer: torch.nn.Module, x: torch.Tensor,
+              bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Quantized forward: y = x . W^T (+ bias), fp16 [..., out_f]."""
+        orig_shape = x.shape
+        packed = bool(getattr(layer, "packed", False))
+        codes = layer.codes_packed if packed else layer.codes
+        dev = _lib.require_device(x, codes)
+        if x.dtype != torch.float16:
+            raise TypeError(f"PolarEngine gfx950 kernels take float16 activations, got {x.dtype}")
+        x2 = x.reshape(-1, layer.in_f)
+        m = x2.shape[0]
+        y = torch.empty(m, layer.out_f, dtype=torch.float16, device=dev)
+        if m == 0:
+            return y.view(*orig_shape[:-1], layer.out_f)
+        b = None
+        if bias is not None:
+            b = bias.to(device=dev, dtype=torch.float16).contiguous()
+        L = _lib.lib()
+        st = _lib.stream_ptr(dev)
+        n_levels = layer.ct_scaled.numel()
+        kp = layer.in_f_padded
+
+        if m >= _SHARE_FWHT_MIN_M:
+            x_tf = self._fwht_cache.get(x, layer.in_f)
+            if x_tf is None:
+                xp = x2 if kp == layer.in_f else F.pad(x2, (0, kp - layer.in_f))
+                x_tf = fwht_pairs(xp)
+                self._fwht_cache.put(x, layer.in_f, x_tf)
+            ws_bytes = L.pe_linear_xtf_workspace_size(m, kp, layer.out_f, layer.bits, int(packed))
+            ws = _lib.workspace(dev, ws_bytes)
+            rc = L.pe_linear_forward_xtf(
+                x_tf.data_ptr(), m, kp, codes.data_ptr(), layer.bits, int(packed),
+                layer.norms.data_ptr(), layer.ct_scaled.data_ptr(), n_levels, _lib.ptr(b),
+                _lib.PE_DTYPE_F16, y.data_ptr(), layer.out_f, _lib.ptr(ws), ws_bytes, st)
+            _lib.check(rc, "pe_linear_forward_xtf")
+        else:
+            xc = x2 if kp == layer.in_f else F.pad(x2, (0, kp - layer.in_f))
+            xc = xc.contiguous()
+            ws_bytes = L.pe_linear_workspace_size(m, kp, layer.out_f, layer.bits, int(packed))
+            ws = _lib.workspace(dev, ws_bytes)
+            rc = L.pe_linear_forward(
+                xc.data_ptr(), _lib.PE_DTYPE_F16, m, kp, kp, codes.data_ptr(), layer.bits,
+                int(packed), layer.norms.data_ptr(), layer.ct_scaled.data_ptr(), n_levels,
+                _lib.ptr(b), y.data_ptr(), layer.out_f, _lib.ptr(ws), ws_bytes, st)
+            _lib.check(rc, "pe_linear_forward")
+        return y.view(*orig_shape[:-1], layer.out_f)
+
+
+def create_fwht_clear_hook(linear_method: PolarQuantLinearMethod):
+    """Forward pre-hook clearing the FWHT cache (reference: linear_method.py:265-288)."""
+
+    def hook(module: torch.nn.Module, args):
+        linear_method._fwht_cache.clear()
+
+    return hook

@@ -1,0 +1,308 @@
+"""GPU parity: the HIP library (through its C ABI) against the CPU oracle on
+identical seeded inputs.
+
+Tolerances: fp16 outputs within normwise
+||y - y_ref||_inf / ||y_ref||_inf <= 1e-2 and cosine >= 0.9999 of the fp32
+oracle; code unpacking and indexing bit-exact (one-hot probe, pack kernels).
+"""
+
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import polar_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+NORMWISE_TOL = 1e-2
+COS_TOL = 0.9999
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def check_close(got, want, what):
+    g = np.asarray(got, dtype=np.float64).reshape(-1)
+    w = np.asarray(want, dtype=np.float64).reshape(-1)
+    assert np.isfinite(g).all(), f"{what}: non-finite output"
+    err = np.abs(g - w).max() / max(np.abs(w).max(), 1e-30)
+    cos = float(g @ w / (np.linalg.norm(g) * np.linalg.norm(w) + 1e-300))
+    assert err <= NORMWISE_TOL, f"{what}: normwise err {err:.3e}"
+    assert cos >= COS_TOL, f"{what}: cosine {cos:.7f}"
+    return err, cos
+
+
+def rand_layer(rng, n, kp, bits):
+    codes = rng.integers(0, 1 << bits, (n, kp), dtype=np.int64).astype(np.uint8).view(np.int8)
+    norms = (np.abs(rng.standard_normal((n, kp // 128))) * 0.2 + 0.05).astype(np.float16)
+    return codes, norms, O.ct_scaled(bits)
+
+
+def to_dev(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    return t if dtype is None else t.to(dtype)
+
+
+def dev_codes(codes, bits):
+    """Runtime layout: nibbles for bits <= 4, int8 otherwise."""
+    if bits <= 4:
+        return to_dev(O.pack_nibble(codes)), True
+    return to_dev(codes), False
+
+
+# ---------------------------------------------------------------------------
+# FWHT
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("m,k", [(1, 4096), (4, 12288), (37, 384), (2048, 4096)])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
+def test_fwht_natural_layouts(m, k, dt):
+    from polarengine_vllm.kernels.fwht import fwht_matmul
+    _say(f"fwht m={m} k={k} dt={dt}")
+    x = torch.from_numpy(O.seeded_normal((m, k), 1.0, 11, np.float32)).to(dt)
+    want = O.fwht_blocks(x.float().numpy())
+    got = fwht_matmul(x.to(DEV)).float().cpu().numpy()
+    tol = {torch.float32: 2e-6, torch.float16: 2e-3, torch.bfloat16: 1e-2}[dt]
+    np.testing.assert_allclose(got, want, atol=tol * 4, rtol=tol)
+    if dt == torch.float32:
+        xi = x.to(DEV).clone()
+        fwht_matmul(xi, out=xi)  # in place (the CUDA fwht_)
+        np.testing.assert_allclose(xi.cpu().numpy(), want, atol=1e-5)
+        fp16_out = torch.empty(m, k, dtype=torch.float16, device=DEV)
+        fwht_matmul(x.to(DEV), out=fp16_out)
+        np.testing.assert_allclose(fp16_out.float().cpu().numpy(), want, atol=4e-3, rtol=2e-3)
+
+
+def test_fwht_pair_layout():
+    from polarengine_vllm.kernels.fwht import fwht_pairs
+    _say("fwht pair layout")
+    x = O.seeded_normal((3, 512), 1.0, 12)
+    want = O.fwht_blocks(x.astype(np.float32)).reshape(3, 4, 128)
+    p = fwht_pairs(to_dev(x)).cpu().numpy().view(np.float16).reshape(3, 4, 64, 2)
+    np.testing.assert_allclose(p[..., 0], want[..., :64], atol=4e-3, rtol=2e-3)
+    np.testing.assert_allclose(p[..., 1], want[..., 64:], atol=4e-3, rtol=2e-3)
+
+
+# ---------------------------------------------------------------------------
+# Packing kernels: bit-exact
+# ---------------------------------------------------------------------------
+
+def test_pack_nibble_kernel_bit_exact():
+    from polarengine_vllm.packing import pack_codes_half_block
+    _say("pack_nibble")
+    rng = np.random.default_rng(0)
+    for shape in [(300, 4096), (7, 128), (12288, 384)]:
+        c = rng.integers(0, 16, shape).astype(np.int8)
+        got = pack_codes_half_block(to_dev(c)).cpu().numpy()
+        assert np.array_equal(got, O.pack_nibble(c)), shape
+    for v in (0, 15):
+        c = np.full((64, 1024), v, dtype=np.int8)
+        assert np.array_equal(pack_codes_half_block(to_dev(c)).cpu().numpy(), O.pack_nibble(c))
+
+
+def test_unpack_q5_kernel_bit_exact():
+    from polarengine_vllm.packing import unpack_codes_q5
+    _say("unpack_q5")
+    rng = np.random.default_rng(1)
+    for shape in [(1, 128), (64, 2688), (513, 4096)]:
+        c = rng.integers(0, 32, shape).astype(np.int8)
+        got = unpack_codes_q5(to_dev(O.pack_q5(c))).cpu().numpy()
+        assert np.array_equal(got, c), shape
+
+
+# ---------------------------------------------------------------------------
+# Code indexing probe: one-hot x_tf, unit norms -> y[n] = ct[code[n, k]]
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+def test_indexing_probe_bit_exact(bits):
+    from polarengine_vllm.kernels.polar_gemv import polar_gemv, polar_gemv_packed
+    _say(f"indexing probe bits={bits}")
+    rng = np.random.default_rng(2)
+    n, kp = 96, 1024
+    codes, _, ct = rand_layer(rng, n, kp, bits)
+    norms = np.ones((n, kp // 128), dtype=np.float16)
+    dcodes, nib = dev_codes(codes, bits)
+    # nibble paths carry the codebook as fp16; int8 paths in fp32
+    ct_k = ct.astype(np.float16).astype(np.float32) if nib else ct
+    for k in (0, 1, 15, 16, 17, 63, 64, 65, 100, 127, 128 + 5, 128 * 3 + 64, kp - 1):
+        x = np.zeros(kp, dtype=np.float32)
+        x[k] = 1.0
+        if nib:
+            y = polar_gemv_packed(dcodes, to_dev(x), to_dev(norms), to_dev(ct), n, kp // 2,
+                                  kp // 128)
+        else:
+            y = polar_gemv(dcodes, to_dev(x), to_dev(norms), to_dev(ct), n, kp, kp // 128)
+        want = ct_k[codes[:, k].view(np.uint8).astype(np.int64)]
+        assert np.array_equal(y.cpu().numpy(), want), f"k={k}"
+
+
+# ---------------------------------------------------------------------------
+# Reference-API GEMV (f32 x_tf -> f32 out), shapes of tests/test_kernel_correctness.py
+# ---------------------------------------------------------------------------
+
+SHAPES = [(4096, 4096), (1024, 4096), (12288, 4096), (4096, 12288), (24576, 4096),
+          (2048, 8192), (512, 4096), (1000, 1408)]
+
+
+@pytest.mark.parametrize("n,k", SHAPES)
+@pytest.mark.parametrize("bits", [3, 4, 5, 6])
+def test_polar_gemv_reference_api(n, k, bits):
+    from polarengine_vllm.kernels.polar_gemv import polar_gemv, polar_gemv_packed
+    _say(f"polar_gemv n={n} k={k} bits={bits}")
+    rng = np.random.default_rng(n * 7 + k + bits)
+    codes, norms, ct = rand_layer(rng, n, k, bits)
+    x_tf = O.fwht_blocks(rng.standard_normal(k).astype(np.float32)[None])[0]
+    want = O.hadamard_domain_matmul(codes, norms, ct, x_tf[None])[0]
+    dcodes, nib = dev_codes(codes, bits)
+    fn = polar_gemv_packed if nib else polar_gemv
+    y = fn(dcodes, to_dev(x_tf), to_dev(norms), to_dev(ct), n, k // 2 if nib else k, k // 128)
+    assert y.shape == (n,) and y.dtype == torch.float32
+    check_close(y.cpu().numpy(), want, f"gemv {n}x{k} q{bits}")
+    y2 = fn(dcodes, to_dev(x_tf), to_dev(norms), to_dev(ct), n, k // 2 if nib else k, k // 128)
+    assert torch.equal(y, y2), "non-deterministic"
+
+
+# ---------------------------------------------------------------------------
+# Fused linear forward, M = 1 (FWHT in the GEMV prologue), BASELINE shapes
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n,k,bits", [(4096, 4096, 5), (12288, 4096, 3), (12288, 4096, 4),
+                                      (4096, 12288, 4), (4096, 12288, 3), (1024, 4096, 5),
+                                      (4096, 4096, 6), (2816, 2048, 3), (2048, 1408, 4)])
+def test_linear_forward_m1(n, k, bits):
+    from polarengine_vllm import _lib
+    _say(f"linear m=1 n={n} k={k} bits={bits}")
+    rng = np.random.default_rng(3 + n + bits)
+    kp = (k + 127) // 128 * 128
+    codes, norms, ct = rand_layer(rng, n, kp, bits)
+    x = O.seeded_normal((1, k), 1.0, 5 + bits)
+    bias = O.seeded_normal((n,), 0.1, 6)
+    want = O.linear_apply(x, codes, norms, ct, k, bias)
+    dcodes, nib = dev_codes(codes, bits)
+    xd = to_dev(np.pad(x, ((0, 0), (0, kp - k))))
+    y = torch.empty(1, n, dtype=torch.float16, device=DEV)
+    L = _lib.lib()
+    rc = L.pe_linear_forward(xd.data_ptr(), 0, 1, kp, kp, dcodes.data_ptr(), bits, int(nib),
+                             to_dev(norms).data_ptr(), to_dev(ct).data_ptr(), 1 << bits,
+                             to_dev(bias).data_ptr(), y.data_ptr(), n, None, 0,
+                             _lib.stream_ptr(torch.device(DEV)))
+    _lib.check(rc, "pe_linear_forward")
+    check_close(y.float().cpu().numpy(), want.astype(np.float32), f"linear m=1 {n}x{k} q{bits}")
+
+
+# ---------------------------------------------------------------------------
+# Batched (M > 1): reference API polar_matmul (f32 out) and the MFMA GEMM
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("m,n,k,bits", [(2, 4096, 4096, 4), (4, 12288, 4096, 3),
+                                        (16, 4096, 12288, 4), (33, 1000, 1408, 5),
+                                        (16, 4096, 4096, 6), (256, 12288, 4096, 4),
+                                        (300, 512, 2048, 3), (64, 1024, 4096, 8)])
+def test_polar_matmul_reference_api(m, n, k, bits):
+    from polarengine_vllm.kernels.polar_gemm import polar_matmul
+    _say(f"polar_matmul m={m} n={n} k={k} bits={bits}")
+    rng = np.random.default_rng(m + n + k + bits)
+    codes, norms, ct = rand_layer(rng, n, k, bits)
+    x_tf = O.fwht_blocks(rng.standard_normal((m, k)).astype(np.float32))
+    want = O.hadamard_domain_matmul(codes, norms, ct, x_tf)
+    dcodes, nib = dev_codes(codes, bits)
+    if nib:
+        y = polar_matmul(None, to_dev(x_tf), to_dev(norms), to_dev(ct), n, k, k // 128,
+                         packed=True, packed_codes=dcodes, in_f_half=k // 2)
+    else:
+        y = polar_matmul(dcodes, to_dev(x_tf), to_dev(norms), to_dev(ct), n, k, k // 128)
+    assert y.shape == (m, n) and y.dtype == torch.float32
+    check_close(y.cpu().numpy(), want, f"matmul {m}x{n}x{k} q{bits}")
+
+
+@pytest.mark.parametrize("m,n,k,bits", [(2048, 12288, 4096, 4), (2048, 4096, 12288, 3),
+                                        (8192, 12288, 4096, 4)])
+def test_prefill_gemm_full_size_row_sample(m, n, k, bits):
+    """BASELINE prefill shapes: the oracle checks a seeded sample of rows."""
+    from polarengine_vllm import _lib
+    _say(f"prefill m={m} n={n} k={k} bits={bits}")
+    rng = np.random.default_rng(bits + m)
+    codes, norms, ct = rand_layer(rng, n, k, bits)
+    x = O.seeded_normal((m, k), 1.0, 21)
+    dcodes, nib = dev_codes(codes, bits)
+    y = torch.empty(m, n, dtype=torch.float16, device=DEV)
+    L = _lib.lib()
+    wsb = L.pe_linear_workspace_size(m, k, n, bits, int(nib))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+    rc = L.pe_linear_forward(to_dev(x).data_ptr(), 0, m, k, k, dcodes.data_ptr(), bits, int(nib),
+                             to_dev(norms).data_ptr(), to_dev(ct).data_ptr(), 1 << bits, None,
+                             y.data_ptr(), n, ws.data_ptr(), wsb,
+                             _lib.stream_ptr(torch.device(DEV)))
+    _lib.check(rc, "pe_linear_forward")
+    rows = np.sort(rng.choice(m, 24, replace=False))
+    rows[0], rows[-1] = 0, m - 1
+    want = O.linear_apply(x[rows], codes, norms, ct, k)
+    got = y[torch.from_numpy(rows).to(DEV)].float().cpu().numpy()
+    check_close(got, want.astype(np.float32), f"prefill {m}x{n}x{k}")
+    assert torch.isfinite(y).all()
+
+
+# ---------------------------------------------------------------------------
+# Plugin path: PolarQuantLinearMethod with quantizer output
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("m", [1, 3, 64])
+@pytest.mark.parametrize("bits,n,k", [(5, 1024, 4096), (3, 2048, 1000), (4, 768, 2048),
+                                      (6, 512, 512)])
+def test_linear_method_apply(m, bits, n, k):
+    from polarengine_vllm.linear_method import PolarQuantLinearMethod
+    from polarengine_vllm.quantizer import PolarQuantizer
+    _say(f"linear_method m={m} bits={bits} n={n} k={k}")
+    w = torch.from_numpy(O.seeded_normal((n, k), 0.02, 31 + bits))
+    q = PolarQuantizer(128).quantize_tensor(w.to(DEV), bits)
+    layer = torch.nn.Module()
+    meth = PolarQuantLinearMethod(128, bits)
+    meth.create_weights(layer, k, [n], k, n, torch.float16)
+    layer.to(DEV)
+    layer.codes.copy_(q["codes"])
+    layer.norms.copy_(q["norms"])
+    meth.process_weights_after_loading(layer)
+    assert layer.packed == (bits <= 4)
+    x = O.seeded_normal((m, k), 1.0, 41)
+    bias = O.seeded_normal((n,), 0.05, 42)
+    y = meth.apply(layer, to_dev(x), to_dev(bias))
+    assert y.shape == (m, n) and y.dtype == torch.float16
+    want = O.linear_apply(x, q["codes"].cpu().numpy(), q["norms"].cpu().numpy(),
+                          q["ct_scaled"].cpu().numpy(), k, bias)
+    check_close(y.float().cpu().numpy(), want.astype(np.float32), "linear_method")
+    meth._fwht_cache.clear()
+
+
+def test_fwht_shared_across_qkv():
+    """q/k/v modules on one hidden state: one transform, three projections."""
+    from polarengine_vllm.kernels.fwht import GLOBAL_FWHT_CACHE
+    from polarengine_vllm.linear_method import PolarQuantLinearMethod
+    _say("qkv sharing")
+    rng = np.random.default_rng(9)
+    k = 1024
+    x = to_dev(O.seeded_normal((8, k), 1.0, 43))
+    GLOBAL_FWHT_CACHE.clear()
+    outs = []
+    for n in (1024, 256, 256):
+        codes, norms, ct = rand_layer(rng, n, k, 5)
+        layer = torch.nn.Module()
+        meth = PolarQuantLinearMethod(128, 5)
+        meth.create_weights(layer, k, [n], k, n, torch.float16)
+        layer.to(DEV)
+        layer.codes.copy_(to_dev(codes))
+        layer.norms.copy_(to_dev(norms))
+        meth.process_weights_after_loading(layer)
+        y = meth.apply(layer, x)
+        outs.append((y, codes, norms, ct))
+        assert GLOBAL_FWHT_CACHE.get(x, k) is not None
+    for y, codes, norms, ct in outs:
+        want = O.linear_apply(x.cpu().numpy(), codes, norms, ct, k)
+        check_close(y.float().cpu().numpy(), want.astype(np.float32), "qkv")
+    GLOBAL_FWHT_CACHE.clear()
