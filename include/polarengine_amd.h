@@ -53,7 +53,8 @@ enum { PE_DTYPE_F16 = 0, PE_DTYPE_BF16 = 1, PE_DTYPE_F32 = 2 };
 enum {
   PE_XTF_F32 = 0,      /* natural layout, float32 [rows, cols]              */
   PE_XTF_F16 = 1,      /* natural layout, float16 [rows, cols]              */
-  PE_XTF_PAIR_F16 = 2  /* pair layout, see header comment                   */
+  PE_XTF_PAIR_F16 = 2, /* pair layout, see header comment                  */
+  PE_XTF_BF16 = 3      /* natural layout, bfloat16 [rows, cols]             */
 };
 
 /* Human-readable text for a status code (static storage). */

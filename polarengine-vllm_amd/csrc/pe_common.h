@@ -35,6 +35,9 @@ constexpr float kInvSqrt128 = 0.08838834764831845f;  // fp32(2^-3.5)
 // ---------------------------------------------------------------------------
 
 // 16-byte streaming load (non-temporal: weights are read once per call)
+__device__ __forceinline__ u32x4v ld_nt16v(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(p));
+}
 __device__ __forceinline__ uint4 ld_nt16(const void* p) {
   const u32x4v v = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(p));
   return make_uint4(v[0], v[1], v[2], v[3]);
@@ -48,6 +51,9 @@ __device__ __forceinline__ float h2f(uint16_t bits) {
 }
 __device__ __forceinline__ uint16_t f2h_bits(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
+  return (uint32_t)f2h_bits(lo) | ((uint32_t)f2h_bits(hi) << 16);
 }
 // bfloat16 <-> float, round-to-nearest-even on the way down (NaN kept quiet).
 __device__ __forceinline__ float bf2f(uint16_t bits) {
@@ -109,6 +115,44 @@ __device__ __forceinline__ void fwht128_group16(float v[8], int q) {
   for (int i = 0; i < 8; ++i) v[i] *= kInvSqrt128;
 }
 
+// ---------------------------------------------------------------------------
+// Per-lane replicated codebook table in LDS: dword e*64 + lane holds entry e.
+// The codebook is read from global memory once per lane (lane j keeps
+// ct[j + 64 i]) and broadcast with v_readlane, so filling the table issues
+// no dependent global loads.
+//   TBL_NIB_H2: entry e = half2(ct[e & 15], ct[e >> 4]) (nibble byte e)
+//   TBL_F16   : entry e = fp16 bits of ct[e] in the low half
+//   TBL_F32   : entry e = ct[e]
+// ---------------------------------------------------------------------------
+enum { TBL_NIB_H2 = 0, TBL_F16 = 1, TBL_F32 = 2 };
+
+__device__ __forceinline__ float bcast_lane(float v, int src_lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src_lane));
+}
+
+template <int KIND>
+__device__ __forceinline__ void fill_codebook(uint32_t* tbl, const float* __restrict__ ct,
+                                              int n_levels, int entries, int nwaves) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  float c[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c[i] = (lane + 64 * i) < n_levels ? ct[lane + 64 * i] : 0.f;
+  for (int e = wave; e < entries; e += nwaves) {
+    uint32_t v;
+    if constexpr (KIND == TBL_NIB_H2) {
+      const int lo = e & 15, hi = e >> 4;  // n_levels <= 16: both in c[0]
+      v = pack_h2(bcast_lane(c[0], lo), bcast_lane(c[0], hi));
+    } else {
+      const int q = e >> 6, r = e & 63;
+      const float src = q == 0 ? c[0] : q == 1 ? c[1] : q == 2 ? c[2] : c[3];
+      const float val = bcast_lane(src, r);
+      v = KIND == TBL_F16 ? (uint32_t)f2h_bits(val) : __builtin_bit_cast(uint32_t, val);
+    }
+    tbl[e * 64 + lane] = v;
+  }
+}
+
 // Load 8 consecutive activations as float from a dtype-tagged pointer.
 template <int DT>
 __device__ __forceinline__ void load8(const void* p, float v[8]) {
@@ -133,9 +177,6 @@ __device__ __forceinline__ void load8(const void* p, float v[8]) {
   }
 }
 
-__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
-  return (uint32_t)f2h_bits(lo) | ((uint32_t)f2h_bits(hi) << 16);
-}
 
 }  // namespace pe
 

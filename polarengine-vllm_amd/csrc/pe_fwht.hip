@@ -55,8 +55,15 @@ __global__ __launch_bounds__(256) void fwht128_kernel(const void* x, void* y, in
     if (!live) return;
     uint16_t* dst = reinterpret_cast<uint16_t*>(y) + (r * (int64_t)nbc * kBlock + (int64_t)cb * kBlock + q * 8);
     uint4 w;
-    w.x = pack_h2(v[0], v[1]); w.y = pack_h2(v[2], v[3]);
-    w.z = pack_h2(v[4], v[5]); w.w = pack_h2(v[6], v[7]);
+    if constexpr (YL == PE_XTF_BF16) {
+      w.x = f2bf_bits(v[0]) | ((uint32_t)f2bf_bits(v[1]) << 16);
+      w.y = f2bf_bits(v[2]) | ((uint32_t)f2bf_bits(v[3]) << 16);
+      w.z = f2bf_bits(v[4]) | ((uint32_t)f2bf_bits(v[5]) << 16);
+      w.w = f2bf_bits(v[6]) | ((uint32_t)f2bf_bits(v[7]) << 16);
+    } else {
+      w.x = pack_h2(v[0], v[1]); w.y = pack_h2(v[2], v[3]);
+      w.z = pack_h2(v[4], v[5]); w.w = pack_h2(v[6], v[7]);
+    }
     *reinterpret_cast<uint4*>(dst) = w;
   }
 }
@@ -70,6 +77,7 @@ static int launch_fwht(const void* x, int64_t rows, int nbc, int64_t ldx, void* 
     case PE_XTF_F32: fwht128_kernel<XDT, PE_XTF_F32><<<grid, block, 0, st>>>(x, y, rows, nbc, ldx); break;
     case PE_XTF_F16: fwht128_kernel<XDT, PE_XTF_F16><<<grid, block, 0, st>>>(x, y, rows, nbc, ldx); break;
     case PE_XTF_PAIR_F16: fwht128_kernel<XDT, PE_XTF_PAIR_F16><<<grid, block, 0, st>>>(x, y, rows, nbc, ldx); break;
+    case PE_XTF_BF16: fwht128_kernel<XDT, PE_XTF_BF16><<<grid, block, 0, st>>>(x, y, rows, nbc, ldx); break;
     default: return PE_ERR_DTYPE;
   }
   return launch_status();

@@ -40,24 +40,6 @@ __device__ __forceinline__ void store_out(void* y, int64_t ldy, int m, int n, fl
   }
 }
 
-// Fill the per-lane codebook table. Nibble: half2(ct[lo], ct[hi]) per byte
-// value; int8: fp16 bits of ct[e] in the low half of the slot.
-template <bool NIB>
-__device__ __forceinline__ void fill_table_f16(uint32_t* tbl, const float* ct, int n_levels,
-                                               int entries, int tid, int nthreads) {
-  const int lane = tid & 63;
-  for (int e = tid >> 6; e < entries; e += nthreads >> 6) {
-    uint32_t val;
-    if constexpr (NIB) {
-      const int lo = e & 15, hi = e >> 4;
-      val = pack_h2(lo < n_levels ? ct[lo] : 0.f, hi < n_levels ? ct[hi] : 0.f);
-    } else {
-      val = (uint32_t)f2h_bits(ct[e]);
-    }
-    tbl[e * 64 + lane] = val;
-  }
-}
-
 // Dequantize one slab worth of B for one MFMA n-tile: 4 pair dwords.
 template <bool NIB>
 __device__ __forceinline__ half8v dequant_slab(const char* tbl, uint32_t wlo, uint32_t whi,
@@ -93,6 +75,75 @@ __device__ __forceinline__ half8v dequant_slab(const char* tbl, uint32_t wlo, ui
   return r;
 }
 
+// B operand registers of one half-block K-tile for the wave's TNW n-tiles
+template <bool NIB, int TNW>
+struct BTile {
+  u32x4v lo[TNW];
+  u32x4v hi[TNW];  // int8 codes only: bytes at +64 (the pair's second position)
+  uint16_t nrm[TNW];
+};
+
+template <bool NIB, int TNW>
+__device__ __forceinline__ void load_btile(BTile<NIB, TNW>& t, const uint8_t* const (&b_row)[TNW],
+                                           const uint16_t* const (&n_row)[TNW], int kt) {
+  const int b = kt >> 1, half = kt & 1;
+#pragma unroll
+  for (int j = 0; j < TNW; ++j) {
+    if constexpr (NIB) {
+      t.lo[j] = ld_nt16v(b_row[j] + b * 64 + half * 32);
+    } else {
+      t.lo[j] = ld_nt16v(b_row[j] + b * kBlock + half * 32);
+      t.hi[j] = ld_nt16v(b_row[j] + b * kBlock + 64 + half * 32);
+    }
+    t.nrm[j] = n_row[j][b];
+  }
+}
+
+template <int KA>
+__device__ __forceinline__ void load_atile(u32x4v (&r)[KA], const uint32_t* const (&a_src)[KA],
+                                           int kt) {
+  const int off = (kt >> 1) * 64 + (kt & 1) * 32;
+#pragma unroll
+  for (int i = 0; i < KA; ++i) r[i] = *reinterpret_cast<const u32x4v*>(a_src[i] + off);
+}
+
+template <int KA>
+__device__ __forceinline__ void store_atile(char* dst, const u32x4v (&r)[KA],
+                                            const int (&a_dst)[KA]) {
+#pragma unroll
+  for (int i = 0; i < KA; ++i) *reinterpret_cast<u32x4v*>(dst + a_dst[i]) = r[i];
+}
+
+// One half-block K-tile of MFMA work on LDS A buffer `abase`.
+template <bool NIB, int TMW, int TNW>
+__device__ __forceinline__ void mma_ktile(float16v (&acc)[TMW][TNW], const BTile<NIB, TNW>& bt,
+                                          const char* abase, const char* tbl, uint32_t lane4,
+                                          uint32_t code_mask) {
+  half2v nrm2[TNW];
+#pragma unroll
+  for (int j = 0; j < TNW; ++j) {
+    const _Float16 nh = __builtin_bit_cast(_Float16, bt.nrm[j]);
+    nrm2[j] = half2v{nh, nh};
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    half8v af[TMW];
+#pragma unroll
+    for (int i = 0; i < TMW; ++i)
+      af[i] = __builtin_bit_cast(half8v, *reinterpret_cast<const u32x4v*>(abase + i * 32 * kAStride + 16 * t));
+#pragma unroll
+    for (int j = 0; j < TNW; ++j) {
+      const uint32_t wl = bt.lo[j][t] & code_mask;
+      uint32_t wh = 0;
+      if constexpr (!NIB) wh = bt.hi[j][t] & code_mask;
+      const half8v bf = dequant_slab<NIB>(tbl, wl, wh, lane4, nrm2[j]);
+#pragma unroll
+      for (int i = 0; i < TMW; ++i)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf, acc[i][j], 0, 0, 0);
+    }
+  }
+}
+
 template <bool NIB, int TMW, int TNW, int OM>
 __global__ __launch_bounds__(256) void gemm_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
@@ -101,7 +152,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     int M, int N, int nb, int64_t ldy, int tiles_m, int tiles_total) {
   constexpr int BM = 2 * TMW * 32;
   constexpr int BN = 2 * TNW * 32;
-  constexpr int kAPerThread = BM * 8 / 256;  // uint4 of A per thread per half-block
+  constexpr int KA = BM * 8 / 256;  // uint4 of A per thread per half-block
   extern __shared__ uint4 smem4[];
   char* smem = reinterpret_cast<char*>(smem4);
   char* tbl = smem;
@@ -113,22 +164,24 @@ __global__ __launch_bounds__(256) void gemm_kernel(
   const int wm = wave >> 1, wn = wave & 1;
   const int h = lane >> 5, l32 = lane & 31;
   const uint32_t lane4 = (uint32_t)lane << 2;
+  (void)BN;
 
   // XCD-aware tile order: ids are dealt round-robin to 8 XCDs; give each XCD a
   // contiguous range of logical tiles.
   int wid = blockIdx.x;
   if ((tiles_total & 7) == 0) wid = (wid & 7) * (tiles_total >> 3) + (wid >> 3);
   const int tm = wid % tiles_m, tn = wid / tiles_m;
-  const int m0 = tm * BM, n0 = tn * BN;
+  const int m0 = tm * BM, n0 = tn * (2 * TNW * 32);
 
-  fill_table_f16<NIB>(reinterpret_cast<uint32_t*>(tbl), ct, n_levels, tbl_entries, tid, 256);
+  if constexpr (NIB) fill_codebook<TBL_NIB_H2>(reinterpret_cast<uint32_t*>(tbl), ct, n_levels, tbl_entries, 4);
+  else fill_codebook<TBL_F16>(reinterpret_cast<uint32_t*>(tbl), ct, n_levels, tbl_entries, 4);
 
-  // ---- A loader: thread t moves uint4 q = t + 256 i (row q >> 3, 16-byte col q & 7)
-  const int64_t xrow_u32 = (int64_t)nb * 64;  // uint32 per x_tf row
-  const uint32_t* a_src[kAPerThread];
-  int a_dst[kAPerThread];
+  // A loader: thread t moves uint4 q = t + 256 i (row q >> 3, 16-byte col q & 7)
+  const int64_t xrow_u32 = (int64_t)nb * 64;
+  const uint32_t* a_src[KA];
+  int a_dst[KA];
 #pragma unroll
-  for (int i = 0; i < kAPerThread; ++i) {
+  for (int i = 0; i < KA; ++i) {
     const int q = tid + 256 * i;
     const int r = q >> 3, c = q & 7;
     int m = m0 + r;
@@ -136,8 +189,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     a_src[i] = xp + (int64_t)m * xrow_u32 + c * 4;
     a_dst[i] = r * kAStride + c * 16;
   }
-
-  // ---- B rows of this wave
+  // B rows of this wave
   const int row_bytes = NIB ? nb * 64 : nb * kBlock;
   const uint8_t* b_row[TNW];
   const uint16_t* n_row[TNW];
@@ -149,37 +201,6 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     n_row[j] = norms + (int64_t)n * nb;
   }
 
-  const int nkt = 2 * nb;  // half-block K-tiles
-  uint4 a_reg[kAPerThread];
-  uint4 c_lo[TNW], c_hi[TNW];
-  uint16_t nrm_bits[TNW];
-
-  auto load_a = [&](int kt) {
-    const int b = kt >> 1, half = kt & 1;
-    const int off = b * 64 + half * 32;
-#pragma unroll
-    for (int i = 0; i < kAPerThread; ++i)
-      a_reg[i] = *reinterpret_cast<const uint4*>(a_src[i] + off);
-  };
-  auto store_a = [&](int buf) {
-    char* dst = abuf + buf * (BM * kAStride);
-#pragma unroll
-    for (int i = 0; i < kAPerThread; ++i) *reinterpret_cast<uint4*>(dst + a_dst[i]) = a_reg[i];
-  };
-  auto load_b = [&](int kt) {
-    const int b = kt >> 1, half = kt & 1;
-#pragma unroll
-    for (int j = 0; j < TNW; ++j) {
-      if constexpr (NIB) {
-        c_lo[j] = ld_nt16((b_row[j] + b * 64 + half * 32));
-      } else {
-        c_lo[j] = ld_nt16((b_row[j] + b * kBlock + half * 32));
-        c_hi[j] = ld_nt16((b_row[j] + b * kBlock + 64 + half * 32));
-      }
-      nrm_bits[j] = n_row[j][b];
-    }
-  };
-
   float16v acc[TMW][TNW];
 #pragma unroll
   for (int i = 0; i < TMW; ++i)
@@ -188,47 +209,40 @@ __global__ __launch_bounds__(256) void gemm_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  load_a(0);
-  load_b(0);
-  store_a(0);
+  const int nkt = 2 * nb;  // half-block K-tiles (always even)
+  const int a_off = (wm * TMW * 32 + l32) * kAStride + 64 * h;
+  u32x4v ar[KA];
+  BTile<NIB, TNW> b0, b1;
+
+  // prologue: A(0) -> LDS 0, A(1) -> regs, B(0), B(1) -> regs
+  load_atile<KA>(ar, a_src, 0);
+  load_btile<NIB, TNW>(b0, b_row, n_row, 0);
+  load_btile<NIB, TNW>(b1, b_row, n_row, 1);
+  store_atile<KA>(abuf, ar, a_dst);
+  load_atile<KA>(ar, a_src, 1);
   __syncthreads();
 
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int cur = kt & 1;
-    // current B operands out of the prefetch registers
-    uint4 cl[TNW], ch[TNW];
-    half2v nrm2[TNW];
-#pragma unroll
-    for (int j = 0; j < TNW; ++j) {
-      cl[j] = c_lo[j];
-      if constexpr (!NIB) ch[j] = c_hi[j];
-      const _Float16 nh = __builtin_bit_cast(_Float16, nrm_bits[j]);
-      nrm2[j] = half2v{nh, nh};
+  for (int kt = 0; kt < nkt; kt += 2) {
+    // ---- even half-block: B from b0, A from LDS buffer 0
+    {
+      const BTile<NIB, TNW> cur = b0;
+      if (kt + 2 < nkt) load_btile<NIB, TNW>(b0, b_row, n_row, kt + 2);
+      mma_ktile<NIB, TMW, TNW>(acc, cur, abuf + a_off, tbl, lane4, code_mask);
+      store_atile<KA>(abuf + BM * kAStride, ar, a_dst);  // A(kt+1) -> LDS 1
+      if (kt + 2 < nkt) load_atile<KA>(ar, a_src, kt + 2);
+      __syncthreads();
     }
-    if (kt + 1 < nkt) {
-      load_a(kt + 1);
-      load_b(kt + 1);
-    }
-    const char* abase = abuf + cur * (BM * kAStride) + (wm * TMW * 32 + l32) * kAStride + 64 * h;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      half8v af[TMW];
-#pragma unroll
-      for (int i = 0; i < TMW; ++i)
-        af[i] = __builtin_bit_cast(half8v, *reinterpret_cast<const uint4*>(abase + i * 32 * kAStride + 16 * t));
-#pragma unroll
-      for (int j = 0; j < TNW; ++j) {
-        const uint32_t wl = (t == 0 ? cl[j].x : t == 1 ? cl[j].y : t == 2 ? cl[j].z : cl[j].w) & code_mask;
-        uint32_t wh = 0;
-        if constexpr (!NIB) wh = (t == 0 ? ch[j].x : t == 1 ? ch[j].y : t == 2 ? ch[j].z : ch[j].w) & code_mask;
-        const half8v bf = dequant_slab<NIB>(tbl, wl, wh, lane4, nrm2[j]);
-#pragma unroll
-        for (int i = 0; i < TMW; ++i)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf, acc[i][j], 0, 0, 0);
+    // ---- odd half-block: B from b1, A from LDS buffer 1
+    {
+      const BTile<NIB, TNW> cur = b1;
+      if (kt + 3 < nkt) load_btile<NIB, TNW>(b1, b_row, n_row, kt + 3);
+      mma_ktile<NIB, TMW, TNW>(acc, cur, abuf + BM * kAStride + a_off, tbl, lane4, code_mask);
+      if (kt + 2 < nkt) {
+        store_atile<KA>(abuf, ar, a_dst);  // A(kt+2) -> LDS 0
+        load_atile<KA>(ar, a_src, kt + 3);
       }
+      __syncthreads();
     }
-    if (kt + 1 < nkt) store_a(cur ^ 1);
-    __syncthreads();
   }
 
   // ---- epilogue: acc[i][j][e] -> row 8*(e/4) + 4*h + e%4, col l32
@@ -295,6 +309,12 @@ int mm_xtf(bool nibble, const void* codes, const uint16_t* norms, const float* c
            const uint16_t* bias, void* ws, size_t ws_bytes, hipStream_t st) {
   (void)ws; (void)ws_bytes;
   if (M > INT32_MAX) return PE_ERR_DIMS;
+  if (M <= kSmallMaxRows) {
+    SmallArgs s{reinterpret_cast<const uint8_t*>(codes), norms, ct, n_levels,
+                reinterpret_cast<const uint32_t*>(x_pair), nullptr, nullptr, 0, 0, y, ldy, bias,
+                (int)M, N, nb};
+    return gemm_small(nibble, out_mode == OM_F32 ? SE_F32 : SE_F16, s, 1, st);
+  }
   GemmArgs a{reinterpret_cast<const uint8_t*>(codes), norms, ct, n_levels, x_pair, y, bias,
              (int)M, N, nb, ldy};
   return gemm(nibble, out_mode, a, st);

@@ -1,0 +1,281 @@
+// Small-M quantized matmul for gfx950 (decode batches M = 2..64, and the
+// grouped-expert MoE products): Y[m, n] = sum_k X_tf[m, k] * W~[n, k].
+//
+// Replaces the reference's M > 1 path for small batches (polar_gemm /
+// polar_gemm_packed, kernels/polar_gemm.py:81-418, autotuned Triton tiles) and
+// provides the quantized expert products the reference never had
+// (moe_method.py forwards experts to vLLM's bf16 fused MoE).
+//
+// Structure:
+//  * v_mfma_f32_16x16x32_f16 with the activations as the A operand (16 rows
+//    per m-tile, rows >= M zero) and the dequantized weights as B
+//    (16 weight rows per n-tile);
+//  * a 512-lane workgroup owns TN n-tiles and all M (up to 4 m-tiles); its 8
+//    waves split the K blocks, each reading a contiguous K range, and combine
+//    through LDS at the end -- no global workspace, deterministic order;
+//  * lane (n = l % 16, g = l / 16) reads 16 contiguous code bytes per row per
+//    128-block (one dwordx4 for nibbles); slab t of the block takes dword t,
+//    i.e. pairs 16g + 4t + j, and A takes the same pairs from the pair-f16
+//    x_tf (16 contiguous bytes per lane per slab);
+//  * the per-block fp16 norm multiplies the 4 fp32 MFMA results of each block
+//    (fp32, as the reference applies it), not the fp16 operands;
+//  * grouped mode (MoE): blockIdx.y selects an expert, whose rows are
+//    [off[e], off[e+1]) of a row list; weights advance by per-expert strides;
+//  * epilogues: fp32 out, fp16 out (+ bias), or SwiGLU: the workgroup also
+//    computes the "up" tile at row n + I for every "gate" tile at row n and
+//    writes fp16 silu(gate) * up.
+
+#include "pe_internal.h"
+
+namespace pe {
+
+constexpr int kSmallThreads = 512;
+constexpr int kSmallWaves = kSmallThreads / 64;
+constexpr int kSmallMaxMT = 4;  // m-tiles of 16 per launch (M <= 64)
+
+template <bool NIB>
+__device__ __forceinline__ half8v dequant_slab_raw(const char* tbl, uint32_t wlo, uint32_t whi,
+                                                   uint32_t lane4) {
+  uint32_t p[4];
+  if constexpr (NIB) {
+    p[0] = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<0>(wlo, lane4));
+    p[1] = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<1>(wlo, lane4));
+    p[2] = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<2>(wlo, lane4));
+    p[3] = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<3>(wlo, lane4));
+  } else {
+    const uint32_t a0 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<0>(wlo, lane4));
+    const uint32_t a1 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<1>(wlo, lane4));
+    const uint32_t a2 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<2>(wlo, lane4));
+    const uint32_t a3 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<3>(wlo, lane4));
+    const uint32_t b0 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<0>(whi, lane4));
+    const uint32_t b1 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<1>(whi, lane4));
+    const uint32_t b2 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<2>(whi, lane4));
+    const uint32_t b3 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<3>(whi, lane4));
+    p[0] = __builtin_amdgcn_perm(b0, a0, 0x05040100u);
+    p[1] = __builtin_amdgcn_perm(b1, a1, 0x05040100u);
+    p[2] = __builtin_amdgcn_perm(b2, a2, 0x05040100u);
+    p[3] = __builtin_amdgcn_perm(b3, a3, 0x05040100u);
+  }
+  u32x4v v = {p[0], p[1], p[2], p[3]};
+  return __builtin_bit_cast(half8v, v);
+}
+
+// TN: n-tiles of 16 weight rows per workgroup (SwiGLU doubles them: gate+up)
+template <bool NIB, int TN, int EP>
+__global__ __launch_bounds__(kSmallThreads) void gemm_small_kernel(
+    SmallArgs a, uint32_t code_mask, int tbl_entries) {
+  constexpr int NT = EP == SE_SWIGLU ? 2 * TN : TN;  // tiles actually computed
+  extern __shared__ uint4 smem4[];
+  char* smem = reinterpret_cast<char*>(smem4);
+  char* tbl = smem;
+  float* red = reinterpret_cast<float*>(smem);  // after the K loop: [waves][4][NT][64][4]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const uint32_t lane4 = (uint32_t)lane << 2;
+
+  // ---- group / rows
+  int row0 = 0, M = a.M;
+  const uint8_t* codes = a.codes;
+  const uint16_t* norms = a.norms;
+  if (a.group_off) {
+    row0 = a.group_off[blockIdx.y];
+    M = a.group_off[blockIdx.y + 1] - row0;
+    codes += (int64_t)blockIdx.y * a.codes_stride;
+    norms += (int64_t)blockIdx.y * a.norms_stride;
+  }
+  if (M <= 0) return;  // whole workgroup exits together (uniform)
+
+  // ---- this lane's weight rows (clamped; clamped rows are never stored)
+  const int row_bytes = NIB ? a.nb * 64 : a.nb * kBlock;
+  const int wrows = EP == SE_SWIGLU ? 2 * a.N : a.N;
+  const uint8_t* brow[NT];
+  const uint16_t* nrow[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    int n = blockIdx.x * TN * 16 + (j % TN) * 16 + l16;
+    if (n >= a.N) n = a.N - 1;
+    if (EP == SE_SWIGLU && j >= TN) n += a.N;  // the matching "up" row
+    if (n >= wrows) n = wrows - 1;
+    brow[j] = codes + (int64_t)n * row_bytes + 16 * g;
+    nrow[j] = norms + (int64_t)n * a.nb;
+  }
+  const int64_t xrow = (int64_t)a.nb * 64;
+  // K range of this wave
+  const int b_begin = (int)((int64_t)a.nb * wave / kSmallWaves);
+  const int b_end = (int)((int64_t)a.nb * (wave + 1) / kSmallWaves);
+
+  // rows are processed 64 at a time (MT <= 4 m-tiles of 16)
+  for (int mbase = 0; mbase < M; mbase += 16 * kSmallMaxMT) {
+    const int mrem = M - mbase;
+    const int MT = mrem >= 16 * kSmallMaxMT ? kSmallMaxMT : (mrem + 15) >> 4;
+
+    // codebook table (LDS is shared with the reduction of the previous chunk)
+    if constexpr (NIB)
+      fill_codebook<TBL_NIB_H2>(reinterpret_cast<uint32_t*>(tbl), a.ct, a.n_levels, tbl_entries, kSmallWaves);
+    else
+      fill_codebook<TBL_F16>(reinterpret_cast<uint32_t*>(tbl), a.ct, a.n_levels, tbl_entries, kSmallWaves);
+    __syncthreads();
+
+    const uint32_t* arow[kSmallMaxMT];
+    bool alive[kSmallMaxMT];
+#pragma unroll
+    for (int i = 0; i < kSmallMaxMT; ++i) {
+      const int m = mbase + i * 16 + l16;
+      alive[i] = i < MT && m < M;
+      int r = row0 + (alive[i] ? m : 0);
+      if (a.a_rows) r = a.a_rows[r];
+      arow[i] = a.xp + (int64_t)r * xrow + 16 * g;
+    }
+
+    float4v acc[kSmallMaxMT][NT];
+#pragma unroll
+    for (int i = 0; i < kSmallMaxMT; ++i)
+#pragma unroll
+      for (int j = 0; j < NT; ++j) acc[i][j] = float4v{0.f, 0.f, 0.f, 0.f};
+
+    for (int b = b_begin; b < b_end; ++b) {
+      u32x4v clo[NT], chi[NT];
+      uint16_t nbits[NT];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        if constexpr (NIB) {
+          clo[j] = ld_nt16v(brow[j] + b * 64);
+        } else {
+          clo[j] = ld_nt16v(brow[j] + b * kBlock);
+          chi[j] = ld_nt16v(brow[j] + b * kBlock + 64);
+        }
+        nbits[j] = nrow[j][b];
+      }
+      u32x4v af[kSmallMaxMT][4];
+#pragma unroll
+      for (int i = 0; i < kSmallMaxMT; ++i) {
+        if (alive[i]) {
+          const u32x4v* p = reinterpret_cast<const u32x4v*>(arow[i] + b * 64);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) af[i][t] = p[t];
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) af[i][t] = u32x4v{0u, 0u, 0u, 0u};
+        }
+      }
+      // all loads of this block issue before any use
+      __builtin_amdgcn_sched_barrier(0);
+      float nrm[NT];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) nrm[j] = h2f(nbits[j]);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        float4v blk[kSmallMaxMT];
+#pragma unroll
+        for (int i = 0; i < kSmallMaxMT; ++i) blk[i] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const uint32_t wl = clo[j][t] & code_mask;
+          const uint32_t wh = NIB ? 0u : (chi[j][t] & code_mask);
+          const half8v bf = dequant_slab_raw<NIB>(tbl, wl, wh, lane4);
+#pragma unroll
+          for (int i = 0; i < kSmallMaxMT; ++i) {
+            if (i < MT) {
+              blk[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, af[i][t]), bf,
+                                                              blk[i], 0, 0, 0);
+            }
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < kSmallMaxMT; ++i) acc[i][j] += blk[i] * nrm[j];
+      }
+    }
+
+    // ---- combine the 8 K-slices through LDS (over the table, now unused):
+    // red[wave][i][j][lane][4]
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kSmallMaxMT; ++i) {
+      if (i >= MT) continue;
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        float4* dst = reinterpret_cast<float4*>(
+            red + ((((int64_t)wave * kSmallMaxMT + i) * NT + j) * 64 + lane) * 4);
+        *dst = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+      }
+    }
+    __syncthreads();
+
+    // outputs: MT*16 rows x TN*16 columns; D element (lane, e) of tile (i, j)
+    // is row i*16 + 4*(lane/16) + e, column j*16 + lane%16
+    const int outs = MT * 16 * TN * 16;
+    for (int o = tid; o < outs; o += kSmallThreads) {
+      const int i = o / (TN * 256);
+      const int rem = o - i * TN * 256;
+      const int j = rem >> 8;
+      const int le = rem & 255;  // lane*4 + e
+      const int ln = le >> 2, e = le & 3;
+      const int m = mbase + i * 16 + 4 * (ln >> 4) + e;
+      const int n = blockIdx.x * TN * 16 + j * 16 + (ln & 15);
+      if (m >= M || n >= a.N) continue;
+      float s = 0.f, u = 0.f;
+#pragma unroll
+      for (int w = 0; w < kSmallWaves; ++w) {
+        s += red[(((int64_t)w * kSmallMaxMT + i) * NT + j) * 256 + le];
+        if constexpr (EP == SE_SWIGLU)
+          u += red[(((int64_t)w * kSmallMaxMT + i) * NT + j + TN) * 256 + le];
+      }
+      const int64_t row = row0 + m;
+      if constexpr (EP == SE_F32) {
+        reinterpret_cast<float*>(a.y)[row * a.ldy + n] = s;
+      } else if constexpr (EP == SE_F16) {
+        _Float16 hv = (_Float16)s;
+        if (a.bias) hv = (_Float16)((float)hv + h2f(a.bias[n]));
+        reinterpret_cast<_Float16*>(a.y)[row * a.ldy + n] = hv;
+      } else {
+        const float act = s / (1.f + __expf(-s)) * u;
+        reinterpret_cast<_Float16*>(a.y)[row * a.ldy + n] = (_Float16)act;
+      }
+    }
+    __syncthreads();  // reduction reads done before the next chunk's table fill
+  }
+}
+
+template <bool NIB, int TN, int EP>
+static int launch_small_t(const SmallArgs& a, int groups, hipStream_t st) {
+  constexpr int NT = EP == SE_SWIGLU ? 2 * TN : TN;
+  auto kern = gemm_small_kernel<NIB, TN, EP>;
+  const int entries = table_entries(NIB, a.n_levels);
+  const size_t red_bytes = (size_t)kSmallWaves * kSmallMaxMT * NT * 64 * 16;
+  const size_t lds = (size_t)entries * 256 > red_bytes ? (size_t)entries * 256 : red_bytes;
+  if (lds > 160 * 1024) return PE_ERR_DIMS;
+  static const bool attr_ok = [&] {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+  }();
+  (void)attr_ok;
+  const int tiles = (a.N + TN * 16 - 1) / (TN * 16);
+  const uint8_t mb = NIB ? (uint8_t)((a.n_levels - 1) * 0x11) : (uint8_t)(a.n_levels - 1);
+  kern<<<dim3(tiles, groups), dim3(kSmallThreads), lds, st>>>(a, 0x01010101u * mb, entries);
+  return launch_status();
+}
+
+template <bool NIB, int EP>
+static int launch_small_ep(const SmallArgs& a, int groups, hipStream_t st) {
+  // two n-tiles per workgroup when that still leaves >= 1 workgroup per CU
+  // (the SwiGLU epilogue already computes two tiles per n-tile: keep TN = 1)
+  const int cus = num_cus();
+  if constexpr (EP != SE_SWIGLU) {
+    if ((int64_t)((a.N + 31) / 32) * groups >= cus) return launch_small_t<NIB, 2, EP>(a, groups, st);
+  }
+  return launch_small_t<NIB, 1, EP>(a, groups, st);
+}
+
+int gemm_small(bool nibble, int epilogue, const SmallArgs& a, int groups, hipStream_t st) {
+  switch (epilogue) {
+    case SE_F32: return nibble ? launch_small_ep<true, SE_F32>(a, groups, st) : launch_small_ep<false, SE_F32>(a, groups, st);
+    case SE_F16: return nibble ? launch_small_ep<true, SE_F16>(a, groups, st) : launch_small_ep<false, SE_F16>(a, groups, st);
+    case SE_SWIGLU: return nibble ? launch_small_ep<true, SE_SWIGLU>(a, groups, st) : launch_small_ep<false, SE_SWIGLU>(a, groups, st);
+    default: return PE_ERR_DTYPE;
+  }
+}
+
+}  // namespace pe

@@ -77,18 +77,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv1_kernel(
   const int C = row_bytes >> 4;  // 16-byte chunks per row
 
   // ---- 1. codebook table, one copy per lane -------------------------------
-  for (int e = wave; e < tbl_entries; e += kWaves) {
-    uint32_t val;
-    if constexpr (NIB) {
-      const int lo = e & 15, hi = e >> 4;
-      const float a = lo < n_levels ? ct[lo] : 0.f;
-      const float c = hi < n_levels ? ct[hi] : 0.f;
-      val = pack_h2(a, c);
-    } else {
-      val = __float_as_uint(ct[e]);
-    }
-    tbl[e * 64 + lane] = val;
-  }
+  if constexpr (NIB) fill_codebook<TBL_NIB_H2>(tbl, ct, n_levels, tbl_entries, kWaves);
+  else fill_codebook<TBL_F32>(tbl, ct, n_levels, tbl_entries, kWaves);
 
   // ---- 2. transformed activation into LDS ----------------------------------
   {
@@ -158,25 +148,33 @@ __global__ __launch_bounds__(kGemvThreads) void gemv1_kernel(
   const int tw = gridDim.x * kWaves;
   const int nshift = NIB ? 2 : 3;  // chunk -> block
 
-  // rows gw, gw + tw, gw + 2 tw, ... (balanced to +-1 row per wave), U at a time
+  // rows gw, gw + tw, gw + 2 tw, ... (balanced to +-1 row per wave), U at a time.
+  // Loads are unconditional on clamped (always valid) addresses and carry the
+  // raw norm bits, so all U*S loads issue back to back with no wait between
+  // them; rows/chunks out of range get a zero norm when accumulated.
   for (int k0 = 0; gw + k0 * tw < N; k0 += U) {
     uint4 d[U][S];
-    float nrm[U][S];
+    uint16_t nbits[U][S];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int n = gw + (k0 + u) * tw;
+      int n = gw + (k0 + u) * tw;
+      n = n < N ? n : N - 1;
 #pragma unroll
       for (int s = 0; s < S; ++s) {
-        const int c = s * 64 + lane;
-        if (n < N && c < C) {
-          d[u][s] = ld_nt16((codes + (size_t)n * row_bytes) + c);
-          nrm[u][s] = h2f(norms[(size_t)n * nb + (c >> nshift)]);
-        } else {
-          d[u][s] = make_uint4(0, 0, 0, 0);
-          nrm[u][s] = 0.f;
-        }
+        const int c = s * 64 + lane < C ? s * 64 + lane : C - 1;
+        d[u][s] = ld_nt16(codes + (size_t)n * row_bytes + (size_t)c * 16);
+        nbits[u][s] = norms[(size_t)n * nb + (c >> nshift)];
       }
     }
+    // keep every load of this batch ahead of the arithmetic: otherwise the
+    // scheduler sinks the norm loads to their uses, one round trip each
+    __builtin_amdgcn_sched_barrier(0);
+    float nrm[U][S];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+        nrm[u][s] = (gw + (k0 + u) * tw < N && s * 64 + lane < C) ? h2f(nbits[u][s]) : 0.f;
     float acc[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {

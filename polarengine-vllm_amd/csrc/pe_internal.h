@@ -38,6 +38,31 @@ struct GemmArgs {
 int gemv1(bool nibble, int xmode, int omode, const Gemv1Args& a, hipStream_t st);
 int gemv1_max_kp(bool nibble);
 
+// small-M epilogues
+enum { SE_F32 = 0, SE_F16 = 1, SE_SWIGLU = 2 };
+
+struct SmallArgs {
+  const uint8_t* codes;
+  const uint16_t* norms;
+  const float* ct;
+  int n_levels;
+  const uint32_t* xp;        // pair-f16 activations, rows of nb*64 uint32
+  const int32_t* a_rows;     // nullable: A row m reads xp row a_rows[m]
+  const int32_t* group_off;  // nullable: grouped mode, gridDim.y groups
+  int64_t codes_stride;      // bytes between experts' codes (grouped)
+  int64_t norms_stride;      // uint16 between experts' norms (grouped)
+  void* y;
+  int64_t ldy;
+  const uint16_t* bias;
+  int M;                     // rows (non-grouped)
+  int N;                     // output columns (SwiGLU: I; the weights hold 2I rows)
+  int nb;
+};
+
+// pe_gemm_small.hip: M <= kSmallMaxRows per pass is cheapest (larger M loops)
+constexpr int kSmallMaxRows = 64;
+int gemm_small(bool nibble, int epilogue, const SmallArgs& a, int groups, hipStream_t st);
+
 // pe_gemm.hip
 int gemm(bool nibble, int omode, const GemmArgs& a, hipStream_t st);
 size_t mm_xtf_workspace(bool nibble, int64_t M, int N, int nb);

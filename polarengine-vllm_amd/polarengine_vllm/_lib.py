@@ -21,7 +21,7 @@ LIB_PATH = os.environ.get(
 
 PE_OK = 0
 PE_DTYPE_F16, PE_DTYPE_BF16, PE_DTYPE_F32 = 0, 1, 2
-PE_XTF_F32, PE_XTF_F16, PE_XTF_PAIR_F16 = 0, 1, 2
+PE_XTF_F32, PE_XTF_F16, PE_XTF_PAIR_F16, PE_XTF_BF16 = 0, 1, 2, 3
 
 _c_int, _c_i64, _c_sz, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
 

@@ -55,7 +55,8 @@ def fwht_matmul(x: torch.Tensor, block_size: int = 128, out: Optional[torch.Tens
     rows = xc.numel() // in_features if in_features else 0
     if out is None:
         out = torch.empty_like(xc)
-    layout = {torch.float32: _lib.PE_XTF_F32, torch.float16: _lib.PE_XTF_F16}.get(out.dtype)
+    layout = {torch.float32: _lib.PE_XTF_F32, torch.float16: _lib.PE_XTF_F16,
+              torch.bfloat16: _lib.PE_XTF_BF16}.get(out.dtype)
     if layout is None:
         raise TypeError(f"unsupported output dtype {out.dtype}")
     dt = {torch.float16: _lib.PE_DTYPE_F16, torch.bfloat16: _lib.PE_DTYPE_BF16,

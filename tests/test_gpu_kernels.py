@@ -175,7 +175,8 @@ def test_polar_gemv_reference_api(n, k, bits):
 
 @pytest.mark.parametrize("n,k,bits", [(4096, 4096, 5), (12288, 4096, 3), (12288, 4096, 4),
                                       (4096, 12288, 4), (4096, 12288, 3), (1024, 4096, 5),
-                                      (4096, 4096, 6), (2816, 2048, 3), (2048, 1408, 4)])
+                                      (4096, 4096, 6), (2816, 2048, 3), (2048, 1408, 4),
+                                      (512, 20480, 4), (256, 9216, 5)])
 def test_linear_forward_m1(n, k, bits):
     from polarengine_vllm import _lib
     _say(f"linear m=1 n={n} k={k} bits={bits}")
@@ -306,3 +307,50 @@ def test_fwht_shared_across_qkv():
         want = O.linear_apply(x.cpu().numpy(), codes, norms, ct, k)
         check_close(y.float().cpu().numpy(), want.astype(np.float32), "qkv")
     GLOBAL_FWHT_CACHE.clear()
+
+
+def test_graph_replay_matches_eager():
+    """The bench replays captured HIP graphs: every replay, with eager work in
+    between, must equal the eager result (decode M=1 and small-M paths)."""
+    from polarengine_vllm import _lib
+    _say("graph replay")
+    rng = np.random.default_rng(12)
+    L = _lib.lib()
+    st = lambda: _lib.stream_ptr(torch.device(DEV))
+    cases = []
+    for m, n, k, bits in [(1, 4096, 4096, 4), (4, 2048, 4096, 3), (80, 1024, 1024, 5)]:
+        codes, norms, ct = rand_layer(rng, n, k, bits)
+        dcodes, nib = dev_codes(codes, bits)
+        x = to_dev(O.seeded_normal((m, k), 1.0, 50 + m))
+        y = torch.empty(m, n, dtype=torch.float16, device=DEV)
+        wsb = L.pe_linear_workspace_size(m, k, n, bits, int(nib))
+        ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=DEV)
+        args = (x, dcodes, to_dev(norms), to_dev(ct), y, ws, wsb, m, n, k, bits, nib)
+        cases.append(args)
+
+    def run(a):
+        x, dc, nr, ct, y, ws, wsb, m, n, k, bits, nib = a
+        _lib.check(L.pe_linear_forward(x.data_ptr(), 0, m, k, k, dc.data_ptr(), bits, int(nib),
+                                       nr.data_ptr(), ct.data_ptr(), 1 << bits, None, y.data_ptr(),
+                                       n, ws.data_ptr(), wsb, st()), "pe_linear_forward")
+
+    eager = []
+    for a in cases:
+        run(a)
+        eager.append(a[4].clone())
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for a in cases:
+            run(a)
+    for rep in range(4):
+        for a in cases:
+            a[4].zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for a, e in zip(cases, eager):
+            assert torch.equal(a[4], e), f"replay {rep} differs"
+        junk = torch.randn(1 << 20, device=DEV).sum()  # eager work between replays
+        torch.cuda.synchronize()
+        del junk
