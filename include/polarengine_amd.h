@@ -153,6 +153,42 @@ int pe_pack_nibble(const int8_t* codes, uint8_t* packed, int64_t rows, int64_t K
  */
 int pe_unpack_q5(const uint8_t* packed, int8_t* codes, int64_t rows, int64_t K, void* stream);
 
+/*
+ * MoE routing: scores (softmax or sigmoid of logits + optional correction
+ * bias) -> top-k (ties to the lower expert id) -> optional renormalise.
+ * Semantics of the routing in nemotron_offload.py:172-189 with the argument
+ * list of PolarPassthroughMoEMethod.apply (moe_method.py:74-78).
+ *   logits float32 [T, E]; topk_w float32 [T, top_k]; topk_ids int32 [T, top_k]
+ *   scoring: 0 = softmax, 1 = sigmoid. E <= 256, top_k <= 16.
+ */
+int pe_moe_route(const float* logits, int64_t T, int E, int top_k, int renormalize,
+                 int scoring, const float* correction_bias, float* topk_w,
+                 int32_t* topk_ids, void* stream);
+
+/*
+ * Quantized SwiGLU MoE forward over resident experts (the grouped-expert
+ * path). The reference forwards MoE layers to vLLM's bf16 fused MoE
+ * (moe_method.py:74-92); the per-expert math is that of
+ * nemotron_offload.py:203-226.
+ *   x       : float16 [T, H], H % 128 == 0
+ *   topk_w / topk_ids : routing (pe_moe_route or the caller's own)
+ *   w13     : codes [E, 2I, ...] in the runtime layout for (bits13, packed13),
+ *             norms float16 [E, 2I, H/128], ct13 float32 [2**bits13];
+ *             rows [0, I) are gate, rows [I, 2I) are up
+ *   w2      : codes [E, H, ...] over in_f = I padded to Ip = ceil(I/128)*128,
+ *             norms float16 [E, H, Ip/128], ct2 float32 [2**bits2]
+ *   out     : float16 [T, H] = sum_k topk_w[t,k] * expert_{ids[t,k]}(x_t)
+ * Workspace: pe_moe_workspace_size(T, top_k, E, H, I) bytes.
+ */
+size_t pe_moe_workspace_size(int64_t T, int top_k, int E, int H, int I);
+int pe_moe_forward(const void* x, int64_t T, int H, int I, int E, int top_k,
+                   const float* topk_w, const int32_t* topk_ids,
+                   const void* w13_codes, int bits13, int packed13,
+                   const uint16_t* w13_norms, const float* ct13, int n_levels13,
+                   const void* w2_codes, int bits2, int packed2,
+                   const uint16_t* w2_norms, const float* ct2, int n_levels2,
+                   void* out, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

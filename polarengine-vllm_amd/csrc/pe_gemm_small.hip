@@ -10,7 +10,7 @@
 //  * v_mfma_f32_16x16x32_f16 with the activations as the A operand (16 rows
 //    per m-tile, rows >= M zero) and the dequantized weights as B
 //    (16 weight rows per n-tile);
-//  * a 512-lane workgroup owns TN n-tiles and all M (up to 4 m-tiles); its 8
+//  * a 512-lane workgroup owns TN n-tiles and all M (1-2 m-tiles per pass); its 8
 //    waves split the K blocks, each reading a contiguous K range, and combine
 //    through LDS at the end -- no global workspace, deterministic order;
 //  * lane (n = l % 16, g = l / 16) reads 16 contiguous code bytes per row per
@@ -31,7 +31,6 @@ namespace pe {
 
 constexpr int kSmallThreads = 512;
 constexpr int kSmallWaves = kSmallThreads / 64;
-constexpr int kSmallMaxMT = 4;  // m-tiles of 16 per launch (M <= 64)
 
 template <bool NIB>
 __device__ __forceinline__ half8v dequant_slab_raw(const char* tbl, uint32_t wlo, uint32_t whi,
@@ -60,15 +59,81 @@ __device__ __forceinline__ half8v dequant_slab_raw(const char* tbl, uint32_t wlo
   return __builtin_bit_cast(half8v, v);
 }
 
-// TN: n-tiles of 16 weight rows per workgroup (SwiGLU doubles them: gate+up)
-template <bool NIB, int TN, int EP>
+// Loads of one 128-block for a wave: codes/norm bits of its NT n-tiles and
+// the pair-f16 activations of its (up to MTM) m-tiles.
+template <int NT, int MTM>
+struct SmallBlk {
+  u32x4v lo[NT];
+  u32x4v hi[NT];
+  uint16_t nbits[NT];
+  u32x4v a[MTM][4];
+};
+
+template <bool NIB, int NT, int MTM>
+__device__ __forceinline__ void load_sblk(SmallBlk<NT, MTM>& k, const uint8_t* const (&brow)[NT],
+                                          const uint16_t* const (&nrow)[NT],
+                                          const uint32_t* const (&arow)[MTM],
+                                          const bool (&alive)[MTM], int b) {
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    if constexpr (NIB) {
+      k.lo[j] = ld_nt16v(brow[j] + b * 64);
+    } else {
+      k.lo[j] = ld_nt16v(brow[j] + b * kBlock);
+      k.hi[j] = ld_nt16v(brow[j] + b * kBlock + 64);
+    }
+    k.nbits[j] = nrow[j][b];
+  }
+#pragma unroll
+  for (int i = 0; i < MTM; ++i) {
+    if (alive[i]) {
+      const u32x4v* p = reinterpret_cast<const u32x4v*>(arow[i] + b * 64);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) k.a[i][t] = p[t];
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) k.a[i][t] = u32x4v{0u, 0u, 0u, 0u};
+    }
+  }
+}
+
+template <bool NIB, int NT, int MTM>
+__device__ __forceinline__ void compute_sblk(float4v (&acc)[MTM][NT], const SmallBlk<NT, MTM>& k,
+                                             const char* tbl, uint32_t lane4, uint32_t code_mask,
+                                             int MT) {
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    float4v blk[MTM];
+#pragma unroll
+    for (int i = 0; i < MTM; ++i) blk[i] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t wl = k.lo[j][t] & code_mask;
+      const uint32_t wh = NIB ? 0u : (k.hi[j][t] & code_mask);
+      const half8v bf = dequant_slab_raw<NIB>(tbl, wl, wh, lane4);
+#pragma unroll
+      for (int i = 0; i < MTM; ++i)
+        if (i < MT)
+          blk[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, k.a[i][t]),
+                                                          bf, blk[i], 0, 0, 0);
+    }
+    // per-block norm applied to the fp32 block partial
+    const float nrm = h2f(k.nbits[j]);
+#pragma unroll
+    for (int i = 0; i < MTM; ++i) acc[i][j] += blk[i] * nrm;
+  }
+}
+
+// TN: n-tiles of 16 weight rows per workgroup (SwiGLU doubles them: gate+up);
+// MTM: m-tiles of 16 rows per pass over the weights.
+template <bool NIB, int TN, int EP, int MTM>
 __global__ __launch_bounds__(kSmallThreads) void gemm_small_kernel(
     SmallArgs a, uint32_t code_mask, int tbl_entries) {
   constexpr int NT = EP == SE_SWIGLU ? 2 * TN : TN;  // tiles actually computed
   extern __shared__ uint4 smem4[];
   char* smem = reinterpret_cast<char*>(smem4);
   char* tbl = smem;
-  float* red = reinterpret_cast<float*>(smem);  // after the K loop: [waves][4][NT][64][4]
+  float* red = reinterpret_cast<float*>(smem);  // after the K loop: [waves][MTM][NT][64][4]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -107,22 +172,21 @@ __global__ __launch_bounds__(kSmallThreads) void gemm_small_kernel(
   const int b_begin = (int)((int64_t)a.nb * wave / kSmallWaves);
   const int b_end = (int)((int64_t)a.nb * (wave + 1) / kSmallWaves);
 
-  // rows are processed 64 at a time (MT <= 4 m-tiles of 16)
-  for (int mbase = 0; mbase < M; mbase += 16 * kSmallMaxMT) {
+  for (int mbase = 0; mbase < M; mbase += 16 * MTM) {
     const int mrem = M - mbase;
-    const int MT = mrem >= 16 * kSmallMaxMT ? kSmallMaxMT : (mrem + 15) >> 4;
+    const int MT = mrem >= 16 * MTM ? MTM : (mrem + 15) >> 4;
 
-    // codebook table (LDS is shared with the reduction of the previous chunk)
+    // codebook table (this LDS also holds the previous pass's reduction)
     if constexpr (NIB)
       fill_codebook<TBL_NIB_H2>(reinterpret_cast<uint32_t*>(tbl), a.ct, a.n_levels, tbl_entries, kSmallWaves);
     else
       fill_codebook<TBL_F16>(reinterpret_cast<uint32_t*>(tbl), a.ct, a.n_levels, tbl_entries, kSmallWaves);
     __syncthreads();
 
-    const uint32_t* arow[kSmallMaxMT];
-    bool alive[kSmallMaxMT];
+    const uint32_t* arow[MTM];
+    bool alive[MTM];
 #pragma unroll
-    for (int i = 0; i < kSmallMaxMT; ++i) {
+    for (int i = 0; i < MTM; ++i) {
       const int m = mbase + i * 16 + l16;
       alive[i] = i < MT && m < M;
       int r = row0 + (alive[i] ? m : 0);
@@ -130,75 +194,32 @@ __global__ __launch_bounds__(kSmallThreads) void gemm_small_kernel(
       arow[i] = a.xp + (int64_t)r * xrow + 16 * g;
     }
 
-    float4v acc[kSmallMaxMT][NT];
+    float4v acc[MTM][NT];
 #pragma unroll
-    for (int i = 0; i < kSmallMaxMT; ++i)
+    for (int i = 0; i < MTM; ++i)
 #pragma unroll
       for (int j = 0; j < NT; ++j) acc[i][j] = float4v{0.f, 0.f, 0.f, 0.f};
 
+    // two-stage pipeline over this wave's blocks: block b+1 loads while b computes
+    SmallBlk<NT, MTM> cur, nxt;
+    if (b_begin < b_end) load_sblk<NIB, NT, MTM>(cur, brow, nrow, arow, alive, b_begin);
     for (int b = b_begin; b < b_end; ++b) {
-      u32x4v clo[NT], chi[NT];
-      uint16_t nbits[NT];
-#pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        if constexpr (NIB) {
-          clo[j] = ld_nt16v(brow[j] + b * 64);
-        } else {
-          clo[j] = ld_nt16v(brow[j] + b * kBlock);
-          chi[j] = ld_nt16v(brow[j] + b * kBlock + 64);
-        }
-        nbits[j] = nrow[j][b];
-      }
-      u32x4v af[kSmallMaxMT][4];
-#pragma unroll
-      for (int i = 0; i < kSmallMaxMT; ++i) {
-        if (alive[i]) {
-          const u32x4v* p = reinterpret_cast<const u32x4v*>(arow[i] + b * 64);
-#pragma unroll
-          for (int t = 0; t < 4; ++t) af[i][t] = p[t];
-        } else {
-#pragma unroll
-          for (int t = 0; t < 4; ++t) af[i][t] = u32x4v{0u, 0u, 0u, 0u};
-        }
-      }
-      // all loads of this block issue before any use
+      if (b + 1 < b_end) load_sblk<NIB, NT, MTM>(nxt, brow, nrow, arow, alive, b + 1);
       __builtin_amdgcn_sched_barrier(0);
-      float nrm[NT];
-#pragma unroll
-      for (int j = 0; j < NT; ++j) nrm[j] = h2f(nbits[j]);
-#pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        float4v blk[kSmallMaxMT];
-#pragma unroll
-        for (int i = 0; i < kSmallMaxMT; ++i) blk[i] = float4v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const uint32_t wl = clo[j][t] & code_mask;
-          const uint32_t wh = NIB ? 0u : (chi[j][t] & code_mask);
-          const half8v bf = dequant_slab_raw<NIB>(tbl, wl, wh, lane4);
-#pragma unroll
-          for (int i = 0; i < kSmallMaxMT; ++i) {
-            if (i < MT) {
-              blk[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, af[i][t]), bf,
-                                                              blk[i], 0, 0, 0);
-            }
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < kSmallMaxMT; ++i) acc[i][j] += blk[i] * nrm[j];
-      }
+      compute_sblk<NIB, NT, MTM>(acc, cur, tbl, lane4, code_mask, MT);
+      cur = nxt;
     }
 
     // ---- combine the 8 K-slices through LDS (over the table, now unused):
     // red[wave][i][j][lane][4]
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < kSmallMaxMT; ++i) {
+    for (int i = 0; i < MTM; ++i) {
       if (i >= MT) continue;
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         float4* dst = reinterpret_cast<float4*>(
-            red + ((((int64_t)wave * kSmallMaxMT + i) * NT + j) * 64 + lane) * 4);
+            red + ((((int64_t)wave * MTM + i) * NT + j) * 64 + lane) * 4);
         *dst = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
       }
     }
@@ -219,9 +240,9 @@ __global__ __launch_bounds__(kSmallThreads) void gemm_small_kernel(
       float s = 0.f, u = 0.f;
 #pragma unroll
       for (int w = 0; w < kSmallWaves; ++w) {
-        s += red[(((int64_t)w * kSmallMaxMT + i) * NT + j) * 256 + le];
+        s += red[(((int64_t)w * MTM + i) * NT + j) * 256 + le];
         if constexpr (EP == SE_SWIGLU)
-          u += red[(((int64_t)w * kSmallMaxMT + i) * NT + j + TN) * 256 + le];
+          u += red[(((int64_t)w * MTM + i) * NT + j + TN) * 256 + le];
       }
       const int64_t row = row0 + m;
       if constexpr (EP == SE_F32) {
@@ -235,16 +256,16 @@ __global__ __launch_bounds__(kSmallThreads) void gemm_small_kernel(
         reinterpret_cast<_Float16*>(a.y)[row * a.ldy + n] = (_Float16)act;
       }
     }
-    __syncthreads();  // reduction reads done before the next chunk's table fill
+    __syncthreads();  // reduction reads done before the next pass's table fill
   }
 }
 
-template <bool NIB, int TN, int EP>
+template <bool NIB, int TN, int EP, int MTM>
 static int launch_small_t(const SmallArgs& a, int groups, hipStream_t st) {
   constexpr int NT = EP == SE_SWIGLU ? 2 * TN : TN;
-  auto kern = gemm_small_kernel<NIB, TN, EP>;
+  auto kern = gemm_small_kernel<NIB, TN, EP, MTM>;
   const int entries = table_entries(NIB, a.n_levels);
-  const size_t red_bytes = (size_t)kSmallWaves * kSmallMaxMT * NT * 64 * 16;
+  const size_t red_bytes = (size_t)kSmallWaves * MTM * NT * 64 * 16;
   const size_t lds = (size_t)entries * 256 > red_bytes ? (size_t)entries * 256 : red_bytes;
   if (lds > 160 * 1024) return PE_ERR_DIMS;
   static const bool attr_ok = [&] {
@@ -260,13 +281,17 @@ static int launch_small_t(const SmallArgs& a, int groups, hipStream_t st) {
 
 template <bool NIB, int EP>
 static int launch_small_ep(const SmallArgs& a, int groups, hipStream_t st) {
+  // one m-tile per pass when every group fits in 16 rows (decode batches);
+  // otherwise two (grouped launches do not know their sizes on the host).
+  const bool one = !a.group_off && a.M <= 16;
   // two n-tiles per workgroup when that still leaves >= 1 workgroup per CU
-  // (the SwiGLU epilogue already computes two tiles per n-tile: keep TN = 1)
+  // (the SwiGLU epilogue already computes gate and up tiles: keep TN = 1)
   const int cus = num_cus();
   if constexpr (EP != SE_SWIGLU) {
-    if ((int64_t)((a.N + 31) / 32) * groups >= cus) return launch_small_t<NIB, 2, EP>(a, groups, st);
+    if ((int64_t)((a.N + 31) / 32) * groups >= cus)
+      return one ? launch_small_t<NIB, 2, EP, 1>(a, groups, st) : launch_small_t<NIB, 2, EP, 2>(a, groups, st);
   }
-  return launch_small_t<NIB, 1, EP>(a, groups, st);
+  return one ? launch_small_t<NIB, 1, EP, 1>(a, groups, st) : launch_small_t<NIB, 1, EP, 2>(a, groups, st);
 }
 
 int gemm_small(bool nibble, int epilogue, const SmallArgs& a, int groups, hipStream_t st) {

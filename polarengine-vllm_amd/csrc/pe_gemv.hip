@@ -58,7 +58,9 @@ __device__ __forceinline__ void stage_block(char* xs, int b, int q, const float 
   }
 }
 
-template <bool NIB, int S, int U, int XM, int OM>
+// XREG: the lane's activation slice lives in registers (S chunks); otherwise
+// it is re-read from LDS per chunk (large K, S = 1 per pass over the row).
+template <bool NIB, int S, int U, int XM, int OM, bool XREG = true>
 __global__ __launch_bounds__(kGemvThreads) void gemv1_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
     const float* __restrict__ ct, int n_levels, uint32_t code_mask, int tbl_entries,
@@ -121,26 +123,32 @@ __global__ __launch_bounds__(kGemvThreads) void gemv1_kernel(
   }
   __syncthreads();
 
-  // ---- 3. this lane's activation slice into registers -----------------------
-  // nibble chunk c: block c>>2, pairs 16*(c&3) .. +15; int8 chunk c: block
-  // c>>3, positions 16*(c&7) .. +15.
+  // ---- 3. activation slice of this lane ------------------------------------
+  // Pass p covers chunks (p*S + s)*64 + lane, s < S. Nibble chunk c: block
+  // c>>2, pairs 16*(c&3)..+15; int8 chunk c: block c>>3, positions
+  // 16*(c&7)..+15. With XREG there is one pass and the slice is loaded once;
+  // otherwise (large K) each pass re-reads its slice from LDS.
+  const int npass = XREG ? 1 : (C + 64 * S - 1) / (64 * S);
   uint32_t xr[S][16];
+  auto load_x = [&](int pass) {
 #pragma unroll
-  for (int s = 0; s < S; ++s) {
-    const int c = s * 64 + lane;
-    if (c < C) {
-      const int off = NIB ? ((c >> 2) * 64 + (c & 3) * 16) * 4 : ((c >> 3) * kBlock + (c & 7) * 16) * 4;
-      const uint4* p = reinterpret_cast<const uint4*>(xs + off);
+    for (int s = 0; s < S; ++s) {
+      const int c = (pass * S + s) * 64 + lane;
+      if (c < C) {
+        const int off = NIB ? ((c >> 2) * 64 + (c & 3) * 16) * 4 : ((c >> 3) * kBlock + (c & 7) * 16) * 4;
+        const u32x4v* p = reinterpret_cast<const u32x4v*>(xs + off);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint4 w = p[j];
-        xr[s][4 * j] = w.x; xr[s][4 * j + 1] = w.y; xr[s][4 * j + 2] = w.z; xr[s][4 * j + 3] = w.w;
+        for (int j = 0; j < 4; ++j) {
+          const u32x4v w = p[j];
+          xr[s][4 * j] = w[0]; xr[s][4 * j + 1] = w[1]; xr[s][4 * j + 2] = w[2]; xr[s][4 * j + 3] = w[3];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) xr[s][j] = 0u;
       }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) xr[s][j] = 0u;
     }
-  }
+  };
+  if constexpr (XREG) load_x(0);
 
   // ---- 4. stream rows --------------------------------------------------------
   const uint32_t lane4 = (uint32_t)lane << 2;
@@ -148,67 +156,72 @@ __global__ __launch_bounds__(kGemvThreads) void gemv1_kernel(
   const int tw = gridDim.x * kWaves;
   const int nshift = NIB ? 2 : 3;  // chunk -> block
 
-  // rows gw, gw + tw, gw + 2 tw, ... (balanced to +-1 row per wave), U at a time.
-  // Loads are unconditional on clamped (always valid) addresses and carry the
-  // raw norm bits, so all U*S loads issue back to back with no wait between
-  // them; rows/chunks out of range get a zero norm when accumulated.
+  // rows gw, gw + tw, gw + 2 tw, ... (balanced to +-1 row per wave), U at a
+  // time. All U*S loads of a batch issue back to back (raw norm bits; no use
+  // before the scheduling barrier); rows past N are skipped (wave-uniform),
+  // chunks past the row end re-read the last chunk and get a zero norm.
   for (int k0 = 0; gw + k0 * tw < N; k0 += U) {
-    uint4 d[U][S];
-    uint16_t nbits[U][S];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      int n = gw + (k0 + u) * tw;
-      n = n < N ? n : N - 1;
-#pragma unroll
-      for (int s = 0; s < S; ++s) {
-        const int c = s * 64 + lane < C ? s * 64 + lane : C - 1;
-        d[u][s] = ld_nt16(codes + (size_t)n * row_bytes + (size_t)c * 16);
-        nbits[u][s] = norms[(size_t)n * nb + (c >> nshift)];
-      }
-    }
-    // keep every load of this batch ahead of the arithmetic: otherwise the
-    // scheduler sinks the norm loads to their uses, one round trip each
-    __builtin_amdgcn_sched_barrier(0);
-    float nrm[U][S];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int s = 0; s < S; ++s)
-        nrm[u][s] = (gw + (k0 + u) * tw < N && s * 64 + lane < C) ? h2f(nbits[u][s]) : 0.f;
     float acc[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float a = 0.f;
+    for (int u = 0; u < U; ++u) acc[u] = 0.f;
+    for (int pass = 0; pass < npass; ++pass) {
+      if constexpr (!XREG) load_x(pass);
+      uint4 d[U][S];
+      uint16_t nbits[U][S];
 #pragma unroll
-      for (int s = 0; s < S; ++s) {
-        const uint32_t ws[4] = {d[u][s].x & code_mask, d[u][s].y & code_mask,
-                                d[u][s].z & code_mask, d[u][s].w & code_mask};
-        float part = 0.f;
+      for (int u = 0; u < U; ++u) {
+        const int n = gw + (k0 + u) * tw;
+        if (n < N) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t a0 = tbl_addr<0>(ws[j], lane4);
-          const uint32_t a1 = tbl_addr<1>(ws[j], lane4);
-          const uint32_t a2 = tbl_addr<2>(ws[j], lane4);
-          const uint32_t a3 = tbl_addr<3>(ws[j], lane4);
-          const uint32_t t0 = *reinterpret_cast<const uint32_t*>(smem + a0);
-          const uint32_t t1 = *reinterpret_cast<const uint32_t*>(smem + a1);
-          const uint32_t t2 = *reinterpret_cast<const uint32_t*>(smem + a2);
-          const uint32_t t3 = *reinterpret_cast<const uint32_t*>(smem + a3);
-          if constexpr (NIB) {
-            part = __builtin_amdgcn_fdot2(as_h2(t0), as_h2(xr[s][4 * j + 0]), part, false);
-            part = __builtin_amdgcn_fdot2(as_h2(t1), as_h2(xr[s][4 * j + 1]), part, false);
-            part = __builtin_amdgcn_fdot2(as_h2(t2), as_h2(xr[s][4 * j + 2]), part, false);
-            part = __builtin_amdgcn_fdot2(as_h2(t3), as_h2(xr[s][4 * j + 3]), part, false);
-          } else {
-            part = fmaf(__uint_as_float(t0), __uint_as_float(xr[s][4 * j + 0]), part);
-            part = fmaf(__uint_as_float(t1), __uint_as_float(xr[s][4 * j + 1]), part);
-            part = fmaf(__uint_as_float(t2), __uint_as_float(xr[s][4 * j + 2]), part);
-            part = fmaf(__uint_as_float(t3), __uint_as_float(xr[s][4 * j + 3]), part);
+          for (int s = 0; s < S; ++s) {
+            int c = (pass * S + s) * 64 + lane;
+            c = c < C ? c : C - 1;
+            d[u][s] = ld_nt16(codes + (size_t)n * row_bytes + (size_t)c * 16);
+            nbits[u][s] = norms[(size_t)n * nb + (c >> nshift)];
+          }
+        } else {
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+            d[u][s] = make_uint4(0, 0, 0, 0);
+            nbits[u][s] = 0;
           }
         }
-        a = fmaf(part, nrm[u][s], a);
       }
-      acc[u] = a;
+      // keep every load of this batch ahead of the arithmetic: otherwise the
+      // scheduler sinks the norm loads to their uses, one round trip each
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float a = acc[u];
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          const bool live = gw + (k0 + u) * tw < N && (pass * S + s) * 64 + lane < C;
+          const float nrm = live ? h2f(nbits[u][s]) : 0.f;
+          const uint32_t ws[4] = {d[u][s].x & code_mask, d[u][s].y & code_mask,
+                                  d[u][s].z & code_mask, d[u][s].w & code_mask};
+          float part = 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t t0 = *reinterpret_cast<const uint32_t*>(smem + tbl_addr<0>(ws[j], lane4));
+            const uint32_t t1 = *reinterpret_cast<const uint32_t*>(smem + tbl_addr<1>(ws[j], lane4));
+            const uint32_t t2 = *reinterpret_cast<const uint32_t*>(smem + tbl_addr<2>(ws[j], lane4));
+            const uint32_t t3 = *reinterpret_cast<const uint32_t*>(smem + tbl_addr<3>(ws[j], lane4));
+            if constexpr (NIB) {
+              part = __builtin_amdgcn_fdot2(as_h2(t0), as_h2(xr[s][4 * j + 0]), part, false);
+              part = __builtin_amdgcn_fdot2(as_h2(t1), as_h2(xr[s][4 * j + 1]), part, false);
+              part = __builtin_amdgcn_fdot2(as_h2(t2), as_h2(xr[s][4 * j + 2]), part, false);
+              part = __builtin_amdgcn_fdot2(as_h2(t3), as_h2(xr[s][4 * j + 3]), part, false);
+            } else {
+              part = fmaf(__uint_as_float(t0), __uint_as_float(xr[s][4 * j + 0]), part);
+              part = fmaf(__uint_as_float(t1), __uint_as_float(xr[s][4 * j + 1]), part);
+              part = fmaf(__uint_as_float(t2), __uint_as_float(xr[s][4 * j + 2]), part);
+              part = fmaf(__uint_as_float(t3), __uint_as_float(xr[s][4 * j + 3]), part);
+            }
+          }
+          a = fmaf(part, nrm, a);
+        }
+        acc[u] = a;
+      }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) acc[u] = wave_sum(acc[u]);
@@ -236,10 +249,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv1_kernel(
 // host launch
 // ---------------------------------------------------------------------------
 
-template <bool NIB, int S, int XM, int OM>
+template <bool NIB, int S, int XM, int OM, bool XREG>
 static int launch_gemv1_s(const Gemv1Args& a, hipStream_t st) {
-  constexpr int U = S <= 2 ? 4 : (S <= 6 ? 2 : 1);
-  auto kern = gemv1_kernel<NIB, S, U, XM, OM>;
+  constexpr int U = !XREG ? 2 : (S <= 2 ? 4 : (S <= 6 ? 2 : 1));
+  auto kern = gemv1_kernel<NIB, S, U, XM, OM, XREG>;
   const int entries = table_entries(NIB, a.n_levels);
   const size_t lds = (size_t)entries * 256 + (size_t)a.nb * (NIB ? 256 : 512);
   if (lds > 160 * 1024) return PE_ERR_DIMS;
@@ -264,17 +277,19 @@ static int launch_gemv1_s(const Gemv1Args& a, hipStream_t st) {
 template <bool NIB, int XM, int OM>
 static int launch_gemv1(const Gemv1Args& a, hipStream_t st) {
   const int C = (NIB ? a.nb * 64 : a.nb * kBlock) / 16;
-  if (C <= 64) return launch_gemv1_s<NIB, 1, XM, OM>(a, st);
-  if (C <= 128) return launch_gemv1_s<NIB, 2, XM, OM>(a, st);
-  if (C <= 192) return launch_gemv1_s<NIB, 3, XM, OM>(a, st);
-  if (C <= 256) return launch_gemv1_s<NIB, 4, XM, OM>(a, st);
-  if (C <= 384) return launch_gemv1_s<NIB, 6, XM, OM>(a, st);
-  if (C <= 512) return launch_gemv1_s<NIB, 8, XM, OM>(a, st);
-  return PE_ERR_DIMS;
+  if (C <= 64) return launch_gemv1_s<NIB, 1, XM, OM, true>(a, st);
+  if (C <= 128) return launch_gemv1_s<NIB, 2, XM, OM, true>(a, st);
+  if (C <= 192) return launch_gemv1_s<NIB, 3, XM, OM, true>(a, st);
+  if (C <= 256) return launch_gemv1_s<NIB, 4, XM, OM, true>(a, st);
+  if (C <= 384) return launch_gemv1_s<NIB, 6, XM, OM, true>(a, st);
+  if (C <= 512) return launch_gemv1_s<NIB, 8, XM, OM, true>(a, st);
+  // large K: activations stay in LDS, four chunks per lane per pass
+  return launch_gemv1_s<NIB, 4, XM, OM, false>(a, st);
 }
 
-// Largest K (padded) the register-resident M = 1 kernel takes.
-int gemv1_max_kp(bool nibble) { return nibble ? 512 * 32 : 512 * 16; }
+// Largest K (padded) the M = 1 kernel takes: LDS holds the codebook table
+// (<= 64 KB) and the activations (256 B per block as pairs, 512 B as fp32).
+int gemv1_max_kp(bool nibble) { return nibble ? 96 * 1024 / 256 * 128 : 96 * 1024 / 512 * 128; }
 
 int gemv1(bool nibble, int xmode, int omode, const Gemv1Args& a, hipStream_t st) {
   if (nibble) {
@@ -302,7 +317,6 @@ int polar_gemv_ref(bool nibble, const void* codes, const float* x_tf, const uint
   if (out_f <= 0 || n_blocks <= 0 || kp != n_blocks * kBlock) return PE_ERR_DIMS;
   if (int rc = check_levels(nibble, n_levels)) return rc;
   if (!aligned16(codes) || !aligned16(x_tf)) return PE_ERR_ALIGN;
-  if (kp > gemv1_max_kp(nibble)) return PE_ERR_DIMS;
   Gemv1Args a{reinterpret_cast<const uint8_t*>(codes), norms, ct, n_levels, x_tf, out, nullptr,
               out_f, n_blocks};
   return gemv1(nibble, XM_XTF_F32, OM_F32, a, st);

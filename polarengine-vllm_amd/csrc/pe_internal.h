@@ -62,6 +62,9 @@ struct SmallArgs {
 // pe_gemm_small.hip: M <= kSmallMaxRows per pass is cheapest (larger M loops)
 constexpr int kSmallMaxRows = 64;
 int gemm_small(bool nibble, int epilogue, const SmallArgs& a, int groups, hipStream_t st);
+// same, with A read from fp32 natural-layout rows (already transformed) and
+// fp32 output: the reference API's GEMV beyond the register kernel's K
+int gemm_small_xf32(bool nibble, const SmallArgs& a, hipStream_t st);
 
 // pe_gemm.hip
 int gemm(bool nibble, int omode, const GemmArgs& a, hipStream_t st);

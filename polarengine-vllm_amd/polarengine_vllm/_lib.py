@@ -43,6 +43,12 @@ _SIGNATURES = {
                                        _vp, _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
     "pe_pack_nibble": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
     "pe_unpack_q5": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
+    "pe_moe_route": (_c_int, [_vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp]),
+    "pe_moe_workspace_size": (_c_sz, [_c_i64, _c_int, _c_int, _c_int, _c_int]),
+    "pe_moe_forward": (_c_int, [_vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
+                                _vp, _c_int, _c_int, _vp, _vp, _c_int,
+                                _vp, _c_int, _c_int, _vp, _vp, _c_int,
+                                _vp, _vp, _c_sz, _vp]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

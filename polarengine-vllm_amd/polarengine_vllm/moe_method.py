@@ -1,0 +1,181 @@
+"""MoE methods (reference: polarengine_vllm/moe_method.py).
+
+* ``PolarQuantMoEMethod`` -- PolarQuant-quantized experts, all resident on
+  the GPU, run by the grouped-expert HIP path (``pe_moe_route`` +
+  ``pe_moe_forward``). The reference has no quantized expert compute (its
+  experts stay bf16 in vLLM's fused MoE); the math follows its in-repo MoE
+  forward (nemotron_offload.py:172-226): scores -> top-k -> renormalise ->
+  SwiGLU(w13 = [gate; up]) -> w2 -> weighted sum.
+* ``PolarPassthroughMoEMethod`` -- the reference's pass-through to vLLM's
+  unquantized fused MoE, for checkpoints whose experts are not quantized
+  (requires vLLM).
+
+Expert weight layout follows the reference's fallback layout
+(moe_method.py:56-72): w13 [E, 2I, H] (rows [0, I) gate, [I, 2I) up) and
+w2 [E, H, I], here as PolarQuant codes / fp16 norms / ct_scaled per matrix.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from polarengine_vllm import _lib
+from polarengine_vllm.utils import get_centroids
+
+
+class PolarQuantMoEMethod:
+    """Quantized fused-MoE method (vLLM FusedMoEMethodBase interface)."""
+
+    def __init__(self, block_size: int = 128, bits13: int = 3, bits2: int = 4) -> None:
+        if block_size != 128:
+            raise ValueError("the gfx950 kernels implement block_size 128")
+        self.block_size = block_size
+        self.bits13 = bits13
+        self.bits2 = bits2
+
+    def create_weights(self, layer: torch.nn.Module, num_experts: int, hidden_size: int,
+                       intermediate_size_per_partition: int, params_dtype: torch.dtype,
+                       **kwargs) -> None:
+        bs = self.block_size
+        e, h, i = num_experts, hidden_size, intermediate_size_per_partition
+        hp = (h + bs - 1) // bs * bs
+        ip = (i + bs - 1) // bs * bs
+        if hp != h:
+            raise ValueError("hidden_size must be a multiple of 128")
+        layer.register_buffer("w13_codes", torch.zeros(e, 2 * i, hp, dtype=torch.int8))
+        layer.register_buffer("w13_norms", torch.zeros(e, 2 * i, hp // bs, dtype=torch.float16))
+        layer.register_buffer("w13_ct_scaled", (get_centroids(self.bits13) / math.sqrt(bs)).clone())
+        layer.register_buffer("w2_codes", torch.zeros(e, h, ip, dtype=torch.int8))
+        layer.register_buffer("w2_norms", torch.zeros(e, h, ip // bs, dtype=torch.float16))
+        layer.register_buffer("w2_ct_scaled", (get_centroids(self.bits2) / math.sqrt(bs)).clone())
+        layer.num_experts = e
+        layer.hidden_size = h
+        layer.intermediate_size = i
+        layer.w13_packed = False
+        layer.w2_packed = False
+
+    def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
+        """ct to the codes' device; nibble-pack matrices with bits <= 4."""
+        from polarengine_vllm.packing import pack_codes_half_block
+        dev = layer.w13_codes.device
+        layer.w13_ct_scaled = layer.w13_ct_scaled.to(dev, torch.float32).contiguous()
+        layer.w2_ct_scaled = layer.w2_ct_scaled.to(dev, torch.float32).contiguous()
+        if self.bits13 <= 4 and not layer.w13_packed:
+            layer.w13_codes = pack_codes_half_block(layer.w13_codes.contiguous(), self.block_size)
+            layer.w13_packed = True
+        if self.bits2 <= 4 and not layer.w2_packed:
+            layer.w2_codes = pack_codes_half_block(layer.w2_codes.contiguous(), self.block_size)
+            layer.w2_packed = True
+
+    def select_experts(self, router_logits: torch.Tensor, top_k: int, renormalize: bool,
+                       scoring_func: str = "softmax",
+                       e_score_correction_bias: Optional[torch.Tensor] = None):
+        """(topk_weights float32 [T, k], topk_ids int32 [T, k]) via pe_moe_route."""
+        dev = _lib.require_device(router_logits)
+        lg = router_logits.to(torch.float32).contiguous()
+        t, e = lg.shape
+        w = torch.empty(t, top_k, dtype=torch.float32, device=dev)
+        ids = torch.empty(t, top_k, dtype=torch.int32, device=dev)
+        bias = None
+        if e_score_correction_bias is not None:
+            bias = e_score_correction_bias.to(device=dev, dtype=torch.float32).contiguous()
+        scoring = {"softmax": 0, "sigmoid": 1}.get(scoring_func)
+        if scoring is None:
+            raise ValueError(f"unsupported scoring_func {scoring_func}")
+        _lib.check(_lib.lib().pe_moe_route(lg.data_ptr(), t, e, top_k, int(bool(renormalize)),
+                                           scoring, _lib.ptr(bias), w.data_ptr(), ids.data_ptr(),
+                                           _lib.stream_ptr(dev)), "pe_moe_route")
+        return w, ids
+
+    def apply(self, layer: torch.nn.Module, x: torch.Tensor, router_logits: torch.Tensor,
+              top_k: int, renormalize: bool, use_grouped_topk: bool = False,
+              topk_group: Optional[int] = None, num_expert_group: Optional[int] = None,
+              custom_routing_function=None, scoring_func: str = "softmax",
+              e_score_correction_bias: Optional[torch.Tensor] = None, **kwargs) -> torch.Tensor:
+        """Routed quantized SwiGLU experts: [T, H] fp16 -> [T, H] fp16."""
+        if use_grouped_topk:
+            raise NotImplementedError("grouped top-k routing is not implemented by the "
+                                      "PolarEngine gfx950 MoE path")
+        dev = _lib.require_device(x, layer.w13_codes)
+        if x.dtype != torch.float16:
+            raise TypeError(f"PolarEngine gfx950 kernels take float16 activations, got {x.dtype}")
+        xs = x.reshape(-1, layer.hidden_size).contiguous()
+        t = xs.shape[0]
+        if custom_routing_function is not None:
+            w, ids = custom_routing_function(hidden_states=xs, gating_output=router_logits,
+                                             topk=top_k, renormalize=renormalize)
+            w = w.to(torch.float32).contiguous()
+            ids = ids.to(torch.int32).contiguous()
+        else:
+            w, ids = self.select_experts(router_logits.reshape(t, -1), top_k, renormalize,
+                                         scoring_func, e_score_correction_bias)
+        out = torch.empty_like(xs)
+        if t == 0:
+            return out.view(x.shape)
+        L = _lib.lib()
+        e, h, i = layer.num_experts, layer.hidden_size, layer.intermediate_size
+        wsb = L.pe_moe_workspace_size(t, top_k, e, h, i)
+        ws = _lib.workspace(dev, wsb)
+        rc = L.pe_moe_forward(
+            xs.data_ptr(), t, h, i, e, top_k, w.data_ptr(), ids.data_ptr(),
+            layer.w13_codes.data_ptr(), self.bits13, int(layer.w13_packed),
+            layer.w13_norms.data_ptr(), layer.w13_ct_scaled.data_ptr(), 1 << self.bits13,
+            layer.w2_codes.data_ptr(), self.bits2, int(layer.w2_packed),
+            layer.w2_norms.data_ptr(), layer.w2_ct_scaled.data_ptr(), 1 << self.bits2,
+            out.data_ptr(), _lib.ptr(ws), wsb, _lib.stream_ptr(dev))
+        _lib.check(rc, "pe_moe_forward")
+        return out.view(x.shape)
+
+    def get_fused_moe_quant_config(self):
+        return None
+
+
+class PolarPassthroughMoEMethod:
+    """Unquantized experts through vLLM's fused MoE (reference moe_method.py:18-98)."""
+
+    def __init__(self):
+        self._initialized = False
+        self._inner = None
+
+    def _lazy_init(self, layer):
+        if self._initialized:
+            return
+        try:
+            from vllm.model_executor.layers.fused_moe.unquantized_fused_moe_method import (  # type: ignore
+                UnquantizedFusedMoEMethod)
+            self._inner = UnquantizedFusedMoEMethod(moe=layer)
+            self._initialized = True
+        except (ImportError, AttributeError, TypeError):
+            pass
+
+    def create_weights(self, layer, num_experts, hidden_size, intermediate_size_per_partition,
+                       params_dtype, **kwargs):
+        self._lazy_init(layer)
+        if not self._initialized:
+            raise RuntimeError("PolarPassthroughMoEMethod needs vLLM's unquantized fused MoE")
+        return self._inner.create_weights(
+            layer, num_experts=num_experts, hidden_size=hidden_size,
+            intermediate_size_per_partition=intermediate_size_per_partition,
+            params_dtype=params_dtype, **kwargs)
+
+    def apply(self, layer, x, router_logits, top_k, renormalize, **kwargs):
+        self._lazy_init(layer)
+        if not self._initialized:
+            raise RuntimeError("PolarPassthroughMoEMethod: vLLM fused MoE not available")
+        return self._inner.apply(layer, x, router_logits, top_k, renormalize, **kwargs)
+
+    def get_fused_moe_quant_config(self):
+        if self._initialized and hasattr(self._inner, "get_fused_moe_quant_config"):
+            return self._inner.get_fused_moe_quant_config()
+        return None
+
+
+try:  # virtual subclass for vLLM's isinstance checks (reference moe_method.py:103-107)
+    from vllm.model_executor.layers.fused_moe.layer import FusedMoEMethodBase  # type: ignore
+    FusedMoEMethodBase.register(PolarQuantMoEMethod)
+    FusedMoEMethodBase.register(PolarPassthroughMoEMethod)
+except Exception:
+    pass

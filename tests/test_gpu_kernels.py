@@ -187,13 +187,15 @@ def test_linear_forward_m1(n, k, bits):
     bias = O.seeded_normal((n,), 0.1, 6)
     want = O.linear_apply(x, codes, norms, ct, k, bias)
     dcodes, nib = dev_codes(codes, bits)
+    # device tensors stay referenced until the kernel has run
     xd = to_dev(np.pad(x, ((0, 0), (0, kp - k))))
+    nd, cd, bd = to_dev(norms), to_dev(ct), to_dev(bias)
     y = torch.empty(1, n, dtype=torch.float16, device=DEV)
     L = _lib.lib()
     rc = L.pe_linear_forward(xd.data_ptr(), 0, 1, kp, kp, dcodes.data_ptr(), bits, int(nib),
-                             to_dev(norms).data_ptr(), to_dev(ct).data_ptr(), 1 << bits,
-                             to_dev(bias).data_ptr(), y.data_ptr(), n, None, 0,
-                             _lib.stream_ptr(torch.device(DEV)))
+                             nd.data_ptr(), cd.data_ptr(), 1 << bits, bd.data_ptr(),
+                             y.data_ptr(), n, None, 0, _lib.stream_ptr(torch.device(DEV)))
+    torch.cuda.synchronize()
     _lib.check(rc, "pe_linear_forward")
     check_close(y.float().cpu().numpy(), want.astype(np.float32), f"linear m=1 {n}x{k} q{bits}")
 
@@ -237,10 +239,12 @@ def test_prefill_gemm_full_size_row_sample(m, n, k, bits):
     L = _lib.lib()
     wsb = L.pe_linear_workspace_size(m, k, n, bits, int(nib))
     ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
-    rc = L.pe_linear_forward(to_dev(x).data_ptr(), 0, m, k, k, dcodes.data_ptr(), bits, int(nib),
-                             to_dev(norms).data_ptr(), to_dev(ct).data_ptr(), 1 << bits, None,
+    xd, nd, cd = to_dev(x), to_dev(norms), to_dev(ct)
+    rc = L.pe_linear_forward(xd.data_ptr(), 0, m, k, k, dcodes.data_ptr(), bits, int(nib),
+                             nd.data_ptr(), cd.data_ptr(), 1 << bits, None,
                              y.data_ptr(), n, ws.data_ptr(), wsb,
                              _lib.stream_ptr(torch.device(DEV)))
+    torch.cuda.synchronize()
     _lib.check(rc, "pe_linear_forward")
     rows = np.sort(rng.choice(m, 24, replace=False))
     rows[0], rows[-1] = 0, m - 1
@@ -354,3 +358,66 @@ def test_graph_replay_matches_eager():
         junk = torch.randn(1 << 20, device=DEV).sum()  # eager work between replays
         torch.cuda.synchronize()
         del junk
+
+
+# ---------------------------------------------------------------------------
+# MoE: routing and the grouped quantized-expert forward (parity unpinned
+# against vLLM's fused MoE, which the reference delegates to; pinned against
+# the oracle's per-expert loop with the routing of nemotron_offload.py)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("scoring", ["softmax", "sigmoid"])
+@pytest.mark.parametrize("renorm", [True, False])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_moe_route_matches_oracle(scoring, renorm, with_bias):
+    from polarengine_vllm.moe_method import PolarQuantMoEMethod
+    _say(f"moe route {scoring} renorm={renorm} bias={with_bias}")
+    logits = O.seeded_normal((128, 64), 1.0, 70, np.float32)
+    bias = O.seeded_normal((64,), 0.5, 71, np.float32) if with_bias else None
+    w_ref, ids_ref = O.moe_route(logits, 8, renorm, scoring, bias)
+    meth = PolarQuantMoEMethod(128, 3, 4)
+    w, ids = meth.select_experts(to_dev(logits), 8, renorm, scoring,
+                                 None if bias is None else to_dev(bias))
+    assert np.array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_allclose(w.cpu().numpy(), w_ref, rtol=2e-6, atol=1e-7)
+
+
+def _moe_layer(rng, e, hdim, inter, b13, b2):
+    from polarengine_vllm.moe_method import PolarQuantMoEMethod
+    ip = (inter + 127) // 128 * 128
+    c13 = rng.integers(0, 1 << b13, (e, 2 * inter, hdim)).astype(np.int8)
+    n13 = (np.abs(rng.standard_normal((e, 2 * inter, hdim // 128))) * 0.3 + 0.05).astype(np.float16)
+    c2 = rng.integers(0, 1 << b2, (e, hdim, ip)).astype(np.int8)
+    n2 = (np.abs(rng.standard_normal((e, hdim, ip // 128))) * 0.3 + 0.05).astype(np.float16)
+    meth = PolarQuantMoEMethod(128, b13, b2)
+    layer = torch.nn.Module()
+    meth.create_weights(layer, e, hdim, inter, torch.float16)
+    layer.to(DEV)
+    layer.w13_codes.copy_(to_dev(c13))
+    layer.w13_norms.copy_(to_dev(n13))
+    layer.w2_codes.copy_(to_dev(c2))
+    layer.w2_norms.copy_(to_dev(n2))
+    meth.process_weights_after_loading(layer)
+    oracle_w = ((c13, n13, O.ct_scaled(b13)), (c2, n2, O.ct_scaled(b2)))
+    return meth, layer, oracle_w
+
+
+@pytest.mark.parametrize("t,e,hdim,inter,k,b13,b2", [
+    (128, 64, 2048, 1408, 8, 3, 4),   # the MoE config of BASELINE (C5)
+    (5, 8, 256, 200, 2, 3, 4),        # I not a multiple of 128 (zero-padded h)
+    (80, 4, 256, 256, 2, 4, 5),       # ~40 tokens per expert: several passes
+    (3, 16, 512, 384, 1, 5, 6),       # most experts empty; int8 experts
+])
+def test_moe_forward_matches_oracle(t, e, hdim, inter, k, b13, b2):
+    _say(f"moe forward t={t} e={e} h={hdim} i={inter} k={k} q{b13}/q{b2}")
+    rng = np.random.default_rng(t + e + hdim)
+    meth, layer, (w13, w2) = _moe_layer(rng, e, hdim, inter, b13, b2)
+    x = O.seeded_normal((t, hdim), 1.0, 72)
+    logits = O.seeded_normal((t, e), 1.0, 73, np.float32)
+    y = meth.apply(layer, to_dev(x), to_dev(logits), k, True)
+    w_ref, ids_ref = O.moe_route(logits, k, True)
+    want = O.moe_forward(x, w_ref, ids_ref, w13, w2).astype(np.float32)
+    assert y.shape == (t, hdim) and y.dtype == torch.float16
+    check_close(y.float().cpu().numpy(), want, f"moe t={t} e={e}")
+    y2 = meth.apply(layer, to_dev(x), to_dev(logits), k, True)
+    assert torch.equal(y, y2), "moe forward not deterministic"
