@@ -66,6 +66,34 @@ __device__ __forceinline__ uint16_t f2bf_bits(float f) {
   return (uint16_t)(u >> 16);
 }
 
+// Raw LDS access by byte address. The kernels of this library declare no
+// static LDS, so their dynamic LDS block starts at address 0 and a table
+// address built by v_perm is used as is (no base add per lookup).
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
+typedef __attribute__((address_space(3))) u32x4v lds_u32x4;
+__device__ __forceinline__ uint32_t lds_ld32(uint32_t addr) {
+  return *reinterpret_cast<const lds_u32*>(static_cast<uintptr_t>(addr));
+}
+__device__ __forceinline__ void lds_st128(uint32_t addr, u32x4v v) {
+  *reinterpret_cast<lds_u32x4*>(static_cast<uintptr_t>(addr)) = v;
+}
+__device__ __forceinline__ void lds_st32(uint32_t addr, uint32_t v) {
+  *reinterpret_cast<lds_u32*>(static_cast<uintptr_t>(addr)) = v;
+}
+__device__ __forceinline__ u32x4v lds_ld128(uint32_t addr) {
+  return *reinterpret_cast<const lds_u32x4*>(static_cast<uintptr_t>(addr));
+}
+
+// 16 bytes per lane from global memory straight into LDS (gfx950
+// global_load_lds_dwordx4, no VGPRs): lane i's bytes land at lds_addr + 16 i,
+// lds_addr wave-uniform. Counted by vmcnt like any other global load.
+typedef __attribute__((address_space(1))) void glb_void;
+typedef __attribute__((address_space(3))) void lds_void;
+__device__ __forceinline__ void g2lds16(const void* src, uint32_t lds_addr) {
+  __builtin_amdgcn_global_load_lds((const glb_void*)src,
+                                   (lds_void*)(static_cast<uintptr_t>(lds_addr)), 16, 0, 0);
+}
+
 // LDS table address for code byte `b` (0..3) of dword `w`: (byte << 8) | lane4.
 // v_perm_b32 picks byte 0 from src1 (= lane4 < 256) and byte 1 from byte b of
 // src0 (= w); bytes 2-3 are zero (selector 0x0c).
@@ -75,13 +103,40 @@ __device__ __forceinline__ uint32_t tbl_addr(uint32_t w, uint32_t lane4) {
 }
 
 // ---------------------------------------------------------------------------
-// wave-level reductions (wave64)
+// Cross-lane moves inside 16-lane rows without LDS data traffic: DPP
+// quad_perm for lane xor 1 / xor 2, DPP row_ror:8 for xor 8 (rotating a
+// 16-lane row by 8 swaps its halves), ds_swizzle bit mode for xor 4.
 // ---------------------------------------------------------------------------
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+  const int i = __builtin_bit_cast(int, v);
+  int r;
+  if constexpr (M == 1) r = __builtin_amdgcn_mov_dpp(i, 0xB1, 0xF, 0xF, false);       // quad_perm [1,0,3,2]
+  else if constexpr (M == 2) r = __builtin_amdgcn_mov_dpp(i, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  else if constexpr (M == 8) r = __builtin_amdgcn_mov_dpp(i, 0x128, 0xF, 0xF, false); // row_ror:8
+  else r = __builtin_amdgcn_ds_swizzle(i, (M << 10) | 0x1F);                          // and 0x1f, xor M
+  return __builtin_bit_cast(float, r);
+}
 
+// Sum over the 64 lanes, result in every lane: shuffles (LDS crossbar).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
   return v;
+}
+
+// Sum over the 64 lanes, wave-uniform result: DPP/swizzle inside 16-lane
+// rows, then the four row sums through readlane (no LDS round trips).
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += lane_xor<1>(v);
+  v += lane_xor<2>(v);
+  v += lane_xor<4>(v);
+  v += lane_xor<8>(v);
+  const int b = __builtin_bit_cast(int, v);
+  return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
+         (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
 }
 
 // ---------------------------------------------------------------------------
@@ -89,6 +144,15 @@ __device__ __forceinline__ float wave_sum(float v) {
 // (positions 8q..8q+7, q = lane & 15). Stages 1, 2, 4 are in-lane, 8..64 use
 // lane xor 1, 2, 4, 8. Result is scaled by 1/sqrt(128).
 // ---------------------------------------------------------------------------
+template <int M>
+__device__ __forceinline__ void fwht_xstage(float v[8], int q) {
+  const bool upper = (q & M) != 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float o = lane_xor<M>(v[i]);
+    v[i] = upper ? (o - v[i]) : (v[i] + o);
+  }
+}
 
 __device__ __forceinline__ void fwht128_group16(float v[8], int q) {
 #pragma unroll
@@ -102,55 +166,66 @@ __device__ __forceinline__ void fwht128_group16(float v[8], int q) {
       }
     }
   }
-#pragma unroll
-  for (int m = 1; m < 16; m <<= 1) {
-    const bool upper = (q & m) != 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float o = __shfl_xor(v[i], m, 64);
-      v[i] = upper ? (o - v[i]) : (v[i] + o);
-    }
-  }
+  fwht_xstage<1>(v, q);
+  fwht_xstage<2>(v, q);
+  fwht_xstage<4>(v, q);
+  fwht_xstage<8>(v, q);
 #pragma unroll
   for (int i = 0; i < 8; ++i) v[i] *= kInvSqrt128;
 }
 
 // ---------------------------------------------------------------------------
 // Per-lane replicated codebook table in LDS: dword e*64 + lane holds entry e.
-// The codebook is read from global memory once per lane (lane j keeps
-// ct[j + 64 i]) and broadcast with v_readlane, so filling the table issues
-// no dependent global loads.
 //   TBL_NIB_H2: entry e = half2(ct[e & 15], ct[e >> 4]) (nibble byte e)
 //   TBL_F16   : entry e = fp16 bits of ct[e] in the low half
 //   TBL_F32   : entry e = ct[e]
+// Lane j first loads ct[j + 64 i] (one global load per lane); each thread then
+// writes four lane copies of one entry per ds_write_b128, the entry value
+// fetched from the owning lane with ds_bpermute.
 // ---------------------------------------------------------------------------
 enum { TBL_NIB_H2 = 0, TBL_F16 = 1, TBL_F32 = 2 };
 
-__device__ __forceinline__ float bcast_lane(float v, int src_lane) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src_lane));
+// Lane j keeps ct[j + 64 i] (i < 4; zero past n_levels).
+__device__ __forceinline__ void codebook_regs(float (&c)[4], const float* __restrict__ ct,
+                                              int n_levels) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c[i] = (lane + 64 * i) < n_levels ? ct[lane + 64 * i] : 0.f;
 }
 
 template <int KIND>
-__device__ __forceinline__ void fill_codebook(uint32_t* tbl, const float* __restrict__ ct,
-                                              int n_levels, int entries, int nwaves) {
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  float c[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) c[i] = (lane + 64 * i) < n_levels ? ct[lane + 64 * i] : 0.f;
-  for (int e = wave; e < entries; e += nwaves) {
+__device__ __forceinline__ void fill_codebook_from(uint32_t tbl_off, const float (&c)[4],
+                                                   int entries, int nwaves) {
+  const int nthreads = nwaves * 64;
+  const int total16 = entries * 16;  // 16-byte stores: 16 per entry (64 lanes x 4 B)
+  // wave-uniform trip count: every lane of the wave takes part in ds_bpermute
+  // (a source lane must be active), only the store is predicated
+  for (int d0 = threadIdx.x & ~63; d0 < total16; d0 += nthreads) {
+    const int d = d0 + (threadIdx.x & 63);
+    const int e = d >> 4;
     uint32_t v;
     if constexpr (KIND == TBL_NIB_H2) {
-      const int lo = e & 15, hi = e >> 4;  // n_levels <= 16: both in c[0]
-      v = pack_h2(bcast_lane(c[0], lo), bcast_lane(c[0], hi));
+      const int lo = e & 15, hi = e >> 4;  // n_levels <= 16: both held in c[0]
+      const int c0 = __builtin_bit_cast(int, c[0]);
+      v = pack_h2(__builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(lo << 2, c0)),
+                  __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(hi << 2, c0)));
     } else {
       const int q = e >> 6, r = e & 63;
       const float src = q == 0 ? c[0] : q == 1 ? c[1] : q == 2 ? c[2] : c[3];
-      const float val = bcast_lane(src, r);
+      const float val = __builtin_bit_cast(
+          float, __builtin_amdgcn_ds_bpermute(r << 2, __builtin_bit_cast(int, src)));
       v = KIND == TBL_F16 ? (uint32_t)f2h_bits(val) : __builtin_bit_cast(uint32_t, val);
     }
-    tbl[e * 64 + lane] = v;
+    if (d < total16) lds_st128(tbl_off + (uint32_t)d * 16u, u32x4v{v, v, v, v});
   }
+}
+
+template <int KIND>
+__device__ __forceinline__ void fill_codebook(uint32_t tbl_off, const float* __restrict__ ct,
+                                              int n_levels, int entries, int nwaves) {
+  float c[4];
+  codebook_regs(c, ct, n_levels);
+  fill_codebook_from<KIND>(tbl_off, c, entries, nwaves);
 }
 
 // Load 8 consecutive activations as float from a dtype-tagged pointer.

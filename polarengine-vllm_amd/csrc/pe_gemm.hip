@@ -46,19 +46,19 @@ __device__ __forceinline__ half8v dequant_slab(const char* tbl, uint32_t wlo, ui
                                                uint32_t lane4, half2v nrm2) {
   uint32_t p[4];
   if constexpr (NIB) {
-    p[0] = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<0>(wlo, lane4));
-    p[1] = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<1>(wlo, lane4));
-    p[2] = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<2>(wlo, lane4));
-    p[3] = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<3>(wlo, lane4));
+    p[0] = lds_ld32(tbl_addr<0>(wlo, lane4));
+    p[1] = lds_ld32(tbl_addr<1>(wlo, lane4));
+    p[2] = lds_ld32(tbl_addr<2>(wlo, lane4));
+    p[3] = lds_ld32(tbl_addr<3>(wlo, lane4));
   } else {
-    const uint32_t a0 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<0>(wlo, lane4));
-    const uint32_t a1 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<1>(wlo, lane4));
-    const uint32_t a2 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<2>(wlo, lane4));
-    const uint32_t a3 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<3>(wlo, lane4));
-    const uint32_t b0 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<0>(whi, lane4));
-    const uint32_t b1 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<1>(whi, lane4));
-    const uint32_t b2 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<2>(whi, lane4));
-    const uint32_t b3 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<3>(whi, lane4));
+    const uint32_t a0 = lds_ld32(tbl_addr<0>(wlo, lane4));
+    const uint32_t a1 = lds_ld32(tbl_addr<1>(wlo, lane4));
+    const uint32_t a2 = lds_ld32(tbl_addr<2>(wlo, lane4));
+    const uint32_t a3 = lds_ld32(tbl_addr<3>(wlo, lane4));
+    const uint32_t b0 = lds_ld32(tbl_addr<0>(whi, lane4));
+    const uint32_t b1 = lds_ld32(tbl_addr<1>(whi, lane4));
+    const uint32_t b2 = lds_ld32(tbl_addr<2>(whi, lane4));
+    const uint32_t b3 = lds_ld32(tbl_addr<3>(whi, lane4));
     // (lo16 of a, lo16 of b): bytes a0,a1,b0,b1 -> selector 0x05040100 over {b, a}
     p[0] = __builtin_amdgcn_perm(b0, a0, 0x05040100u);
     p[1] = __builtin_amdgcn_perm(b1, a1, 0x05040100u);
@@ -173,8 +173,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(
   const int tm = wid % tiles_m, tn = wid / tiles_m;
   const int m0 = tm * BM, n0 = tn * (2 * TNW * 32);
 
-  if constexpr (NIB) fill_codebook<TBL_NIB_H2>(reinterpret_cast<uint32_t*>(tbl), ct, n_levels, tbl_entries, 4);
-  else fill_codebook<TBL_F16>(reinterpret_cast<uint32_t*>(tbl), ct, n_levels, tbl_entries, 4);
+  if constexpr (NIB) fill_codebook<TBL_NIB_H2>(0, ct, n_levels, tbl_entries, 4);
+  else fill_codebook<TBL_F16>(0, ct, n_levels, tbl_entries, 4);
 
   // A loader: thread t moves uint4 q = t + 256 i (row q >> 3, 16-byte col q & 7)
   const int64_t xrow_u32 = (int64_t)nb * 64;

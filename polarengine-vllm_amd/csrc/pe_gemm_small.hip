@@ -37,19 +37,19 @@ __device__ __forceinline__ half8v dequant_slab_raw(const char* tbl, uint32_t wlo
                                                    uint32_t lane4) {
   uint32_t p[4];
   if constexpr (NIB) {
-    p[0] = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<0>(wlo, lane4));
-    p[1] = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<1>(wlo, lane4));
-    p[2] = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<2>(wlo, lane4));
-    p[3] = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<3>(wlo, lane4));
+    p[0] = lds_ld32(tbl_addr<0>(wlo, lane4));
+    p[1] = lds_ld32(tbl_addr<1>(wlo, lane4));
+    p[2] = lds_ld32(tbl_addr<2>(wlo, lane4));
+    p[3] = lds_ld32(tbl_addr<3>(wlo, lane4));
   } else {
-    const uint32_t a0 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<0>(wlo, lane4));
-    const uint32_t a1 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<1>(wlo, lane4));
-    const uint32_t a2 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<2>(wlo, lane4));
-    const uint32_t a3 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<3>(wlo, lane4));
-    const uint32_t b0 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<0>(whi, lane4));
-    const uint32_t b1 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<1>(whi, lane4));
-    const uint32_t b2 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<2>(whi, lane4));
-    const uint32_t b3 = *reinterpret_cast<const uint32_t*>(tbl + tbl_addr<3>(whi, lane4));
+    const uint32_t a0 = lds_ld32(tbl_addr<0>(wlo, lane4));
+    const uint32_t a1 = lds_ld32(tbl_addr<1>(wlo, lane4));
+    const uint32_t a2 = lds_ld32(tbl_addr<2>(wlo, lane4));
+    const uint32_t a3 = lds_ld32(tbl_addr<3>(wlo, lane4));
+    const uint32_t b0 = lds_ld32(tbl_addr<0>(whi, lane4));
+    const uint32_t b1 = lds_ld32(tbl_addr<1>(whi, lane4));
+    const uint32_t b2 = lds_ld32(tbl_addr<2>(whi, lane4));
+    const uint32_t b3 = lds_ld32(tbl_addr<3>(whi, lane4));
     p[0] = __builtin_amdgcn_perm(b0, a0, 0x05040100u);
     p[1] = __builtin_amdgcn_perm(b1, a1, 0x05040100u);
     p[2] = __builtin_amdgcn_perm(b2, a2, 0x05040100u);
@@ -178,9 +178,9 @@ __global__ __launch_bounds__(kSmallThreads) void gemm_small_kernel(
 
     // codebook table (this LDS also holds the previous pass's reduction)
     if constexpr (NIB)
-      fill_codebook<TBL_NIB_H2>(reinterpret_cast<uint32_t*>(tbl), a.ct, a.n_levels, tbl_entries, kSmallWaves);
+      fill_codebook<TBL_NIB_H2>(0, a.ct, a.n_levels, tbl_entries, kSmallWaves);
     else
-      fill_codebook<TBL_F16>(reinterpret_cast<uint32_t*>(tbl), a.ct, a.n_levels, tbl_entries, kSmallWaves);
+      fill_codebook<TBL_F16>(0, a.ct, a.n_levels, tbl_entries, kSmallWaves);
     __syncthreads();
 
     const uint32_t* arow[MTM];

@@ -38,7 +38,7 @@ __device__ __forceinline__ void stage_block(char* xs, int b, int q, const float 
   if constexpr (NIB) {
     float o[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = __shfl_xor(v[i], 8, 64);
+    for (int i = 0; i < 8; ++i) o[i] = lane_xor<8>(v[i]);
     uint4 w;
     int p0;
     if (q < 8) {
@@ -58,8 +58,63 @@ __device__ __forceinline__ void stage_block(char* xs, int b, int q, const float 
   }
 }
 
+// Dot product of one 16-byte code chunk with the lane's activations: all 16
+// table lookups issue before any is consumed; four independent accumulators.
+template <bool NIB>
+__device__ __forceinline__ float chunk_dot(const uint4& d, uint32_t code_mask, uint32_t lane4,
+                                           const uint32_t (&xr)[16]) {
+  const uint32_t ws[4] = {d.x & code_mask, d.y & code_mask, d.z & code_mask, d.w & code_mask};
+  uint32_t t[16];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    t[4 * j + 0] = lds_ld32(tbl_addr<0>(ws[j], lane4));
+    t[4 * j + 1] = lds_ld32(tbl_addr<1>(ws[j], lane4));
+    t[4 * j + 2] = lds_ld32(tbl_addr<2>(ws[j], lane4));
+    t[4 * j + 3] = lds_ld32(tbl_addr<3>(ws[j], lane4));
+  }
+  float p[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      if constexpr (NIB)
+        p[b] = __builtin_amdgcn_fdot2(as_h2(t[4 * j + b]), as_h2(xr[4 * j + b]), p[b], false);
+      else
+        p[b] = fmaf(__uint_as_float(t[4 * j + b]), __uint_as_float(xr[4 * j + b]), p[b]);
+    }
+  }
+  return (p[0] + p[1]) + (p[2] + p[3]);
+}
+
+// Issue the loads of one batch of U rows (S chunks each) into registers.
+// Straight-line code (no branches), so the compiler can count outstanding
+// loads exactly: rows past N re-read the wave's home row (an L2 hit, never a
+// shared hot row) and chunks past the row end re-read the last chunk; both
+// are masked out at use.
+template <bool NIB, int S, int U>
+__device__ __forceinline__ void issue_rows(uint4 (&d)[U][S], uint16_t (&nbits)[U][S],
+                                           const uint8_t* __restrict__ codes,
+                                           const uint16_t* __restrict__ norms, int home, int gw,
+                                           int tw, int k0, int pass, int N, int nb, int C,
+                                           int lane) {
+  const int row_bytes = NIB ? nb * 64 : nb * kBlock;
+  constexpr int nshift = NIB ? 2 : 3;  // chunk -> block
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    int n = gw + (k0 + u) * tw;
+    n = n < N ? n : home;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      int c = (pass * S + s) * 64 + lane;
+      c = c < C ? c : C - 1;
+      d[u][s] = ld_nt16(codes + (size_t)n * row_bytes + (size_t)c * 16);
+      nbits[u][s] = norms[(size_t)n * nb + (c >> nshift)];
+    }
+  }
+}
+
 // XREG: the lane's activation slice lives in registers (S chunks); otherwise
-// it is re-read from LDS per chunk (large K, S = 1 per pass over the row).
+// it is re-read from LDS per chunk (large K, several passes over the row).
 template <bool NIB, int S, int U, int XM, int OM, bool XREG = true>
 __global__ __launch_bounds__(kGemvThreads) void gemv1_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
@@ -68,56 +123,94 @@ __global__ __launch_bounds__(kGemvThreads) void gemv1_kernel(
     int N, int nb) {
   extern __shared__ uint4 smem4[];
   char* smem = reinterpret_cast<char*>(smem4);
-  uint32_t* tbl = reinterpret_cast<uint32_t*>(smem);
-  char* xs = smem + tbl_entries * 256;
+  char* xs = smem + tbl_entries * 256;  // the table occupies [0, tbl_entries * 256)
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   constexpr int kWaves = kGemvThreads / 64;
+  constexpr int kGroups = kGemvThreads / 16;
   const int row_bytes = NIB ? nb * 64 : nb * kBlock;
   const int C = row_bytes >> 4;  // 16-byte chunks per row
+  const int gw = blockIdx.x * kWaves + wave;
+  const int tw = gridDim.x * kWaves;
+  const int g = tid >> 4, q = tid & 15;
+  const int npass = XREG ? 1 : (C + 64 * S - 1) / (64 * S);
+
+  // ---- 0. loads, in the order they are needed: the codebook, the activation
+  // block of this 16-lane group (FWHT input), then the first batch of weight
+  // rows. Loads complete in order, so the prologue below waits only for the
+  // first two while the weights stream in.
+  float cb[4];
+  codebook_regs(cb, ct, n_levels);
+  // first FWHT input block of this group, kept raw until after the barrier
+  // (block index clamped: groups past nb re-read block 0 and discard it)
+  const int gb = g < nb ? g : 0;
+  u32x4v xraw[XM == XM_XTF_F32 ? 2 : 1];
+  if constexpr (XM == XM_RAW_F16) {
+    xraw[0] = *reinterpret_cast<const u32x4v*>(reinterpret_cast<const uint16_t*>(x) + gb * kBlock + q * 8);
+  } else if constexpr (XM == XM_XTF_F32) {
+    const u32x4v* p = reinterpret_cast<const u32x4v*>(reinterpret_cast<const float*>(x) + gb * kBlock + q * 8);
+    xraw[0] = p[0];
+    xraw[1] = p[1];
+  }
+  __builtin_amdgcn_sched_barrier(0);  // codebook and activation loads go first
+  const int home = gw < N ? gw : N - 1;
+  uint4 d[U][S];
+  uint16_t nbits[U][S];
+  issue_rows<NIB, S, U>(d, nbits, codes, norms, home, gw, tw, 0, 0, N, nb, C, lane);
+  __builtin_amdgcn_sched_barrier(0);
 
   // ---- 1. codebook table, one copy per lane -------------------------------
-  if constexpr (NIB) fill_codebook<TBL_NIB_H2>(tbl, ct, n_levels, tbl_entries, kWaves);
-  else fill_codebook<TBL_F32>(tbl, ct, n_levels, tbl_entries, kWaves);
+  if constexpr (NIB) fill_codebook_from<TBL_NIB_H2>(0, cb, tbl_entries, kWaves);
+  else fill_codebook_from<TBL_F32>(0, cb, tbl_entries, kWaves);
 
   // ---- 2. transformed activation into LDS ----------------------------------
-  {
-    const int g = tid >> 4, q = tid & 15;
-    constexpr int kGroups = kGemvThreads / 16;
-    if constexpr (XM == XM_RAW_F16 || XM == XM_XTF_F32) {
-      for (int b = g; b < nb; b += kGroups) {
-        float v[8];
+  if constexpr (XM == XM_RAW_F16 || XM == XM_XTF_F32) {
+    for (int b = g; b < nb; b += kGroups) {
+      float v[8];
+      if (b == g) {
         if constexpr (XM == XM_RAW_F16) {
-          load8<PE_DTYPE_F16>(reinterpret_cast<const uint16_t*>(x) + b * kBlock + q * 8, v);
-          fwht128_group16(v, q);
-        } else {
-          load8<PE_DTYPE_F32>(reinterpret_cast<const float*>(x) + b * kBlock + q * 8, v);
-        }
-        stage_block<NIB>(xs, b, q, v);
-      }
-    } else {  // pair f16 input: nb * 64 half2
-      const uint4* src = reinterpret_cast<const uint4*>(x);
-      if constexpr (NIB) {
-        for (int i = tid; i < nb * 16; i += kGemvThreads)
-          reinterpret_cast<uint4*>(xs)[i] = src[i];
-      } else {
-        // pairs p..p+3 of block b -> x[p..p+3] and x[p+64..p+67]
-        for (int i = tid; i < nb * 16; i += kGemvThreads) {
-          const uint4 w = src[i];
-          const int b = i >> 4, p = (i & 15) * 4;
-          const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-          float lo[4], hi[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            lo[j] = h2f((uint16_t)(ws[j] & 0xffff));
-            hi[j] = h2f((uint16_t)(ws[j] >> 16));
+          for (int i = 0; i < 4; ++i) {
+            v[2 * i] = h2f((uint16_t)(xraw[0][i] & 0xffff));
+            v[2 * i + 1] = h2f((uint16_t)(xraw[0][i] >> 16));
           }
-          float* d = reinterpret_cast<float*>(xs) + b * kBlock + p;
-          *reinterpret_cast<float4*>(d) = make_float4(lo[0], lo[1], lo[2], lo[3]);
-          *reinterpret_cast<float4*>(d + 64) = make_float4(hi[0], hi[1], hi[2], hi[3]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            v[i] = __uint_as_float(xraw[0][i]);
+            v[4 + i] = __uint_as_float(xraw[XM == XM_XTF_F32 ? 1 : 0][i]);
+          }
         }
+      } else if constexpr (XM == XM_RAW_F16) {
+        load8<PE_DTYPE_F16>(reinterpret_cast<const uint16_t*>(x) + b * kBlock + q * 8, v);
+      } else {
+        load8<PE_DTYPE_F32>(reinterpret_cast<const float*>(x) + b * kBlock + q * 8, v);
+      }
+      if constexpr (XM == XM_RAW_F16) fwht128_group16(v, q);
+      stage_block<NIB>(xs, b, q, v);
+    }
+  } else {  // pair f16 input: nb * 64 half2
+    const uint4* src = reinterpret_cast<const uint4*>(x);
+    if constexpr (NIB) {
+      for (int i = tid; i < nb * 16; i += kGemvThreads)
+        reinterpret_cast<uint4*>(xs)[i] = src[i];
+    } else {
+      // pairs p..p+3 of block b -> x[p..p+3] and x[p+64..p+67]
+      for (int i = tid; i < nb * 16; i += kGemvThreads) {
+        const uint4 w = src[i];
+        const int b = i >> 4, p = (i & 15) * 4;
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+        float lo[4], hi[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          lo[j] = h2f((uint16_t)(ws[j] & 0xffff));
+          hi[j] = h2f((uint16_t)(ws[j] >> 16));
+        }
+        float* dst = reinterpret_cast<float*>(xs) + b * kBlock + p;
+        *reinterpret_cast<float4*>(dst) = make_float4(lo[0], lo[1], lo[2], lo[3]);
+        *reinterpret_cast<float4*>(dst + 64) = make_float4(hi[0], hi[1], hi[2], hi[3]);
       }
     }
   }
@@ -128,7 +221,6 @@ __global__ __launch_bounds__(kGemvThreads) void gemv1_kernel(
   // c>>2, pairs 16*(c&3)..+15; int8 chunk c: block c>>3, positions
   // 16*(c&7)..+15. With XREG there is one pass and the slice is loaded once;
   // otherwise (large K) each pass re-reads its slice from LDS.
-  const int npass = XREG ? 1 : (C + 64 * S - 1) / (64 * S);
   uint32_t xr[S][16];
   auto load_x = [&](int pass) {
 #pragma unroll
@@ -151,87 +243,40 @@ __global__ __launch_bounds__(kGemvThreads) void gemv1_kernel(
   if constexpr (XREG) load_x(0);
 
   // ---- 4. stream rows --------------------------------------------------------
-  const uint32_t lane4 = (uint32_t)lane << 2;
-  const int gw = blockIdx.x * kWaves + wave;
-  const int tw = gridDim.x * kWaves;
-  const int nshift = NIB ? 2 : 3;  // chunk -> block
-
   // rows gw, gw + tw, gw + 2 tw, ... (balanced to +-1 row per wave), U at a
-  // time. All U*S loads of a batch issue back to back (raw norm bits; no use
-  // before the scheduling barrier); rows past N are skipped (wave-uniform),
-  // chunks past the row end re-read the last chunk and get a zero norm.
+  // time; the first batch (pass 0) was issued before the prologue.
+  const uint32_t lane4 = (uint32_t)lane << 2;
   for (int k0 = 0; gw + k0 * tw < N; k0 += U) {
     float acc[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) acc[u] = 0.f;
     for (int pass = 0; pass < npass; ++pass) {
       if constexpr (!XREG) load_x(pass);
-      uint4 d[U][S];
-      uint16_t nbits[U][S];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int n = gw + (k0 + u) * tw;
-        if (n < N) {
-#pragma unroll
-          for (int s = 0; s < S; ++s) {
-            int c = (pass * S + s) * 64 + lane;
-            c = c < C ? c : C - 1;
-            d[u][s] = ld_nt16(codes + (size_t)n * row_bytes + (size_t)c * 16);
-            nbits[u][s] = norms[(size_t)n * nb + (c >> nshift)];
-          }
-        } else {
-#pragma unroll
-          for (int s = 0; s < S; ++s) {
-            d[u][s] = make_uint4(0, 0, 0, 0);
-            nbits[u][s] = 0;
-          }
-        }
+      if (k0 != 0 || pass != 0) {
+        issue_rows<NIB, S, U>(d, nbits, codes, norms, home, gw, tw, k0, pass, N, nb, C, lane);
+        // keep every load of this batch ahead of the arithmetic: otherwise the
+        // scheduler sinks the norm loads to their uses, one round trip each
+        __builtin_amdgcn_sched_barrier(0);
       }
-      // keep every load of this batch ahead of the arithmetic: otherwise the
-      // scheduler sinks the norm loads to their uses, one round trip each
-      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int u = 0; u < U; ++u) {
+        if (gw + (k0 + u) * tw >= N) continue;  // wave-uniform
         float a = acc[u];
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-          const bool live = gw + (k0 + u) * tw < N && (pass * S + s) * 64 + lane < C;
+          const bool live = (pass * S + s) * 64 + lane < C;
           const float nrm = live ? h2f(nbits[u][s]) : 0.f;
-          const uint32_t ws[4] = {d[u][s].x & code_mask, d[u][s].y & code_mask,
-                                  d[u][s].z & code_mask, d[u][s].w & code_mask};
-          float part = 0.f;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const uint32_t t0 = *reinterpret_cast<const uint32_t*>(smem + tbl_addr<0>(ws[j], lane4));
-            const uint32_t t1 = *reinterpret_cast<const uint32_t*>(smem + tbl_addr<1>(ws[j], lane4));
-            const uint32_t t2 = *reinterpret_cast<const uint32_t*>(smem + tbl_addr<2>(ws[j], lane4));
-            const uint32_t t3 = *reinterpret_cast<const uint32_t*>(smem + tbl_addr<3>(ws[j], lane4));
-            if constexpr (NIB) {
-              part = __builtin_amdgcn_fdot2(as_h2(t0), as_h2(xr[s][4 * j + 0]), part, false);
-              part = __builtin_amdgcn_fdot2(as_h2(t1), as_h2(xr[s][4 * j + 1]), part, false);
-              part = __builtin_amdgcn_fdot2(as_h2(t2), as_h2(xr[s][4 * j + 2]), part, false);
-              part = __builtin_amdgcn_fdot2(as_h2(t3), as_h2(xr[s][4 * j + 3]), part, false);
-            } else {
-              part = fmaf(__uint_as_float(t0), __uint_as_float(xr[s][4 * j + 0]), part);
-              part = fmaf(__uint_as_float(t1), __uint_as_float(xr[s][4 * j + 1]), part);
-              part = fmaf(__uint_as_float(t2), __uint_as_float(xr[s][4 * j + 2]), part);
-              part = fmaf(__uint_as_float(t3), __uint_as_float(xr[s][4 * j + 3]), part);
-            }
-          }
-          a = fmaf(part, nrm, a);
+          a = fmaf(chunk_dot<NIB>(d[u][s], code_mask, lane4, xr[s]), nrm, a);
         }
         acc[u] = a;
       }
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) acc[u] = wave_sum(acc[u]);
-    if (lane < U) {
-      float r = acc[0];
-#pragma unroll
-      for (int u = 1; u < U; ++u)
-        if (lane == u) r = acc[u];
-      const int n = gw + (k0 + lane) * tw;
-      if (n < N) {
+    for (int u = 0; u < U; ++u) {
+      const int n = gw + (k0 + u) * tw;
+      if (n >= N) continue;  // wave-uniform
+      const float r = wave_sum_dpp(acc[u]);
+      if (lane == 0) {
         if constexpr (OM == OM_F32) {
           reinterpret_cast<float*>(y)[n] = r;
         } else {
@@ -281,7 +326,6 @@ static int launch_gemv1(const Gemv1Args& a, hipStream_t st) {
   if (C <= 128) return launch_gemv1_s<NIB, 2, XM, OM, true>(a, st);
   if (C <= 192) return launch_gemv1_s<NIB, 3, XM, OM, true>(a, st);
   if (C <= 256) return launch_gemv1_s<NIB, 4, XM, OM, true>(a, st);
-  if (C <= 384) return launch_gemv1_s<NIB, 6, XM, OM, true>(a, st);
   if (C <= 512) return launch_gemv1_s<NIB, 8, XM, OM, true>(a, st);
   // large K: activations stay in LDS, four chunks per lane per pass
   return launch_gemv1_s<NIB, 4, XM, OM, false>(a, st);

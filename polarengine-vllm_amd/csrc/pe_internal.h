@@ -62,9 +62,22 @@ struct SmallArgs {
 // pe_gemm_small.hip: M <= kSmallMaxRows per pass is cheapest (larger M loops)
 constexpr int kSmallMaxRows = 64;
 int gemm_small(bool nibble, int epilogue, const SmallArgs& a, int groups, hipStream_t st);
-// same, with A read from fp32 natural-layout rows (already transformed) and
-// fp32 output: the reference API's GEMV beyond the register kernel's K
-int gemm_small_xf32(bool nibble, const SmallArgs& a, hipStream_t st);
+
+// pe_gemv_mfma.hip: decode GEMV, 1 <= M <= 16, fp16 out (+ fp16 bias)
+struct DecArgs {
+  const uint8_t* codes;
+  const uint16_t* norms;
+  const float* ct;
+  int n_levels;
+  const void* x;   // raw fp16 rows (xraw) or pair-f16 x_tf rows
+  int64_t ldx;     // row stride of x in fp16 elements
+  void* y;
+  int64_t ldy;     // row stride of y in fp16 elements
+  const uint16_t* bias;
+  int M, N, nb;
+};
+bool gemv_mfma_fits(bool nibble, int M, int nb, int n_levels);
+int gemv_mfma(bool nibble, bool xraw, const DecArgs& a, hipStream_t st);
 
 // pe_gemm.hip
 int gemm(bool nibble, int omode, const GemmArgs& a, hipStream_t st);

@@ -3,9 +3,11 @@
 // (polar_matmul, kernels/polar_gemm.py:425-534).
 //
 // Routing by M (rows of the activation):
-//   M == 1            -> gemv1: register-resident M=1 decode GEMV, FWHT fused
+//   M <= 16 (when x fits in LDS beside the codebook table)
+//                     -> gemv_mfma: decode GEMV on 16x16x32 MFMA, FWHT fused
 //                        into its prologue (one launch per linear);
-//   2 <= M <= kSmallM -> FWHT-128 to pair-f16 x_tf, then the small-M MFMA
+//   M == 1 otherwise  -> gemv1 (register-resident dot2 GEMV, LDS activations);
+//   2 <= M <= 64      -> FWHT-128 to pair-f16 x_tf, then the small-M MFMA
 //                        kernel (16x16x32 f16, K split across waves);
 //   M >  kSmallM      -> FWHT-128 to pair-f16 x_tf, then the prefill GEMM
 //                        (32x32x16 f16 MFMA, LDS A tiles, dequantized B).
@@ -58,10 +60,11 @@ extern "C" int pe_linear_forward_xtf(const void* x_tf_pair, int64_t M, int in_f_
   if (!aligned16(x_tf_pair) || !aligned16(codes)) return PE_ERR_ALIGN;
   if (M == 0) return PE_OK;
   const int nb = in_f_padded / kBlock;
-  if (M == 1 && in_f_padded <= gemv1_max_kp(nib)) {
-    Gemv1Args a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels,
-                x_tf_pair, y, reinterpret_cast<const uint16_t*>(bias), out_f, nb};
-    return gemv1(nib, XM_PAIR_F16, OM_F16, a, st);
+  if (M <= 16 && gemv_mfma_fits(nib, (int)M, nb, n_levels)) {
+    DecArgs a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels,
+              x_tf_pair, (int64_t)in_f_padded, y, out_f, reinterpret_cast<const uint16_t*>(bias),
+              (int)M, out_f, nb};
+    return gemv_mfma(nib, false, a, st);
   }
   return mm_xtf(nib, codes, norms_f16, ct_scaled, n_levels, x_tf_pair, M, out_f, nb, y, OM_F16,
                 out_f, reinterpret_cast<const uint16_t*>(bias), workspace, workspace_bytes, st);
@@ -84,6 +87,11 @@ extern "C" int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f
   if (!aligned16(x) || !aligned16(codes) || (ldx * 2) % 16) return PE_ERR_ALIGN;
   if (M == 0) return PE_OK;
   const int nb = in_f / kBlock;
+  if (M <= 16 && gemv_mfma_fits(nib, (int)M, nb, n_levels)) {
+    DecArgs a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels, x, ldx, y,
+              out_f, reinterpret_cast<const uint16_t*>(bias), (int)M, out_f, nb};
+    return gemv_mfma(nib, true, a, st);
+  }
   if (M == 1 && in_f <= gemv1_max_kp(nib)) {
     Gemv1Args a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels, x, y,
                 reinterpret_cast<const uint16_t*>(bias), out_f, nb};

@@ -201,6 +201,113 @@ def test_linear_forward_m1(n, k, bits):
 
 
 # ---------------------------------------------------------------------------
+# Decode (M <= 16): MFMA decode GEMV with the FWHT fused (raw fp16 rows) or
+# fed pair-f16 x_tf; shapes with nb < 8 (idle waves), ragged N, row stride
+# ldx > in_f, every bit width, and M past the LDS limit (FWHT + small GEMM)
+# ---------------------------------------------------------------------------
+
+def pair_f16(x_tf):
+    """[M, K] -> pair-f16 rows as uint32 [M, K/2]: (x[128b+p], x[128b+64+p])."""
+    m, k = x_tf.shape
+    h = np.ascontiguousarray(
+        x_tf.astype(np.float16).reshape(m, k // 128, 2, 64).transpose(0, 1, 3, 2))
+    return h.view(np.uint32).reshape(m, k // 2)
+
+
+DECODE_CASES = [(1, 12288, 4096, 4), (1, 4096, 4096, 5), (2, 1000, 1408, 3),
+                (3, 4096, 12288, 4), (4, 257, 384, 2), (5, 96, 640, 8), (7, 2816, 2048, 6),
+                (8, 12288, 4096, 4), (12, 333, 1024, 7), (16, 4096, 2048, 4),
+                (16, 1536, 1536, 5), (16, 4096, 4096, 4), (1, 512, 20480, 4),
+                (1, 64, 128, 3), (2, 48, 256, 8)]
+
+
+@pytest.mark.parametrize("m,n,k,bits", DECODE_CASES)
+def test_decode_linear_forward(m, n, k, bits):
+    from polarengine_vllm import _lib
+    _say(f"decode m={m} n={n} k={k} bits={bits}")
+    rng = np.random.default_rng(m * 1000 + n + k + bits)
+    codes, norms, ct = rand_layer(rng, n, k, bits)
+    x = O.seeded_normal((m, k), 1.0, 50 + m)
+    bias = O.seeded_normal((n,), 0.1, 51)
+    want = O.linear_apply(x, codes, norms, ct, k, bias).astype(np.float32)
+    dcodes, nib = dev_codes(codes, bits)
+    ldx = k + 64  # rows of a wider buffer
+    xb = np.zeros((m, ldx), dtype=np.float16)
+    xb[:, :k] = x
+    xd, nd, cd, bd = to_dev(xb), to_dev(norms), to_dev(ct), to_dev(bias)
+    L = _lib.lib()
+    wsb = L.pe_linear_workspace_size(m, k, n, bits, int(nib))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+    outs = []
+    for _ in range(2):
+        y = torch.empty(m, n, dtype=torch.float16, device=DEV)
+        rc = L.pe_linear_forward(xd.data_ptr(), 0, m, k, ldx, dcodes.data_ptr(), bits, int(nib),
+                                 nd.data_ptr(), cd.data_ptr(), 1 << bits, bd.data_ptr(),
+                                 y.data_ptr(), n, ws.data_ptr(), wsb,
+                                 _lib.stream_ptr(torch.device(DEV)))
+        torch.cuda.synchronize()
+        _lib.check(rc, "pe_linear_forward")
+        outs.append(y)
+    check_close(outs[0].float().cpu().numpy(), want, f"decode {m}x{n}x{k} q{bits}")
+    assert torch.equal(outs[0], outs[1]), "non-deterministic"
+
+
+@pytest.mark.parametrize("m,n,k,bits", [(1, 12288, 4096, 4), (4, 1000, 1408, 3),
+                                        (16, 2048, 2048, 5), (9, 200, 384, 8)])
+def test_decode_linear_forward_xtf(m, n, k, bits):
+    """Pair-f16 x_tf given (the QKV-shared transform): pe_linear_forward_xtf."""
+    from polarengine_vllm import _lib
+    _say(f"decode xtf m={m} n={n} k={k} bits={bits}")
+    rng = np.random.default_rng(m + n + k + bits + 7)
+    codes, norms, ct = rand_layer(rng, n, k, bits)
+    x = O.seeded_normal((m, k), 1.0, 60 + m)
+    x_tf = O.fwht_blocks(x.astype(np.float32)).astype(np.float16)
+    want = O.hadamard_domain_matmul(codes, norms, ct, x_tf.astype(np.float32))
+    dcodes, nib = dev_codes(codes, bits)
+    xp, nd, cd = to_dev(pair_f16(x_tf)), to_dev(norms), to_dev(ct)
+    L = _lib.lib()
+    wsb = L.pe_linear_xtf_workspace_size(m, k, n, bits, int(nib))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+    y = torch.empty(m, n, dtype=torch.float16, device=DEV)
+    rc = L.pe_linear_forward_xtf(xp.data_ptr(), m, k, dcodes.data_ptr(), bits, int(nib),
+                                 nd.data_ptr(), cd.data_ptr(), 1 << bits, None, 0,
+                                 y.data_ptr(), n, ws.data_ptr(), wsb,
+                                 _lib.stream_ptr(torch.device(DEV)))
+    torch.cuda.synchronize()
+    _lib.check(rc, "pe_linear_forward_xtf")
+    check_close(y.float().cpu().numpy(), want.astype(np.float32), f"decode xtf {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+def test_decode_indexing_probe_bit_exact(bits):
+    """One-hot pair-f16 rows, unit norms: y[m, n] = fp16(ct)[code[n, k_m]] exactly."""
+    from polarengine_vllm import _lib
+    _say(f"decode indexing probe bits={bits}")
+    rng = np.random.default_rng(12 + bits)
+    m, n, kp = 5, 80, 1024
+    codes, _, ct = rand_layer(rng, n, kp, bits)
+    norms = np.ones((n, kp // 128), dtype=np.float16)
+    dcodes, nib = dev_codes(codes, bits)
+    ct16 = ct.astype(np.float16)
+    nd, cd = to_dev(norms), to_dev(ct)
+    L = _lib.lib()
+    ks = [0, 1, 15, 16, 17, 63, 64, 65, 100, 127, 133, 448, 575, 700, kp - 1]
+    for c in range(0, len(ks), m):
+        sel = (ks[c:c + m] + ks[:m])[:m]
+        x_tf = np.zeros((m, kp), dtype=np.float16)
+        x_tf[np.arange(m), sel] = 1.0
+        xp = to_dev(pair_f16(x_tf))
+        y = torch.empty(m, n, dtype=torch.float16, device=DEV)
+        rc = L.pe_linear_forward_xtf(xp.data_ptr(), m, kp, dcodes.data_ptr(), bits, int(nib),
+                                     nd.data_ptr(), cd.data_ptr(), 1 << bits, None, 0,
+                                     y.data_ptr(), n, None, 0, _lib.stream_ptr(torch.device(DEV)))
+        torch.cuda.synchronize()
+        _lib.check(rc, "pe_linear_forward_xtf")
+        want = np.stack([ct16[codes[:, k].view(np.uint8).astype(np.int64)] for k in sel])
+        assert np.array_equal(y.cpu().numpy(), want), f"k={sel}"
+
+
+# ---------------------------------------------------------------------------
 # Batched (M > 1): reference API polar_matmul (f32 out) and the MFMA GEMM
 # ---------------------------------------------------------------------------
 
