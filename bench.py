@@ -155,6 +155,58 @@ def cpu_baseline(budget_s=15.0):
                       f"Q4 {n}x{k} M=1, {calls} calls in {budget_s:.0f} s"}
 
 
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic_gemv_q4_12288x4096_m1.json")
+COPY_BYTES = 256 << 20
+
+
+def profile_traffic(dev):
+    """Workload for the two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE):
+    the headline call over the rotating copies, then a plain device copy of
+    COPY_BYTES whose counter reading calibrates the KiB units."""
+    n, k, bits, m = 12288, 4096, 4, 1
+    x = torch.randn(m, k, device=dev, dtype=torch.float16)
+    layers = [Linear(n, k, bits, m, dev, seed=100 + i, x=x) for i in range(N_COPIES)]
+    for _ in range(4):
+        for c in layers:
+            c()
+    # plain copy kernel of known traffic: reads and writes COPY_BYTES once
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize(dev)
+
+
+def summarize_pmc(fetch_csv, write_csv):
+    """HBM bytes per launch of the headline kernel from the two pmc passes,
+    each counter scaled by (known copy bytes / the copy kernel's reading)."""
+    import csv
+
+    def per_kernel(path, counter):
+        vals = {}
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] != counter:
+                continue
+            vals.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+        return vals
+
+    out = {}
+    for path, counter in ((fetch_csv, "FETCH_SIZE"), (write_csv, "WRITE_SIZE")):
+        v = per_kernel(path, counter)
+        gemv = [k for k in v if "gemv_mfma_kernel" in k or "gemv1_kernel" in k]
+        copy = [k for k in v if "neg_kernel" in k]
+        if not gemv or not copy:
+            raise SystemExit(f"{path}: kernels not found: {list(v)[:6]}")
+        kg, kc = gemv[0], copy[0]
+        scale = COPY_BYTES / (np.median(v[kc]) * 1024.0)
+        out[counter] = {"kernel": kg, "kib_per_launch": float(np.median(v[kg])),
+                        "copy_kernel": kc, "copy_kib": float(np.median(v[kc])),
+                        "scale": float(scale),
+                        "bytes_per_launch": float(np.median(v[kg]) * 1024.0 * scale)}
+    out["traffic_bytes"] = out["FETCH_SIZE"]["bytes_per_launch"] + out["WRITE_SIZE"]["bytes_per_launch"]
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -162,7 +214,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--profile-traffic", action="store_true",
+                    help="run only the workload of the FETCH_SIZE / WRITE_SIZE pmc passes")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="print the traffic JSON from the two pmc passes and exit")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        print(json.dumps(summarize_pmc(*args.summarize_pmc), indent=1))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build's hot path is a single-GPU kernel "
               "(multi-GPU sharding is design-only); run with --gpus 1", file=sys.stderr)
@@ -170,6 +229,9 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     _lib.lib()
+    if args.profile_traffic:
+        profile_traffic(dev)
+        return
 
     n, k, bits, m = 12288, 4096, 4, 1
     x = torch.randn(m, k, device=dev, dtype=torch.float16)
@@ -199,6 +261,10 @@ def main():
                              "note": "one weight copy, Infinity-Cache resident"}
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    traffic = None  # HBM bytes per launch from the committed pmc summary, if any
+    if os.path.exists(TRAFFIC_JSON):
+        with open(TRAFFIC_JSON) as f:
+            traffic = round(json.load(f)["traffic_bytes"])
     out = {
         "metric": "HBM GB/s + us/call, Q4 GEMV 12288x4096 M=1; prefill GEMM TFLOPS M=2048",
         "value": round(gbs, 1),
@@ -211,14 +277,15 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16 operands, fp32 accumulate (codes u4, norms f16)",
+        "dtype": "f16",
         "data": "synthetic: random nibble codes, |N| fp16 norms, Lloyd-Max Q4 codebook, "
-                "x ~ N(0,1) fp16",
+                "x ~ N(0,1) fp16; f16 MFMA operands, fp32 accumulate",
         "config": {"workload": "decode linear Q4 12288x4096 M=1 (FWHT fused + nibble GEMV), "
                                f"{N_COPIES} rotating weight copies",
                    "M": m, "N": n, "K": k, "bits": bits, "algorithmic_bytes": B},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic},
         "cpu_baseline": cpu,
         "extra": extra,
     }
