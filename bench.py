@@ -59,12 +59,17 @@ def make_layer(n, k, bits, dev, seed):
 
 
 class Linear:
-    """Direct C-ABI call with preallocated buffers (what apply() launches)."""
+    """Direct C-ABI call with preallocated buffers and the tiled-16 weight
+    layout (what apply() launches)."""
 
     def __init__(self, n, k, bits, m, dev, seed, x=None):
+        from polarengine_vllm.packing import tile_weights_16
         self.n, self.k, self.bits, self.m = n, k, bits, m
-        self.codes, self.norms, self.ct = make_layer(n, k, bits, dev, seed)
-        self.packed = int(bits <= 4)
+        codes, norms, self.ct = make_layer(n, k, bits, dev, seed)
+        # the runtime layout process_weights_after_loading produces
+        self.codes, self.norms = tile_weights_16(codes, norms)
+        del codes, norms
+        self.packed = (_lib.PE_PACK_NIBBLE if bits <= 4 else 0) | _lib.PE_LAYOUT_TILE16
         self.x = x if x is not None else torch.randn(m, k, device=dev, dtype=torch.float16)
         self.y = torch.empty(m, n, device=dev, dtype=torch.float16)
         L = _lib.lib()

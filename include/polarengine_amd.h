@@ -48,6 +48,13 @@ enum {
   PE_ERR_DEVICE = 8     /* device query failed                                */
 };
 
+/* ---- weight format flags (the `packed` argument of the linear entry points) */
+enum {
+  PE_PACK_NIBBLE = 1,  /* half-block nibble codes (bits 2..4), else int8         */
+  PE_LAYOUT_TILE16 = 2 /* tiled-16 runtime layout from pe_tile_weights, else the
+                          reference's row-major [N, row_bytes] / [N, nb]         */
+};
+
 /* ---- dtype / layout codes ---------------------------------------------- */
 enum { PE_DTYPE_F16 = 0, PE_DTYPE_BF16 = 1, PE_DTYPE_F32 = 2 };
 enum {
@@ -114,7 +121,8 @@ int pe_polar_matmul(const void* codes, int packed, const float* x_tf, int64_t M,
  * (polarengine_vllm/linear_method.py:157-222): pad -> FWHT -> quantized
  * GEMV/GEMM (fp32 accumulate) -> cast -> + bias.
  *   x      : [M, in_f] in x_dtype (PE_DTYPE_F16), row stride ldx
- *   codes  : runtime layout for (bits, packed)
+ *   codes  : runtime layout for (bits, packed); packed = PE_PACK_NIBBLE for
+ *            nibble codes, | PE_LAYOUT_TILE16 for the tiled-16 layout
  *   bias   : NULL or [out_f] in x_dtype
  *   y      : [M, out_f] in x_dtype, row stride out_f
  * Needs pe_linear_workspace_size(...) bytes of workspace (0 is valid when the
@@ -145,6 +153,19 @@ int pe_linear_forward_xtf(const void* x_tf_pair, int64_t M, int in_f_padded,
  * codes int8 [rows, K] -> packed uint8 [rows, K/2]; K % 128 == 0.
  */
 int pe_pack_nibble(const int8_t* codes, uint8_t* packed, int64_t rows, int64_t K, void* stream);
+
+/*
+ * Tiled-16 runtime layout (PE_LAYOUT_TILE16) of one quantized matrix, bit-exact
+ * rearrangement: codes [N, row_bytes] (row_bytes = nb * bpb, bpb = 64 nibble /
+ * 128 int8 bytes per 128-block) -> codes_t [ceil(N/16)][nb][16][bpb], norms
+ * [N, nb] -> norms_t [ceil(N/16)][nb][16]; rows past N are zero. One (16-row
+ * tile, block) is then one contiguous 1-2 KB read for the decode and GEMM
+ * kernels. No reference counterpart: like the nibble packing of
+ * process_weights_after_loading (linear_method.py:243-248), it is a one-time
+ * runtime re-layout of the registered buffers.
+ */
+int pe_tile_weights(const void* codes, const uint16_t* norms, int64_t N, int row_bytes, int nb,
+                    void* codes_t, uint16_t* norms_t, void* stream);
 
 /*
  * On-disk Q5 (LSB-first, 8 codes in 5 bytes) to int8 codes, bit-exact:

@@ -144,14 +144,13 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 // (positions 8q..8q+7, q = lane & 15). Stages 1, 2, 4 are in-lane, 8..64 use
 // lane xor 1, 2, 4, 8. Result is scaled by 1/sqrt(128).
 // ---------------------------------------------------------------------------
+// Butterfly across lanes: lower lane v + o, upper lane o - v, as one fma with
+// a per-lane sign (exact: a product by +-1 rounds nothing).
 template <int M>
 __device__ __forceinline__ void fwht_xstage(float v[8], int q) {
-  const bool upper = (q & M) != 0;
+  const float sgn = (q & M) ? -1.f : 1.f;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float o = lane_xor<M>(v[i]);
-    v[i] = upper ? (o - v[i]) : (v[i] + o);
-  }
+  for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(sgn, v[i], lane_xor<M>(v[i]));
 }
 
 __device__ __forceinline__ void fwht128_group16(float v[8], int q) {

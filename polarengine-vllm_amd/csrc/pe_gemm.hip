@@ -85,17 +85,15 @@ struct BTile {
 
 template <bool NIB, int TNW>
 __device__ __forceinline__ void load_btile(BTile<NIB, TNW>& t, const uint8_t* const (&b_row)[TNW],
-                                           const uint16_t* const (&n_row)[TNW], int kt) {
+                                           const uint16_t* const (&n_row)[TNW], int kt,
+                                           int64_t c_blk, int64_t n_blk) {
   const int b = kt >> 1, half = kt & 1;
 #pragma unroll
   for (int j = 0; j < TNW; ++j) {
-    if constexpr (NIB) {
-      t.lo[j] = ld_nt16v(b_row[j] + b * 64 + half * 32);
-    } else {
-      t.lo[j] = ld_nt16v(b_row[j] + b * kBlock + half * 32);
-      t.hi[j] = ld_nt16v(b_row[j] + b * kBlock + 64 + half * 32);
-    }
-    t.nrm[j] = n_row[j][b];
+    const uint8_t* pc = b_row[j] + b * c_blk + half * 32;
+    t.lo[j] = ld_nt16v(pc);
+    if constexpr (!NIB) t.hi[j] = ld_nt16v(pc + 64);
+    t.nrm[j] = n_row[j][b * n_blk];
   }
 }
 
@@ -149,7 +147,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
     const float* __restrict__ ct, int n_levels, uint32_t code_mask, int tbl_entries,
     const uint32_t* __restrict__ xp, void* __restrict__ y, const uint16_t* __restrict__ bias,
-    int M, int N, int nb, int64_t ldy, int tiles_m, int tiles_total) {
+    int M, int N, int nb, int64_t ldy, int tiles_m, int tiles_total, WLayout lay) {
   constexpr int BM = 2 * TMW * 32;
   constexpr int BN = 2 * TNW * 32;
   constexpr int KA = BM * 8 / 256;  // uint4 of A per thread per half-block
@@ -190,15 +188,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     a_dst[i] = r * kAStride + c * 16;
   }
   // B rows of this wave
-  const int row_bytes = NIB ? nb * 64 : nb * kBlock;
   const uint8_t* b_row[TNW];
   const uint16_t* n_row[TNW];
 #pragma unroll
   for (int j = 0; j < TNW; ++j) {
     int n = n0 + wn * TNW * 32 + j * 32 + l32;
     if (n >= N) n = N - 1;
-    b_row[j] = codes + (int64_t)n * row_bytes + 16 * h;
-    n_row[j] = norms + (int64_t)n * nb;
+    b_row[j] = codes + lay.codes_off(n) + 16 * h;
+    n_row[j] = norms + lay.norms_off(n);
   }
 
   float16v acc[TMW][TNW];
@@ -216,8 +213,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(
 
   // prologue: A(0) -> LDS 0, A(1) -> regs, B(0), B(1) -> regs
   load_atile<KA>(ar, a_src, 0);
-  load_btile<NIB, TNW>(b0, b_row, n_row, 0);
-  load_btile<NIB, TNW>(b1, b_row, n_row, 1);
+  load_btile<NIB, TNW>(b0, b_row, n_row, 0, lay.c_blk, lay.n_blk);
+  load_btile<NIB, TNW>(b1, b_row, n_row, 1, lay.c_blk, lay.n_blk);
   store_atile<KA>(abuf, ar, a_dst);
   load_atile<KA>(ar, a_src, 1);
   __syncthreads();
@@ -226,7 +223,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     // ---- even half-block: B from b0, A from LDS buffer 0
     {
       const BTile<NIB, TNW> cur = b0;
-      if (kt + 2 < nkt) load_btile<NIB, TNW>(b0, b_row, n_row, kt + 2);
+      if (kt + 2 < nkt) load_btile<NIB, TNW>(b0, b_row, n_row, kt + 2, lay.c_blk, lay.n_blk);
       mma_ktile<NIB, TMW, TNW>(acc, cur, abuf + a_off, tbl, lane4, code_mask);
       store_atile<KA>(abuf + BM * kAStride, ar, a_dst);  // A(kt+1) -> LDS 1
       if (kt + 2 < nkt) load_atile<KA>(ar, a_src, kt + 2);
@@ -235,7 +232,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     // ---- odd half-block: B from b1, A from LDS buffer 1
     {
       const BTile<NIB, TNW> cur = b1;
-      if (kt + 3 < nkt) load_btile<NIB, TNW>(b1, b_row, n_row, kt + 3);
+      if (kt + 3 < nkt) load_btile<NIB, TNW>(b1, b_row, n_row, kt + 3, lay.c_blk, lay.n_blk);
       mma_ktile<NIB, TMW, TNW>(acc, cur, abuf + BM * kAStride + a_off, tbl, lane4, code_mask);
       if (kt + 2 < nkt) {
         store_atile<KA>(abuf, ar, a_dst);  // A(kt+2) -> LDS 0
@@ -281,7 +278,7 @@ static int launch_gemm_t(const GemmArgs& a, hipStream_t st) {
   kern<<<dim3((unsigned)total), dim3(256), lds, st>>>(
       a.codes, a.norms, a.ct, a.n_levels, 0x01010101u * mb, entries,
       reinterpret_cast<const uint32_t*>(a.xp), a.y, a.bias, a.M, a.N, a.nb, a.ldy, tiles_m,
-      (int)total);
+      (int)total, a.lay);
   return launch_status();
 }
 
@@ -304,19 +301,20 @@ size_t mm_xtf_workspace(bool nibble, int64_t M, int N, int nb) {
   return 0;
 }
 
-int mm_xtf(bool nibble, const void* codes, const uint16_t* norms, const float* ct, int n_levels,
-           const void* x_pair, int64_t M, int N, int nb, void* y, int out_mode, int64_t ldy,
-           const uint16_t* bias, void* ws, size_t ws_bytes, hipStream_t st) {
+int mm_xtf(bool nibble, bool tiled, const void* codes, const uint16_t* norms, const float* ct,
+           int n_levels, const void* x_pair, int64_t M, int N, int nb, void* y, int out_mode,
+           int64_t ldy, const uint16_t* bias, void* ws, size_t ws_bytes, hipStream_t st) {
   (void)ws; (void)ws_bytes;
   if (M > INT32_MAX) return PE_ERR_DIMS;
+  const WLayout lay = wlayout(nibble, tiled, nb);
   if (M <= kSmallMaxRows) {
     SmallArgs s{reinterpret_cast<const uint8_t*>(codes), norms, ct, n_levels,
                 reinterpret_cast<const uint32_t*>(x_pair), nullptr, nullptr, 0, 0, y, ldy, bias,
-                (int)M, N, nb};
+                (int)M, N, nb, lay};
     return gemm_small(nibble, out_mode == OM_F32 ? SE_F32 : SE_F16, s, 1, st);
   }
   GemmArgs a{reinterpret_cast<const uint8_t*>(codes), norms, ct, n_levels, x_pair, y, bias,
-             (int)M, N, nb, ldy};
+             (int)M, N, nb, ldy, lay};
   return gemm(nibble, out_mode, a, st);
 }
 

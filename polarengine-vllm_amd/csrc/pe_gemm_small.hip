@@ -73,16 +73,13 @@ template <bool NIB, int NT, int MTM>
 __device__ __forceinline__ void load_sblk(SmallBlk<NT, MTM>& k, const uint8_t* const (&brow)[NT],
                                           const uint16_t* const (&nrow)[NT],
                                           const uint32_t* const (&arow)[MTM],
-                                          const bool (&alive)[MTM], int b) {
+                                          const bool (&alive)[MTM], int b, const WLayout& lay) {
 #pragma unroll
   for (int j = 0; j < NT; ++j) {
-    if constexpr (NIB) {
-      k.lo[j] = ld_nt16v(brow[j] + b * 64);
-    } else {
-      k.lo[j] = ld_nt16v(brow[j] + b * kBlock);
-      k.hi[j] = ld_nt16v(brow[j] + b * kBlock + 64);
-    }
-    k.nbits[j] = nrow[j][b];
+    const uint8_t* pc = brow[j] + b * lay.c_blk;
+    k.lo[j] = ld_nt16v(pc);
+    if constexpr (!NIB) k.hi[j] = ld_nt16v(pc + 64);
+    k.nbits[j] = nrow[j][b * lay.n_blk];
   }
 #pragma unroll
   for (int i = 0; i < MTM; ++i) {
@@ -154,7 +151,6 @@ __global__ __launch_bounds__(kSmallThreads) void gemm_small_kernel(
   if (M <= 0) return;  // whole workgroup exits together (uniform)
 
   // ---- this lane's weight rows (clamped; clamped rows are never stored)
-  const int row_bytes = NIB ? a.nb * 64 : a.nb * kBlock;
   const int wrows = EP == SE_SWIGLU ? 2 * a.N : a.N;
   const uint8_t* brow[NT];
   const uint16_t* nrow[NT];
@@ -164,8 +160,8 @@ __global__ __launch_bounds__(kSmallThreads) void gemm_small_kernel(
     if (n >= a.N) n = a.N - 1;
     if (EP == SE_SWIGLU && j >= TN) n += a.N;  // the matching "up" row
     if (n >= wrows) n = wrows - 1;
-    brow[j] = codes + (int64_t)n * row_bytes + 16 * g;
-    nrow[j] = norms + (int64_t)n * a.nb;
+    brow[j] = codes + a.lay.codes_off(n) + 16 * g;
+    nrow[j] = norms + a.lay.norms_off(n);
   }
   const int64_t xrow = (int64_t)a.nb * 64;
   // K range of this wave
@@ -202,9 +198,9 @@ __global__ __launch_bounds__(kSmallThreads) void gemm_small_kernel(
 
     // two-stage pipeline over this wave's blocks: block b+1 loads while b computes
     SmallBlk<NT, MTM> cur, nxt;
-    if (b_begin < b_end) load_sblk<NIB, NT, MTM>(cur, brow, nrow, arow, alive, b_begin);
+    if (b_begin < b_end) load_sblk<NIB, NT, MTM>(cur, brow, nrow, arow, alive, b_begin, a.lay);
     for (int b = b_begin; b < b_end; ++b) {
-      if (b + 1 < b_end) load_sblk<NIB, NT, MTM>(nxt, brow, nrow, arow, alive, b + 1);
+      if (b + 1 < b_end) load_sblk<NIB, NT, MTM>(nxt, brow, nrow, arow, alive, b + 1, a.lay);
       __builtin_amdgcn_sched_barrier(0);
       compute_sblk<NIB, NT, MTM>(acc, cur, tbl, lane4, code_mask, MT);
       cur = nxt;

@@ -35,22 +35,32 @@ struct DecBlk {
   uint16_t nb[TN];
 };
 
-// Loads of one block of the TN rows; an invalid block (past the wave's range)
-// loads 16 bytes of the codebook instead, so the number of loads issued is
-// the same on every path (exact vmcnt waits) at no HBM cost.
+// Weight source of one lane: buffer resources for codes and norms (a real one
+// and a zero-length one), the lane's row offsets in VGPRs. The block offset
+// goes in the scalar offset, so a block's loads cost no VALU; a block past the
+// wave's range reads through the zero-length resource, which returns zeros
+// without touching memory -- the load count stays the same on every path
+// (exact vmcnt waits).
+struct DecSrc {
+  __amdgpu_buffer_rsrc_t codes, codes_none, norms, norms_none;
+  uint32_t voff_codes, voff_norms;
+};
+
+constexpr int kBufNT = 2;
+constexpr int kBufFlags = 0x00020000;  // raw buffer, 32-bit data format (dword 3 of the resource)  // buffer load cache policy: non-temporal (weights are read once)
+
 template <bool NIB, int TN>
-__device__ __forceinline__ void dec_load(DecBlk<NIB, TN>& k, const uint8_t* const (&brow)[TN],
-                                         const uint16_t* const (&nrow)[TN], int b, bool valid,
-                                         const void* dummy) {
-#pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const uint8_t* pc = valid ? brow[j] + (NIB ? b * 64 : b * kBlock)
-                              : reinterpret_cast<const uint8_t*>(dummy);
-    const uint16_t* pn = valid ? nrow[j] + b : reinterpret_cast<const uint16_t*>(dummy);
-    k.lo[j] = ld_nt16v(pc);
-    if constexpr (!NIB) k.hi[j] = ld_nt16v(valid ? pc + 64 : pc);
-    k.nb[j] = *pn;
-  }
+__device__ __forceinline__ void dec_load(DecBlk<NIB, TN>& k, const DecSrc& src, int b, bool valid,
+                                         int c_blk, int n_blk2) {
+  static_assert(TN == 1, "one 16-row tile per wave");
+  const __amdgpu_buffer_rsrc_t rc = valid ? src.codes : src.codes_none;
+  const __amdgpu_buffer_rsrc_t rn = valid ? src.norms : src.norms_none;
+  k.lo[0] = __builtin_bit_cast(
+      u32x4v, __builtin_amdgcn_raw_buffer_load_b128(rc, src.voff_codes, b * c_blk, kBufNT));
+  if constexpr (!NIB)
+    k.hi[0] = __builtin_bit_cast(
+        u32x4v, __builtin_amdgcn_raw_buffer_load_b128(rc, src.voff_codes, b * c_blk + 64, kBufNT));
+  k.nb[0] = __builtin_amdgcn_raw_buffer_load_b16(rn, src.voff_norms, b * n_blk2, kBufNT);
 }
 
 template <bool NIB>
@@ -74,42 +84,75 @@ __device__ __forceinline__ half8v dec_dequant(uint32_t wl, uint32_t wh, uint32_t
   return __builtin_bit_cast(half8v, u32x4v{p[0], p[1], p[2], p[3]});
 }
 
-// Codebook table from wave-uniform (scalar) loads of ct; every lane writes its
-// own copy of each entry. Nibble: entry (hi << 4) | lo = half2(ct[lo], ct[hi]),
-// wave w takes hi = w, w + NW, ...; int8: entry e = fp16(ct[e]) in the low
-// half, wave w takes e = 16 w .. 16 w + 15, then + 16 NW.
+// Codebook table from wave-uniform (scalar) loads of ct, issued by every
+// wave as its first memory request (scalar loads do not queue behind the
+// vector weight stream); every lane then writes its own copy of each entry.
+// Nibble: entry (hi << 4) | lo = half2(ct[lo], ct[hi]) (the 16 loaded values
+// are the whole codebook), wave w takes hi = w and w + NW; int8: entry e = fp16(ct[e]) in the low half, wave w takes
+// e = 16 w .. 16 w + 15 and 16 (w + NW) .. + 15. NW >= 8 covers 256 entries.
+template <bool NIB>
+struct DecTable {
+  float c[NIB ? 16 : 32];  // nibble: ct[0..15] (clamped); int8: two 16-entry chunks
+};
+
 template <bool NIB, int NW>
-__device__ __forceinline__ void dec_fill_table(const float* __restrict__ ct, int n_levels, int wave,
-                                               uint32_t lane4) {
+__device__ __forceinline__ void dec_table_load(DecTable<NIB>& t, const float* __restrict__ ct,
+                                               int n_levels, int wave) {
+  const int last = n_levels - 1;
   if constexpr (NIB) {
-    float clo[16];
 #pragma unroll
-    for (int lo = 0; lo < 16; ++lo) clo[lo] = ct[lo < n_levels ? lo : n_levels - 1];
-    for (int hi = wave; hi < n_levels; hi += NW) {
-      const float chi = ct[hi];
+    for (int lo = 0; lo < 16; ++lo) t.c[lo] = ct[lo < n_levels ? lo : last];
+  } else {
 #pragma unroll
-      for (int lo = 0; lo < 16; ++lo)
-        if (lo < n_levels)
-          lds_st32((uint32_t)((hi << 4) | lo) << 8 | lane4, pack_h2(clo[lo], chi));
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int e = (wave + h * NW) * 16 + k;
+        t.c[h * 16 + k] = ct[e < n_levels ? e : last];
+      }
+  }
+}
+
+template <bool NIB, int NW>
+__device__ __forceinline__ void dec_table_write(const DecTable<NIB>& t, int n_levels, int wave,
+                                                uint32_t lane4) {
+  if constexpr (NIB) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int hi = wave + h * NW;
+      if (hi < n_levels) {
+        float chi = t.c[0];  // ct[hi] by a uniform select (no further load)
+#pragma unroll
+        for (int k = 1; k < 16; ++k) chi = hi == k ? t.c[k] : chi;
+#pragma unroll
+        for (int lo = 0; lo < 16; ++lo)
+          if (lo < n_levels)
+            lds_st32((uint32_t)((hi << 4) | lo) << 8 | lane4, pack_h2(t.c[lo], chi));
+      }
     }
   } else {
-    for (int e0 = wave * 16; e0 < n_levels; e0 += NW * 16) {
 #pragma unroll
-      for (int k = 0; k < 16; ++k)
-        if (e0 + k < n_levels)
-          lds_st32((uint32_t)(e0 + k) << 8 | lane4, (uint32_t)f2h_bits(ct[e0 + k]));
-    }
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int e = (wave + h * NW) * 16 + k;
+        if (e < n_levels) lds_st32((uint32_t)e << 8 | lane4, (uint32_t)f2h_bits(t.c[h * 16 + k]));
+      }
   }
 }
 
 // x: raw fp16 activations [M, K] (XRAW) or pair-f16 x_tf [M][nb][64] (else),
-// row stride ldx fp16 elements. XC: activation registers per lane.
-template <bool NIB, int TN, int NW, bool XRAW, bool MASK, int XC, int SCHED = 0>
-__global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(
+// row stride ldx fp16 elements. The workgroup covers TN 16-row tiles with
+// NW = TN * KS waves: wave w works on tile w % TN over the K-slice w / TN
+// (contiguous 128-blocks), streaming it D blocks deep. XC: activation
+// registers per lane.
+template <bool NIB, int TN, int KS, bool XRAW, bool MASK, int XC, int D>
+__global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
     const float* __restrict__ ct, int n_levels, uint32_t code_mask,
     const void* __restrict__ x, int64_t ldx, void* __restrict__ y, int64_t ldy,
-    const uint16_t* __restrict__ bias, int M, int N, int nb, uint32_t xs_addr) {
+    const uint16_t* __restrict__ bias, int M, int N, int nb, uint32_t xs_addr, WLayout lay) {
+  constexpr int NW = TN * KS;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar loads, branches
@@ -118,28 +161,32 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(
   // LDS: [codebook table][activations, 256 B per (row, block) from xs_addr];
   // after the K loop the reduction buffer reuses the start of LDS.
 
-  const int b_begin = (int)((int64_t)nb * wave / NW);
-  const int b_end = (int)((int64_t)nb * (wave + 1) / NW);
+  const int jt = wave % TN, ks = wave / TN;
+  const int b_begin = (int)((int64_t)nb * ks / KS);
+  const int b_end = (int)((int64_t)nb * (ks + 1) / KS);
   const int nbw = b_end - b_begin;  // blocks of this wave (uniform)
 
-  // weight rows of this lane (clamped; clamped rows are never stored)
-  const int row_bytes = NIB ? nb * 64 : nb * kBlock;
-  const uint8_t* brow[TN];
-  const uint16_t* nrow[TN];
-#pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    int n = blockIdx.x * TN * 16 + j * 16 + l16;
+  // weight row of this lane (clamped; clamped rows are never stored)
+  DecSrc src;
+  const int c_blk = (int)lay.c_blk, n_blk2 = (int)lay.n_blk * 2;  // block strides in bytes
+  {
+    int n = (blockIdx.x * TN + jt) * 16 + l16;
     n = n < N ? n : N - 1;
-    brow[j] = codes + (int64_t)n * row_bytes + 16 * g;
-    nrow[j] = norms + (int64_t)n * nb;
+    // extents up to the last row's end (< 2 GiB: host check)
+    const int codes_bytes = (int)(lay.codes_off(N - 1) + (int64_t)nb * lay.c_blk);
+    const int norms_bytes = (int)(lay.norms_off(N - 1) + (int64_t)nb * lay.n_blk) * 2;
+    src.codes = __builtin_amdgcn_make_buffer_rsrc((void*)codes, (short)0, codes_bytes, kBufFlags);
+    src.codes_none = __builtin_amdgcn_make_buffer_rsrc((void*)codes, (short)0, 0, kBufFlags);
+    src.norms = __builtin_amdgcn_make_buffer_rsrc((void*)norms, (short)0, norms_bytes, kBufFlags);
+    src.norms_none = __builtin_amdgcn_make_buffer_rsrc((void*)norms, (short)0, 0, kBufFlags);
+    src.voff_codes = (uint32_t)(lay.codes_off(n) + 16 * g);
+    src.voff_norms = (uint32_t)(lay.norms_off(n) * 2);
   }
 
   // ---- 0. activations: the workgroup's M x nb (row, block) items are spread
-  // over the 16-lane groups of its first PW waves ("prologue waves"): group
-  // gi = 4 wave + g takes items gi + 4 PW i (i < XC), lane l16 holding
-  // elements 8 l16 .. 8 l16 + 7. Unconditional (clamped) loads.
-  constexpr int PW = SCHED == 2 ? NW / 2 : NW;
-  const bool pro = wave < PW;  // uniform
+  // over its 4 NW 16-lane groups: group gi = 4 wave + g takes items
+  // gi + 4 NW i (i < XC), lane l16 holding elements 8 l16 .. 8 l16 + 7.
+  // Unconditional (clamped) loads, queued on the CU before any weight load.
   const int nitems = M * nb;
   const int gi = wave * 4 + g;
   int it_m, it_b;
@@ -149,31 +196,48 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(
     it_b = it - it_m * nb;
   }
   u32x4v xr[XC];
-  if (pro) {
+  {
     const char* xb = reinterpret_cast<const char*>(x);
     int m = it_m, b = it_b;
 #pragma unroll
     for (int i = 0; i < XC; ++i) {
-      const bool ok = gi + 4 * PW * i < nitems;
+      const bool ok = gi + 4 * NW * i < nitems;
       const int64_t off = ok ? ((int64_t)m * ldx + (int64_t)b * kBlock) * 2 + l16 * 16 : 0;
       xr[i] = *reinterpret_cast<const u32x4v*>(xb + off);
-      b += 4 * PW;
+      b += 4 * NW;
       while (b >= nb) {
         b -= nb;
         ++m;
       }
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
+  // codebook values (scalar loads: they do not queue behind the weight stream)
+  DecTable<NIB> tab;
+  dec_table_load<NIB, NW>(tab, ct, n_levels, wave);
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
 
-  // ---- table + transform of the activations into LDS as pair f16: 256 B per
-  // (row, block), pair p = (x_tf[128 b + p], x_tf[128 b + 64 + p]) at byte 4 p.
-  // XRAW: FWHT of the item by its 16-lane group first.
-  auto prologue = [&]() {
-    dec_fill_table<NIB, PW>(ct, n_levels, wave, lane4);
+  // ---- first D blocks of weights: the stream starts before the prologue
+  DecBlk<NIB, 1> ring[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    dec_load<NIB, 1>(ring[d], src, b_begin + d, d < nbw, c_blk, n_blk2);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // ---- 1. codebook table (all waves)
+  dec_table_write<NIB, NW>(tab, n_levels, wave, lane4);
+
+  // ---- 2. activations into LDS as pair f16: 256 B per (row, block), pair p
+  // = (x_tf[128 b + p], x_tf[128 b + 64 + p]) at byte 4 p. XRAW: FWHT of the
+  // item by its 16-lane group first.
+  {
     int m = it_m, b = it_b;
 #pragma unroll
     for (int i = 0; i < XC; ++i) {
-      if (gi + 4 * PW * i < nitems) {  // uniform inside the group
+      if (gi + 4 * NW * i < nitems) {  // uniform inside the group
         const uint32_t blk = xs_addr + (uint32_t)(m * nb + b) * 256u;
         if constexpr (XRAW) {
           const int q = l16;
@@ -204,105 +268,65 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(
           lds_st128(blk + (uint32_t)l16 * 16u, xr[i]);
         }
       }
-      b += 4 * PW;
+      b += 4 * NW;
       while (b >= nb) {
         b -= nb;
         ++m;
       }
     }
-  };
-
-  DecBlk<NIB, TN> r0, r1;
-  if constexpr (SCHED == 1) {
-    // prologue first, then the weight stream
-    prologue();
-    __syncthreads();
-    dec_load<NIB, TN>(r0, brow, nrow, b_begin, nbw > 0, ct);
-    dec_load<NIB, TN>(r1, brow, nrow, b_begin + 1, nbw > 1, ct);
-  } else {
-    // every wave has queued its activation loads before any weight load
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (SCHED == 0) {
-      dec_load<NIB, TN>(r0, brow, nrow, b_begin, nbw > 0, ct);
-      __builtin_amdgcn_sched_barrier(0);
-      prologue();
-      dec_load<NIB, TN>(r1, brow, nrow, b_begin + 1, nbw > 1, ct);
-    } else {
-      if (!pro) {
-        dec_load<NIB, TN>(r0, brow, nrow, b_begin, nbw > 0, ct);
-        dec_load<NIB, TN>(r1, brow, nrow, b_begin + 1, nbw > 1, ct);
-      } else {
-        prologue();
-        dec_load<NIB, TN>(r0, brow, nrow, b_begin, nbw > 0, ct);
-        dec_load<NIB, TN>(r1, brow, nrow, b_begin + 1, nbw > 1, ct);
-      }
-    }
-    __syncthreads();
   }
+  __syncthreads();
 
-  // ---- 3. K loop, two blocks in flight: A (row m = l16, zero past M) from
+  // ---- 3. K loop, D blocks in flight: A (row m = l16) from
   // LDS, B dequantized from the code registers; a block's lookups are issued
   // before its MFMAs.
-  float4v acc[TN];
-#pragma unroll
-  for (int j = 0; j < TN; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
-  const bool arow_ok = l16 < M;
-  const uint32_t arow = xs_addr + (uint32_t)(l16 * nb) * 256u + 64u * g;
-  auto do_block = [&](const DecBlk<NIB, TN>& k, int b) {
+  float4v acc = float4v{0.f, 0.f, 0.f, 0.f};
+  // A row of this lane: rows past M repeat row M-1; they only feed D rows
+  // >= M, which are never stored
+  const uint32_t arow = xs_addr + (uint32_t)((l16 < M ? l16 : M - 1) * nb) * 256u + 64u * g;
+  auto do_block = [&](const DecBlk<NIB, 1>& k, int b) {
     u32x4v af[4];
-    if (arow_ok) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) af[t] = lds_ld128(arow + (uint32_t)b * 256u + 16u * t);
-    } else {
+    for (int t = 0; t < 4; ++t) af[t] = lds_ld128(arow + (uint32_t)b * 256u + 16u * t);
+    half8v bf[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) af[t] = u32x4v{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      half8v bf[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        uint32_t wl = k.lo[j][t], wh = NIB ? 0u : k.hi[j][t];
-        if constexpr (MASK) {
-          wl &= code_mask;
-          wh &= code_mask;
-        }
-        bf[t] = dec_dequant<NIB>(wl, wh, lane4);
+    for (int t = 0; t < 4; ++t) {
+      uint32_t wl = k.lo[0][t], wh = NIB ? 0u : k.hi[0][t];
+      if constexpr (MASK) {
+        wl &= code_mask;
+        wh &= code_mask;
       }
-      float4v blk = float4v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-        blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, af[t]), bf[t], blk,
-                                                     0, 0, 0);
-      acc[j] += blk * h2f(k.nb[j]);
+      bf[t] = dec_dequant<NIB>(wl, wh, lane4);
     }
+    float4v blk = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, af[t]), bf[t], blk,
+                                                   0, 0, 0);
+    acc += blk * h2f(k.nb[0]);
   };
-  for (int i = 0; i < nbw; i += 2) {
-    do_block(r0, b_begin + i);
-    dec_load<NIB, TN>(r0, brow, nrow, b_begin + i + 2, i + 2 < nbw, ct);
-    __builtin_amdgcn_sched_barrier(0);
-    if (i + 1 < nbw) do_block(r1, b_begin + i + 1);
-    dec_load<NIB, TN>(r1, brow, nrow, b_begin + i + 3, i + 3 < nbw, ct);
-    __builtin_amdgcn_sched_barrier(0);
+  for (int i = 0; i < nbw; i += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      if (i + d < nbw) do_block(ring[d], b_begin + i + d);
+      dec_load<NIB, 1>(ring[d], src, b_begin + i + d + D, i + d + D < nbw, c_blk, n_blk2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 
-  // ---- 4. combine the NW K-slices through LDS: red[w][j][lane][4]
+  // ---- 4. combine the KS K-slices of each tile through LDS: red[ks][jt][lane][4]
   __syncthreads();
-#pragma unroll
-  for (int j = 0; j < TN; ++j)
-    lds_st128((uint32_t)(((wave * TN + j) * 64 + lane) * 16), __builtin_bit_cast(u32x4v, acc[j]));
+  lds_st128((uint32_t)(((ks * TN + jt) * 64 + lane) * 16), __builtin_bit_cast(u32x4v, acc));
   __syncthreads();
   // outputs: rows m < M (D element e of lane l: row 4*(l/16) + e), 16*TN columns
   for (int o = tid; o < TN * 256; o += NW * 64) {
     const int j = o >> 8, le = o & 255, ln = le >> 2, e = le & 3;
     const int m = 4 * (ln >> 4) + e;
-    const int n = blockIdx.x * TN * 16 + j * 16 + (ln & 15);
+    const int n = (blockIdx.x * TN + j) * 16 + (ln & 15);
     if (m >= M || n >= N) continue;
     float s = 0.f;
 #pragma unroll
-    for (int w = 0; w < NW; ++w)
+    for (int w = 0; w < KS; ++w)
       s += __builtin_bit_cast(float, lds_ld32((uint32_t)((((w * TN + j) * 64) * 4 + le) * 4)));
     _Float16 hv = (_Float16)s;
     if (bias) hv = (_Float16)((float)hv + h2f(bias[n]));
@@ -314,23 +338,29 @@ __global__ __launch_bounds__(NW * 64) void gemv_mfma_kernel(
 // host launch
 // ---------------------------------------------------------------------------
 
-constexpr int kDecNW = 16;  // waves per workgroup (one workgroup per CU)
+// waves per workgroup: TN tiles x KS K-slices, at most 16 and at least 8 (the
+// table fill covers 256 entries with two per wave) -- one workgroup per CU
+constexpr int kDecMaxW = 16;
+template <int TN>
+constexpr int dec_ks() { return kDecMaxW / TN; }
 
-// activation registers per lane: M * nb items of 16 x 16 B over the 4 * NW
+// activation registers per lane: M * nb items of 16 x 16 B over the 4 NW
 // 16-lane groups of the workgroup
-static int dec_xc(int M, int nb) { return (M * nb + 4 * kDecNW - 1) / (4 * kDecNW); }
+static int dec_xc(int M, int nb, int nw) { return (M * nb + 4 * nw - 1) / (4 * nw); }
 
-static size_t dec_lds(bool nibble, int M, int nb, int n_levels, int tn) {
+static size_t dec_lds(bool nibble, int M, int nb, int n_levels, int nw) {
   size_t lds = (size_t)table_entries(nibble, n_levels) * 256 + (size_t)M * nb * 256;
-  const size_t red = (size_t)kDecNW * tn * 64 * 16;
+  const size_t red = (size_t)nw * 64 * 16;
   return lds < red ? red : lds;
 }
 
 template <bool NIB, int TN, bool XRAW, bool MASK, int XC>
 static int launch_dec(const DecArgs& a, hipStream_t st) {
-  auto kern = gemv_mfma_kernel<NIB, TN, kDecNW, XRAW, MASK, XC>;
-  const size_t lds = dec_lds(NIB, a.M, a.nb, a.n_levels, TN);
-  if (lds > 160 * 1024 || dec_xc(a.M, a.nb) > XC) return PE_ERR_DIMS;
+  constexpr int KS = dec_ks<TN>(), NW = TN * KS;
+  constexpr int D = NIB ? 4 : 2;  // blocks in flight per wave (nibble 1 KB, int8 2 KB each)
+  auto kern = gemv_mfma_kernel<NIB, TN, KS, XRAW, MASK, XC, D>;
+  const size_t lds = dec_lds(NIB, a.M, a.nb, a.n_levels, NW);
+  if (lds > 160 * 1024 || dec_xc(a.M, a.nb, NW) > XC) return PE_ERR_DIMS;
   static const bool attr_ok = [&] {
     return hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
@@ -339,15 +369,15 @@ static int launch_dec(const DecArgs& a, hipStream_t st) {
   const int tiles = (a.N + TN * 16 - 1) / (TN * 16);
   const uint8_t mb = NIB ? (uint8_t)((a.n_levels - 1) * 0x11) : (uint8_t)(a.n_levels - 1);
   const uint32_t xs_addr = (uint32_t)table_entries(NIB, a.n_levels) * 256u;
-  kern<<<dim3(tiles), dim3(kDecNW * 64), lds, st>>>(a.codes, a.norms, a.ct, a.n_levels,
-                                                   0x01010101u * mb, a.x, a.ldx, a.y, a.ldy,
-                                                   a.bias, a.M, a.N, a.nb, xs_addr);
+  kern<<<dim3(tiles), dim3(NW * 64), lds, st>>>(a.codes, a.norms, a.ct, a.n_levels,
+                                               0x01010101u * mb, a.x, a.ldx, a.y, a.ldy, a.bias,
+                                               a.M, a.N, a.nb, xs_addr, a.lay);
   return launch_status();
 }
 
 template <bool NIB, int TN, bool XRAW, bool MASK>
 static int launch_dec_xc(const DecArgs& a, hipStream_t st) {
-  const int xc = dec_xc(a.M, a.nb);
+  const int xc = dec_xc(a.M, a.nb, TN * dec_ks<TN>());
   if (xc <= 1) return launch_dec<NIB, TN, XRAW, MASK, 1>(a, st);
   if (xc <= 2) return launch_dec<NIB, TN, XRAW, MASK, 2>(a, st);
   if (xc <= 4) return launch_dec<NIB, TN, XRAW, MASK, 4>(a, st);
@@ -361,7 +391,7 @@ static int dec_tn(int N) {
   const int tiles16 = (N + 15) / 16, cus = num_cus();
   int best = 1;
   long best_cost = -1;
-  for (int tn = 1; tn <= 3; ++tn) {
+  for (int tn = 1; tn <= 4; ++tn) {
     const long wgs = (tiles16 + tn - 1) / tn;
     const long cost = (wgs + cus - 1) / cus * tn;
     if (best_cost < 0 || cost <= best_cost) {
@@ -377,7 +407,8 @@ static int launch_dec_tn(const DecArgs& a, hipStream_t st) {
   switch (dec_tn(a.N)) {
     case 1: return launch_dec_xc<NIB, 1, XRAW, MASK>(a, st);
     case 2: return launch_dec_xc<NIB, 2, XRAW, MASK>(a, st);
-    default: return launch_dec_xc<NIB, 3, XRAW, MASK>(a, st);
+    case 3: return launch_dec_xc<NIB, 3, XRAW, MASK>(a, st);
+    default: return launch_dec_xc<NIB, 4, XRAW, MASK>(a, st);
   }
 }
 
@@ -387,13 +418,17 @@ static int launch_dec_m(const DecArgs& a, hipStream_t st) {
   return mask ? launch_dec_tn<NIB, XRAW, true>(a, st) : launch_dec_tn<NIB, XRAW, false>(a, st);
 }
 
-bool gemv_mfma_fits(bool nibble, int M, int nb, int n_levels) {
-  if (M < 1 || M > 16 || dec_xc(M, nb) > 8) return false;
-  return dec_lds(nibble, M, nb, n_levels, 3) <= 160 * 1024;
+bool gemv_mfma_fits(bool nibble, int M, int N, int nb, int n_levels) {
+  // the smallest workgroup (15 waves, TN = 3) bounds the activation registers
+  if (M < 1 || M > 16 || dec_xc(M, nb, 15) > 8) return false;
+  // buffer resources address codes and norms with 31-bit offsets (tiled
+  // layouts round N up to 16 rows)
+  if ((int64_t)(N + 15) * nb * (nibble ? 64 : kBlock) >= (int64_t)1 << 31) return false;
+  return dec_lds(nibble, M, nb, n_levels, kDecMaxW) <= 160 * 1024;
 }
 
 int gemv_mfma(bool nibble, bool xraw, const DecArgs& a, hipStream_t st) {
-  if (!gemv_mfma_fits(nibble, a.M, a.nb, a.n_levels)) return PE_ERR_DIMS;
+  if (!gemv_mfma_fits(nibble, a.M, a.N, a.nb, a.n_levels)) return PE_ERR_DIMS;
   if (nibble) return xraw ? launch_dec_m<true, true>(a, st) : launch_dec_m<true, false>(a, st);
   return xraw ? launch_dec_m<false, true>(a, st) : launch_dec_m<false, false>(a, st);
 }

@@ -5,6 +5,31 @@
 
 namespace pe {
 
+// Weight layout of one quantized matrix (nb 128-blocks per row, bpb code
+// bytes per block: 64 nibble-packed, 128 int8). Byte offset of (row n, block b)
+// in the codes: (n >> 4) * c_tile + (n & 15) * c_row + b * c_blk; norms alike,
+// in elements.
+//   row-major (the reference layout): c_tile = 16 row_bytes, c_row = row_bytes,
+//     c_blk = bpb;
+//   tiled-16 (PE_LAYOUT_TILE16): the 16 rows x bpb bytes of one (16-row tile,
+//     block) are contiguous, c_tile = 16 nb bpb, c_row = bpb, c_blk = 16 bpb;
+//     rows are padded to a multiple of 16.
+struct WLayout {
+  int64_t c_tile, c_row, c_blk;
+  int64_t n_tile, n_row, n_blk;
+  __host__ __device__ int64_t codes_off(int n) const {
+    return (int64_t)(n >> 4) * c_tile + (int64_t)(n & 15) * c_row;
+  }
+  __host__ __device__ int64_t norms_off(int n) const {
+    return (int64_t)(n >> 4) * n_tile + (int64_t)(n & 15) * n_row;
+  }
+};
+inline WLayout wlayout(bool nibble, bool tiled, int nb) {
+  const int64_t bpb = nibble ? 64 : 128;
+  if (tiled) return WLayout{16 * nb * bpb, bpb, 16 * bpb, 16 * (int64_t)nb, 1, 16};
+  return WLayout{16 * nb * bpb, nb * bpb, bpb, 16 * (int64_t)nb, nb, 1};
+}
+
 // activation source of the M = 1 GEMV
 enum { XM_RAW_F16 = 0, XM_XTF_F32 = 1, XM_PAIR_F16 = 2 };
 // output element type of GEMV/GEMM epilogues
@@ -32,6 +57,7 @@ struct GemmArgs {
   const uint16_t* bias;
   int M, N, nb;
   int64_t ldy;
+  WLayout lay;
 };
 
 // pe_gemv.hip
@@ -57,6 +83,7 @@ struct SmallArgs {
   int M;                     // rows (non-grouped)
   int N;                     // output columns (SwiGLU: I; the weights hold 2I rows)
   int nb;
+  WLayout lay;               // per-expert layout (row-major for the MoE path)
 };
 
 // pe_gemm_small.hip: M <= kSmallMaxRows per pass is cheapest (larger M loops)
@@ -75,16 +102,17 @@ struct DecArgs {
   int64_t ldy;     // row stride of y in fp16 elements
   const uint16_t* bias;
   int M, N, nb;
+  WLayout lay;
 };
-bool gemv_mfma_fits(bool nibble, int M, int nb, int n_levels);
+bool gemv_mfma_fits(bool nibble, int M, int N, int nb, int n_levels);
 int gemv_mfma(bool nibble, bool xraw, const DecArgs& a, hipStream_t st);
 
 // pe_gemm.hip
 int gemm(bool nibble, int omode, const GemmArgs& a, hipStream_t st);
 size_t mm_xtf_workspace(bool nibble, int64_t M, int N, int nb);
-int mm_xtf(bool nibble, const void* codes, const uint16_t* norms, const float* ct, int n_levels,
-           const void* x_pair, int64_t M, int N, int nb, void* y, int out_mode, int64_t ldy,
-           const uint16_t* bias, void* ws, size_t ws_bytes, hipStream_t st);
+int mm_xtf(bool nibble, bool tiled, const void* codes, const uint16_t* norms, const float* ct,
+           int n_levels, const void* x_pair, int64_t M, int N, int nb, void* y, int out_mode,
+           int64_t ldy, const uint16_t* bias, void* ws, size_t ws_bytes, hipStream_t st);
 
 // pe_fwht.hip
 int fwht128(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t ldx, void* y,

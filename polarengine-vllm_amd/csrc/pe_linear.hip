@@ -18,11 +18,14 @@
 
 namespace pe {
 
-static int check_format(int bits, int packed, int n_levels, bool* nibble) {
+// `packed` flags: PE_PACK_NIBBLE (bit 0, bits <= 4), PE_LAYOUT_TILE16 (bit 1).
+static int check_format(int bits, int packed, int n_levels, bool* nibble, bool* tiled) {
   if (bits < 2 || bits > 8) return PE_ERR_BITS;
-  if (packed && bits > 4) return PE_ERR_BITS;
+  if (packed & ~(PE_PACK_NIBBLE | PE_LAYOUT_TILE16)) return PE_ERR_BITS;
+  if ((packed & PE_PACK_NIBBLE) && bits > 4) return PE_ERR_BITS;
   if (n_levels != (1 << bits)) return PE_ERR_BITS;
-  *nibble = packed != 0;
+  *nibble = (packed & PE_PACK_NIBBLE) != 0;
+  *tiled = (packed & PE_LAYOUT_TILE16) != 0;
   return PE_OK;
 }
 
@@ -34,7 +37,8 @@ using namespace pe;
 extern "C" size_t pe_linear_xtf_workspace_size(int64_t M, int in_f_padded, int out_f, int bits,
                                                int packed) {
   if (M <= 1 || in_f_padded <= 0 || out_f <= 0) return 0;
-  return mm_xtf_workspace(packed != 0 && bits <= 4, M, out_f, in_f_padded / kBlock);
+  return mm_xtf_workspace((packed & PE_PACK_NIBBLE) != 0 && bits <= 4, M, out_f,
+                          in_f_padded / kBlock);
 }
 
 extern "C" size_t pe_linear_workspace_size(int64_t M, int in_f, int out_f, int bits, int packed) {
@@ -55,19 +59,20 @@ extern "C" int pe_linear_forward_xtf(const void* x_tf_pair, int64_t M, int in_f_
   if (!x_tf_pair || !codes || !norms_f16 || !ct_scaled || !y) return PE_ERR_NULL;
   if (M < 0 || out_f <= 0 || in_f_padded <= 0 || in_f_padded % kBlock) return PE_ERR_DIMS;
   if (out_dtype != PE_DTYPE_F16) return PE_ERR_DTYPE;
-  bool nib = false;
-  if (int rc = check_format(bits, packed, n_levels, &nib)) return rc;
+  bool nib = false, tiled = false;
+  if (int rc = check_format(bits, packed, n_levels, &nib, &tiled)) return rc;
   if (!aligned16(x_tf_pair) || !aligned16(codes)) return PE_ERR_ALIGN;
   if (M == 0) return PE_OK;
   const int nb = in_f_padded / kBlock;
-  if (M <= 16 && gemv_mfma_fits(nib, (int)M, nb, n_levels)) {
+  if (M <= 16 && gemv_mfma_fits(nib, (int)M, out_f, nb, n_levels)) {
     DecArgs a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels,
               x_tf_pair, (int64_t)in_f_padded, y, out_f, reinterpret_cast<const uint16_t*>(bias),
-              (int)M, out_f, nb};
+              (int)M, out_f, nb, wlayout(nib, tiled, nb)};
     return gemv_mfma(nib, false, a, st);
   }
-  return mm_xtf(nib, codes, norms_f16, ct_scaled, n_levels, x_tf_pair, M, out_f, nb, y, OM_F16,
-                out_f, reinterpret_cast<const uint16_t*>(bias), workspace, workspace_bytes, st);
+  return mm_xtf(nib, tiled, codes, norms_f16, ct_scaled, n_levels, x_tf_pair, M, out_f, nb, y,
+                OM_F16, out_f, reinterpret_cast<const uint16_t*>(bias), workspace,
+                workspace_bytes, st);
 }
 
 extern "C" int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f, int64_t ldx,
@@ -82,17 +87,18 @@ extern "C" int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f
   // The kernels read 128-wide blocks of x: in_f must already be a multiple of
   // 128 (the Python layer pads otherwise, as linear_method.py:194-195 does).
   if (in_f % kBlock) return PE_ERR_DIMS;
-  bool nib = false;
-  if (int rc = check_format(bits, packed, n_levels, &nib)) return rc;
+  bool nib = false, tiled = false;
+  if (int rc = check_format(bits, packed, n_levels, &nib, &tiled)) return rc;
   if (!aligned16(x) || !aligned16(codes) || (ldx * 2) % 16) return PE_ERR_ALIGN;
   if (M == 0) return PE_OK;
   const int nb = in_f / kBlock;
-  if (M <= 16 && gemv_mfma_fits(nib, (int)M, nb, n_levels)) {
+  if (M <= 16 && gemv_mfma_fits(nib, (int)M, out_f, nb, n_levels)) {
     DecArgs a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels, x, ldx, y,
-              out_f, reinterpret_cast<const uint16_t*>(bias), (int)M, out_f, nb};
+              out_f, reinterpret_cast<const uint16_t*>(bias), (int)M, out_f, nb,
+              wlayout(nib, tiled, nb)};
     return gemv_mfma(nib, true, a, st);
   }
-  if (M == 1 && in_f <= gemv1_max_kp(nib)) {
+  if (M == 1 && !tiled && in_f <= gemv1_max_kp(nib)) {
     Gemv1Args a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels, x, y,
                 reinterpret_cast<const uint16_t*>(bias), out_f, nb};
     return gemv1(nib, XM_RAW_F16, OM_F16, a, st);
@@ -103,9 +109,9 @@ extern "C" int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f
   char* ws = reinterpret_cast<char*>(workspace);
   const size_t xtf_bytes = round_up((size_t)M * in_f * 2, 256);
   if (int rc = fwht128(x, x_dtype, M, in_f, ldx, ws, PE_XTF_PAIR_F16, st)) return rc;
-  return mm_xtf(nib, codes, norms_f16, ct_scaled, n_levels, ws, M, out_f, nb, y, OM_F16, out_f,
-                reinterpret_cast<const uint16_t*>(bias), ws + xtf_bytes, workspace_bytes - xtf_bytes,
-                st);
+  return mm_xtf(nib, tiled, codes, norms_f16, ct_scaled, n_levels, ws, M, out_f, nb, y, OM_F16,
+                out_f, reinterpret_cast<const uint16_t*>(bias), ws + xtf_bytes,
+                workspace_bytes - xtf_bytes, st);
 }
 
 extern "C" size_t pe_polar_matmul_workspace_size(int64_t M, int in_f_padded) {
@@ -121,6 +127,7 @@ extern "C" int pe_polar_matmul(const void* codes, int packed, const float* x_tf,
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (!codes || !x_tf || !norms_f16 || !ct_scaled || !out) return PE_ERR_NULL;
   if (M < 0 || out_f <= 0 || in_f_padded <= 0 || in_f_padded % kBlock) return PE_ERR_DIMS;
+  if (packed & ~PE_PACK_NIBBLE) return PE_ERR_BITS;  // reference layout only
   const bool nib = packed != 0;
   if (n_levels < 2 || n_levels > (nib ? 16 : 256) || (n_levels & (n_levels - 1))) return PE_ERR_BITS;
   if (!aligned16(codes) || !aligned16(x_tf)) return PE_ERR_ALIGN;
@@ -136,6 +143,6 @@ extern "C" int pe_polar_matmul(const void* codes, int packed, const float* x_tf,
   if (!aligned16(workspace)) return PE_ERR_ALIGN;
   if (int rc = repack_pair(x_tf, M, in_f_padded, workspace, st)) return rc;
   char* ws = reinterpret_cast<char*>(workspace);
-  return mm_xtf(nib, codes, norms_f16, ct_scaled, n_levels, ws, M, out_f, nb, out, OM_F32, out_f,
-                nullptr, ws + need, workspace_bytes - need, st);
+  return mm_xtf(nib, false, codes, norms_f16, ct_scaled, n_levels, ws, M, out_f, nb, out, OM_F32,
+                out_f, nullptr, ws + need, workspace_bytes - need, st);
 }

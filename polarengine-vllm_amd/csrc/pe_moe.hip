@@ -239,7 +239,8 @@ extern "C" int pe_moe_forward(const void* x, int64_t T, int H, int I, int E, int
   for (int which = 0; which < 2; ++which) {
     const int bits = which ? bits2 : bits13, packed = which ? packed2 : packed13;
     const int nl = which ? n_levels2 : n_levels13;
-    if (bits < 2 || bits > 8 || (packed && bits > 4) || nl != (1 << bits)) return PE_ERR_BITS;
+    if (bits < 2 || bits > 8 || (packed & ~1) || (packed && bits > 4) || nl != (1 << bits))
+      return PE_ERR_BITS;  // experts stay row-major (no PE_LAYOUT_TILE16)
   }
   if (!aligned16(x) || !aligned16(w13_codes) || !aligned16(w2_codes) || !aligned16(out))
     return PE_ERR_ALIGN;
@@ -276,7 +277,7 @@ extern "C" int pe_moe_forward(const void* x, int64_t T, int H, int I, int E, int
     SmallArgs a{reinterpret_cast<const uint8_t*>(w13_codes), w13_norms, ct13, n_levels13,
                 reinterpret_cast<const uint32_t*>(ws + L.xtf), sorted_token, offsets,
                 2 * (int64_t)I * row13, 2 * (int64_t)I * nb13, ws + L.h, Ip, nullptr, 0, I,
-                nb13};
+                nb13, wlayout(nib13, false, nb13)};
     if (int rc = gemm_small(nib13, SE_SWIGLU, a, E, st)) return rc;
   }
   // 4. h -> pair f16
@@ -285,7 +286,8 @@ extern "C" int pe_moe_forward(const void* x, int64_t T, int H, int I, int E, int
   {
     SmallArgs a{reinterpret_cast<const uint8_t*>(w2_codes), w2_norms, ct2, n_levels2,
                 reinterpret_cast<const uint32_t*>(ws + L.htf), nullptr, offsets,
-                (int64_t)H * row2, (int64_t)H * nb2, ws + L.y2, H, nullptr, 0, H, nb2};
+                (int64_t)H * row2, (int64_t)H * nb2, ws + L.y2, H, nullptr, 0, H, nb2,
+                wlayout(nib2, false, nb2)};
     if (int rc = gemm_small(nib2, SE_F32, a, E, st)) return rc;
   }
   // 6. weighted combine -> out fp16

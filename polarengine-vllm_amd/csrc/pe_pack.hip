@@ -7,6 +7,8 @@
 //    packing.py:22-60.
 //  * pe_unpack_q5: on-disk LSB-first Q5 (8 codes in 5 bytes) -> int8 codes.
 //    Replaces unpack_codes_q5 (packing.py:163-209) used by loader.py:412-417.
+//  * pe_tile_weights: row-major codes/norms -> the tiled-16 runtime layout
+//    (16 rows x one block contiguous), rows padded to 16 with zeros.
 //
 // One lane per 16 output bytes; both are pure streaming kernels.
 
@@ -57,7 +59,60 @@ __global__ __launch_bounds__(256) void unpack_q5_kernel(const uint8_t* __restric
   *reinterpret_cast<uint2*>(codes + t * 8) = make_uint2(w0, w1);
 }
 
+// lane t moves 16 bytes of codes: destination chunk t of codes_t
+// [tiles][nb][16][bpb], source row tile*16 + r, block b, bytes c*16 .. +15
+__global__ __launch_bounds__(256) void tile_codes_kernel(const uint8_t* __restrict__ codes,
+                                                         uint8_t* __restrict__ codes_t,
+                                                         int64_t N, int row_bytes, int nb,
+                                                         int64_t chunks) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= chunks) return;
+  const int bpb16 = row_bytes / nb / 16;  // 16-byte chunks per block (4 or 8)
+  const int64_t c = t % bpb16;
+  int64_t u = t / bpb16;
+  const int r = (int)(u & 15);
+  u >>= 4;
+  const int64_t b = u % nb, tile = u / nb;
+  const int64_t n = tile * 16 + r;
+  uint4 v = make_uint4(0u, 0u, 0u, 0u);
+  if (n < N) v = *reinterpret_cast<const uint4*>(codes + n * row_bytes + b * (bpb16 * 16) + c * 16);
+  *reinterpret_cast<uint4*>(codes_t + t * 16) = v;
+}
+
+// lane t writes norms_t[t] of [tiles][nb][16]
+__global__ __launch_bounds__(256) void tile_norms_kernel(const uint16_t* __restrict__ norms,
+                                                         uint16_t* __restrict__ norms_t,
+                                                         int64_t N, int nb, int64_t total) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= total) return;
+  const int r = (int)(t & 15);
+  const int64_t u = t >> 4;
+  const int64_t b = u % nb, tile = u / nb;
+  const int64_t n = tile * 16 + r;
+  norms_t[t] = n < N ? norms[n * nb + b] : (uint16_t)0;
+}
+
 }  // namespace pe
+
+extern "C" int pe_tile_weights(const void* codes, const uint16_t* norms, int64_t N, int row_bytes,
+                               int nb, void* codes_t, uint16_t* norms_t, void* stream) {
+  if (!codes || !norms || !codes_t || !norms_t) return PE_ERR_NULL;
+  if (N <= 0 || nb <= 0 || row_bytes <= 0) return PE_ERR_DIMS;
+  if (row_bytes != nb * 64 && row_bytes != nb * pe::kBlock) return PE_ERR_DIMS;
+  if (!pe::aligned16(codes) || !pe::aligned16(codes_t)) return PE_ERR_ALIGN;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int64_t tiles = (N + 15) / 16;
+  const int64_t chunks = tiles * 16 * row_bytes / 16;
+  const int64_t nnorm = tiles * 16 * nb;
+  if (chunks > (int64_t(1) << 31) || nnorm > (int64_t(1) << 31)) return PE_ERR_DIMS;
+  pe::tile_codes_kernel<<<dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, st>>>(
+      reinterpret_cast<const uint8_t*>(codes), reinterpret_cast<uint8_t*>(codes_t), N, row_bytes,
+      nb, chunks);
+  if (int rc = pe::launch_status()) return rc;
+  pe::tile_norms_kernel<<<dim3((unsigned)((nnorm + 255) / 256)), dim3(256), 0, st>>>(
+      norms, norms_t, N, nb, nnorm);
+  return pe::launch_status();
+}
 
 extern "C" int pe_pack_nibble(const int8_t* codes, uint8_t* packed, int64_t rows, int64_t K,
                               void* stream) {

@@ -20,6 +20,7 @@ LIB_PATH = os.environ.get(
 )
 
 PE_OK = 0
+PE_PACK_NIBBLE, PE_LAYOUT_TILE16 = 1, 2
 PE_DTYPE_F16, PE_DTYPE_BF16, PE_DTYPE_F32 = 0, 1, 2
 PE_XTF_F32, PE_XTF_F16, PE_XTF_PAIR_F16, PE_XTF_BF16 = 0, 1, 2, 3
 
@@ -43,6 +44,7 @@ _SIGNATURES = {
                                        _vp, _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
     "pe_pack_nibble": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
     "pe_unpack_q5": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
+    "pe_tile_weights": (_c_int, [_vp, _vp, _c_i64, _c_int, _c_int, _vp, _vp, _vp]),
     "pe_moe_route": (_c_int, [_vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp]),
     "pe_moe_workspace_size": (_c_sz, [_c_i64, _c_int, _c_int, _c_int, _c_int]),
     "pe_moe_forward": (_c_int, [_vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp, _vp,

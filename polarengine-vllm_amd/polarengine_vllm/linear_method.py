@@ -80,6 +80,7 @@ class PolarQuantLinearMethod:
         layer.bits = self.bits
         layer.block_size = bs
         layer.packed = False
+        layer.tiled = False
         set_weight_attrs(layer.codes, {"input_dim": 1, "output_dim": 0})
         set_weight_attrs(layer.norms, {"input_dim": 1, "output_dim": 0})
 
@@ -87,8 +88,10 @@ class PolarQuantLinearMethod:
     def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
         """Move ct to the codes' device; nibble-pack bits <= 4 on the GPU
         (``pe_pack_nibble``) and free the int8 codes
-        (reference: linear_method.py:228-258)."""
-        device = layer.codes.device
+        (reference: linear_method.py:228-258); then re-lay codes and norms out
+        in the tiled-16 runtime layout (``pe_tile_weights``: one 16-row x
+        block tile is one contiguous read for the decode and GEMM kernels)."""
+        device = layer.codes.device if hasattr(layer, "codes") else layer.codes_packed.device
         layer.ct_scaled = layer.ct_scaled.to(device=device, dtype=torch.float32).contiguous()
         if layer.norms.dtype != torch.float16:
             layer.norms = layer.norms.to(torch.float16)
@@ -101,6 +104,13 @@ class PolarQuantLinearMethod:
             del layer.codes
             logger.debug("packed codes to nibbles: out_f=%d in_f_half=%d bits=%d",
                          layer.out_f, layer.in_f_half, layer.bits)
+        if not getattr(layer, "tiled", False):
+            from polarengine_vllm.packing import tile_weights_16
+            name = "codes_packed" if layer.packed else "codes"
+            codes_t, norms_t = tile_weights_16(getattr(layer, name), layer.norms)
+            setattr(layer, name, codes_t)
+            layer.norms = norms_t
+            layer.tiled = True
 
     # ------------------------------------------------------------------
     def apply(self, layer: torch.nn.Module, x: torch.Tensor,
@@ -124,6 +134,8 @@ class PolarQuantLinearMethod:
         st = _lib.stream_ptr(dev)
         n_levels = layer.ct_scaled.numel()
         kp = layer.in_f_padded
+        fmt = (_lib.PE_PACK_NIBBLE if packed else 0) | (
+            _lib.PE_LAYOUT_TILE16 if getattr(layer, "tiled", False) else 0)
 
         if m >= _SHARE_FWHT_MIN_M:
             x_tf = self._fwht_cache.get(x, layer.in_f)
@@ -131,21 +143,21 @@ class PolarQuantLinearMethod:
                 xp = x2 if kp == layer.in_f else F.pad(x2, (0, kp - layer.in_f))
                 x_tf = fwht_pairs(xp)
                 self._fwht_cache.put(x, layer.in_f, x_tf)
-            ws_bytes = L.pe_linear_xtf_workspace_size(m, kp, layer.out_f, layer.bits, int(packed))
+            ws_bytes = L.pe_linear_xtf_workspace_size(m, kp, layer.out_f, layer.bits, fmt)
             ws = _lib.workspace(dev, ws_bytes)
             rc = L.pe_linear_forward_xtf(
-                x_tf.data_ptr(), m, kp, codes.data_ptr(), layer.bits, int(packed),
+                x_tf.data_ptr(), m, kp, codes.data_ptr(), layer.bits, fmt,
                 layer.norms.data_ptr(), layer.ct_scaled.data_ptr(), n_levels, _lib.ptr(b),
                 _lib.PE_DTYPE_F16, y.data_ptr(), layer.out_f, _lib.ptr(ws), ws_bytes, st)
             _lib.check(rc, "pe_linear_forward_xtf")
         else:
             xc = x2 if kp == layer.in_f else F.pad(x2, (0, kp - layer.in_f))
             xc = xc.contiguous()
-            ws_bytes = L.pe_linear_workspace_size(m, kp, layer.out_f, layer.bits, int(packed))
+            ws_bytes = L.pe_linear_workspace_size(m, kp, layer.out_f, layer.bits, fmt)
             ws = _lib.workspace(dev, ws_bytes)
             rc = L.pe_linear_forward(
                 xc.data_ptr(), _lib.PE_DTYPE_F16, m, kp, kp, codes.data_ptr(), layer.bits,
-                int(packed), layer.norms.data_ptr(), layer.ct_scaled.data_ptr(), n_levels,
+                fmt, layer.norms.data_ptr(), layer.ct_scaled.data_ptr(), n_levels,
                 _lib.ptr(b), y.data_ptr(), layer.out_f, _lib.ptr(ws), ws_bytes, st)
             _lib.check(rc, "pe_linear_forward")
         return y.view(*orig_shape[:-1], layer.out_f)

@@ -46,6 +46,27 @@ def pack_codes_half_block(codes: torch.Tensor, block_size: int = 128) -> torch.T
     return ((b[..., half:] << 4) | b[..., :half]).reshape(*lead, k // 2)
 
 
+def tile_weights_16(codes: torch.Tensor, norms: torch.Tensor):
+    """Runtime tiled-16 layout of one matrix (``pe_tile_weights``, GPU only):
+    codes [N, row_bytes] -> [ceil(N/16)*16, row_bytes] holding
+    [tiles][nb][16][bpb], norms [N, nb] -> [ceil(N/16)*16, nb] holding
+    [tiles][nb][16]; padded rows are zero. The shapes keep two dims so the
+    buffers still read as rows x bytes."""
+    from polarengine_vllm import _lib
+    dev = _lib.require_device(codes, norms)
+    n, row_bytes = codes.shape
+    nb = norms.shape[1]
+    npad = (n + 15) // 16 * 16
+    src = codes.contiguous()
+    nsrc = norms.to(torch.float16).contiguous()
+    codes_t = torch.empty(npad, row_bytes, dtype=codes.dtype, device=dev)
+    norms_t = torch.empty(npad, nb, dtype=torch.float16, device=dev)
+    _lib.check(_lib.lib().pe_tile_weights(src.data_ptr(), nsrc.data_ptr(), n, row_bytes, nb,
+                                          codes_t.data_ptr(), norms_t.data_ptr(),
+                                          _lib.stream_ptr(dev)), "pe_tile_weights")
+    return codes_t, norms_t
+
+
 def unpack_codes_half_block(packed: torch.Tensor, block_size: int = 128) -> torch.Tensor:
     """uint8 [..., K/2] -> int8 codes [..., K]."""
     assert block_size % 2 == 0, f"block_size must be even, got {block_size}"

@@ -308,6 +308,75 @@ def test_decode_indexing_probe_bit_exact(bits):
 
 
 # ---------------------------------------------------------------------------
+# Tiled-16 runtime layout (what process_weights_after_loading produces)
+# ---------------------------------------------------------------------------
+
+def tile16_np(codes_rt, norms):
+    """numpy statement of the tiled-16 layout: [tiles][nb][16][bpb] and [tiles][nb][16]."""
+    n, row_bytes = codes_rt.shape
+    nb = norms.shape[1]
+    bpb = row_bytes // nb
+    npad = (n + 15) // 16 * 16
+    c = np.zeros((npad, row_bytes), dtype=codes_rt.dtype)
+    c[:n] = codes_rt
+    g = np.zeros((npad, nb), dtype=norms.dtype)
+    g[:n] = norms
+    ct = c.reshape(npad // 16, 16, nb, bpb).transpose(0, 2, 1, 3).reshape(npad, row_bytes)
+    gt = g.reshape(npad // 16, 16, nb).transpose(0, 2, 1).reshape(npad, nb)
+    return np.ascontiguousarray(ct), np.ascontiguousarray(gt)
+
+
+def dev_tiled(codes, norms, bits):
+    from polarengine_vllm.packing import tile_weights_16
+    dcodes, nib = dev_codes(codes, bits)
+    ct, nt = tile_weights_16(dcodes, to_dev(norms))
+    return ct, nt, nib
+
+
+@pytest.mark.parametrize("n,k,bits", [(37, 384, 4), (64, 256, 6), (1000, 1408, 3), (16, 128, 8)])
+def test_tile_weights_bit_exact(n, k, bits):
+    _say(f"tile16 n={n} k={k} bits={bits}")
+    rng = np.random.default_rng(n + k)
+    codes, norms, _ = rand_layer(rng, n, k, bits)
+    rt = O.pack_nibble(codes) if bits <= 4 else codes
+    want_c, want_n = tile16_np(np.asarray(rt), norms)
+    ct, nt, _ = dev_tiled(codes, norms, bits)
+    torch.cuda.synchronize()
+    assert np.array_equal(ct.cpu().numpy().view(np.uint8), want_c.view(np.uint8))
+    assert np.array_equal(nt.cpu().numpy().view(np.uint16), want_n.view(np.uint16))
+
+
+TILED_CASES = [(1, 12288, 4096, 4), (1, 4096, 12288, 3), (1, 1000, 1408, 5), (4, 257, 384, 2),
+               (16, 4096, 2048, 4), (16, 4096, 4096, 4), (33, 1000, 1408, 6), (256, 1536, 1024, 4),
+               (300, 200, 640, 8), (1, 48, 256, 6)]
+
+
+@pytest.mark.parametrize("m,n,k,bits", TILED_CASES)
+def test_linear_forward_tiled_layout(m, n, k, bits):
+    """Every dispatch (decode, small GEMM, prefill GEMM) on the tiled-16 layout."""
+    from polarengine_vllm import _lib
+    _say(f"tiled linear m={m} n={n} k={k} bits={bits}")
+    rng = np.random.default_rng(m * 7 + n + k + bits)
+    codes, norms, ct = rand_layer(rng, n, k, bits)
+    x = O.seeded_normal((m, k), 1.0, 70 + m)
+    bias = O.seeded_normal((n,), 0.1, 71)
+    want = O.linear_apply(x, codes, norms, ct, k, bias).astype(np.float32)
+    dcodes, dnorms, nib = dev_tiled(codes, norms, bits)
+    fmt = (_lib.PE_PACK_NIBBLE if nib else 0) | _lib.PE_LAYOUT_TILE16
+    xd, cd, bd = to_dev(x), to_dev(ct), to_dev(bias)
+    L = _lib.lib()
+    wsb = L.pe_linear_workspace_size(m, k, n, bits, fmt)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+    y = torch.empty(m, n, dtype=torch.float16, device=DEV)
+    rc = L.pe_linear_forward(xd.data_ptr(), 0, m, k, k, dcodes.data_ptr(), bits, fmt,
+                             dnorms.data_ptr(), cd.data_ptr(), 1 << bits, bd.data_ptr(),
+                             y.data_ptr(), n, ws.data_ptr(), wsb, _lib.stream_ptr(torch.device(DEV)))
+    torch.cuda.synchronize()
+    _lib.check(rc, "pe_linear_forward")
+    check_close(y.float().cpu().numpy(), want, f"tiled {m}x{n}x{k} q{bits}")
+
+
+# ---------------------------------------------------------------------------
 # Batched (M > 1): reference API polar_matmul (f32 out) and the MFMA GEMM
 # ---------------------------------------------------------------------------
 
