@@ -338,11 +338,12 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
 // host launch
 // ---------------------------------------------------------------------------
 
-// waves per workgroup: TN tiles x KS K-slices, at most 16 and at least 8 (the
-// table fill covers 256 entries with two per wave) -- one workgroup per CU
-constexpr int kDecMaxW = 16;
+// waves per workgroup: TN tiles x KS K-slices = 12 (one workgroup per CU;
+// measured better than 15-16 waves: fewer competing streams per CU); at least
+// 8 so that the table fill covers 256 entries with two per wave
+constexpr int kDecW = 12;
 template <int TN>
-constexpr int dec_ks() { return kDecMaxW / TN; }
+constexpr int dec_ks() { return kDecW / TN; }
 
 // activation registers per lane: M * nb items of 16 x 16 B over the 4 NW
 // 16-lane groups of the workgroup
@@ -357,7 +358,7 @@ static size_t dec_lds(bool nibble, int M, int nb, int n_levels, int nw) {
 template <bool NIB, int TN, bool XRAW, bool MASK, int XC>
 static int launch_dec(const DecArgs& a, hipStream_t st) {
   constexpr int KS = dec_ks<TN>(), NW = TN * KS;
-  constexpr int D = NIB ? 4 : 2;  // blocks in flight per wave (nibble 1 KB, int8 2 KB each)
+  constexpr int D = NIB ? 3 : 2;  // blocks in flight per wave (nibble 1 KB, int8 2 KB each)
   auto kern = gemv_mfma_kernel<NIB, TN, KS, XRAW, MASK, XC, D>;
   const size_t lds = dec_lds(NIB, a.M, a.nb, a.n_levels, NW);
   if (lds > 160 * 1024 || dec_xc(a.M, a.nb, NW) > XC) return PE_ERR_DIMS;
@@ -419,12 +420,12 @@ static int launch_dec_m(const DecArgs& a, hipStream_t st) {
 }
 
 bool gemv_mfma_fits(bool nibble, int M, int N, int nb, int n_levels) {
-  // the smallest workgroup (15 waves, TN = 3) bounds the activation registers
-  if (M < 1 || M > 16 || dec_xc(M, nb, 15) > 8) return false;
+  // the workgroup's 4 * kDecW lane groups hold the activations in <= 8 registers
+  if (M < 1 || M > 16 || dec_xc(M, nb, kDecW) > 8) return false;
   // buffer resources address codes and norms with 31-bit offsets (tiled
   // layouts round N up to 16 rows)
   if ((int64_t)(N + 15) * nb * (nibble ? 64 : kBlock) >= (int64_t)1 << 31) return false;
-  return dec_lds(nibble, M, nb, n_levels, kDecMaxW) <= 160 * 1024;
+  return dec_lds(nibble, M, nb, n_levels, kDecW) <= 160 * 1024;
 }
 
 int gemv_mfma(bool nibble, bool xraw, const DecArgs& a, hipStream_t st) {
