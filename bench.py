@@ -69,6 +69,7 @@ class Linear:
         # the runtime layout process_weights_after_loading produces
         self.codes, self.norms = tile_weights_16(codes, norms)
         del codes, norms
+        self.ct_host = np.ascontiguousarray(self.ct.cpu().numpy(), dtype=np.float32)
         self.packed = (_lib.PE_PACK_NIBBLE if bits <= 4 else 0) | _lib.PE_LAYOUT_TILE16
         self.x = x if x is not None else torch.randn(m, k, device=dev, dtype=torch.float16)
         self.y = torch.empty(m, n, device=dev, dtype=torch.float16)
@@ -81,7 +82,8 @@ class Linear:
         L = _lib.lib()
         rc = L.pe_linear_forward(self.x.data_ptr(), 0, self.m, self.k, self.k,
                                  self.codes.data_ptr(), self.bits, self.packed,
-                                 self.norms.data_ptr(), self.ct.data_ptr(), 1 << self.bits, None,
+                                 self.norms.data_ptr(), self.ct.data_ptr(),
+                                 self.ct_host.ctypes.data, 1 << self.bits, None,
                                  self.y.data_ptr(), self.n, self.ws.data_ptr(), self.wsb,
                                  _lib.stream_ptr(self.dev))
         if rc:

@@ -123,6 +123,9 @@ int pe_polar_matmul(const void* codes, int packed, const float* x_tf, int64_t M,
  *   x      : [M, in_f] in x_dtype (PE_DTYPE_F16), row stride ldx
  *   codes  : runtime layout for (bits, packed); packed = PE_PACK_NIBBLE for
  *            nibble codes, | PE_LAYOUT_TILE16 for the tiled-16 layout
+ *   ct_host: NULL, or a host copy of ct_scaled (n_levels floats, equal to the
+ *            device values); the decode kernel then takes the codebook by
+ *            value in its kernel arguments instead of reading ct_scaled
  *   bias   : NULL or [out_f] in x_dtype
  *   y      : [M, out_f] in x_dtype, row stride out_f
  * Needs pe_linear_workspace_size(...) bytes of workspace (0 is valid when the
@@ -131,20 +134,21 @@ int pe_polar_matmul(const void* codes, int packed, const float* x_tf, int64_t M,
 size_t pe_linear_workspace_size(int64_t M, int in_f, int out_f, int bits, int packed);
 int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f, int64_t ldx,
                       const void* codes, int bits, int packed, const uint16_t* norms_f16,
-                      const float* ct_scaled, int n_levels, const void* bias, void* y,
-                      int out_f, void* workspace, size_t workspace_bytes, void* stream);
+                      const float* ct_scaled, const float* ct_host, int n_levels,
+                      const void* bias, void* y, int out_f, void* workspace,
+                      size_t workspace_bytes, void* stream);
 
 /*
  * Same, starting from an already-transformed activation in the pair-f16
  * layout (the FWHTCache hit of linear_method.py:190-197, shared by Q/K/V).
- * in_f_padded = 128 * nb of x_tf.
+ * in_f_padded = 128 * nb of x_tf; ct_host as for pe_linear_forward.
  */
 size_t pe_linear_xtf_workspace_size(int64_t M, int in_f_padded, int out_f, int bits, int packed);
 int pe_linear_forward_xtf(const void* x_tf_pair, int64_t M, int in_f_padded,
                           const void* codes, int bits, int packed, const uint16_t* norms_f16,
-                          const float* ct_scaled, int n_levels, const void* bias, int out_dtype,
-                          void* y, int out_f, void* workspace, size_t workspace_bytes,
-                          void* stream);
+                          const float* ct_scaled, const float* ct_host, int n_levels,
+                          const void* bias, int out_dtype, void* y, int out_f, void* workspace,
+                          size_t workspace_bytes, void* stream);
 
 /*
  * Nibble packing of int8 codes in [0, 15] (bit-exact): replaces

@@ -84,31 +84,47 @@ __device__ __forceinline__ half8v dec_dequant(uint32_t wl, uint32_t wh, uint32_t
   return __builtin_bit_cast(half8v, u32x4v{p[0], p[1], p[2], p[3]});
 }
 
-// Codebook table from wave-uniform (scalar) loads of ct, issued by every
-// wave as its first memory request (scalar loads do not queue behind the
-// vector weight stream); every lane then writes its own copy of each entry.
-// Nibble: entry (hi << 4) | lo = half2(ct[lo], ct[hi]) (the 16 loaded values
-// are the whole codebook), wave w takes hi = w and w + NW; int8: entry e = fp16(ct[e]) in the low half, wave w takes
-// e = 16 w .. 16 w + 15 and 16 (w + NW) .. + 15. NW >= 8 covers 256 entries.
+// Codebook table. The values come either by value in the kernel arguments
+// (the host passed its copy of ct: they arrive with the other arguments, no
+// dependent memory read on the critical path) or from wave-uniform scalar
+// loads of the device ct (which at least do not queue behind the vector
+// weight stream). Every lane then writes its own copy of each entry.
+// Nibble: entry (hi << 4) | lo = half2(ct[lo], ct[hi]) (the 16 values are the
+// whole codebook), wave w takes hi = w and w + NW; int8: entry e = fp16(ct[e])
+// in the low half, wave w takes e = 16 w .. 16 w + 15 and 16 (w + NW) .. + 15.
+// NW >= 8 covers 256 entries.
 template <bool NIB>
 struct DecTable {
   float c[NIB ? 16 : 32];  // nibble: ct[0..15] (clamped); int8: two 16-entry chunks
 };
 
+// Codebook by value, entries past n_levels repeat the last one.
+template <bool NIB>
+struct DecCtArg {
+  float v[NIB ? 16 : 256];
+};
+
 template <bool NIB, int NW>
 __device__ __forceinline__ void dec_table_load(DecTable<NIB>& t, const float* __restrict__ ct,
+                                               const DecCtArg<NIB>& ctv, bool by_value,
                                                int n_levels, int wave) {
   const int last = n_levels - 1;
   if constexpr (NIB) {
+    if (by_value) {
 #pragma unroll
-    for (int lo = 0; lo < 16; ++lo) t.c[lo] = ct[lo < n_levels ? lo : last];
+      for (int lo = 0; lo < 16; ++lo) t.c[lo] = ctv.v[lo];
+    } else {
+#pragma unroll
+      for (int lo = 0; lo < 16; ++lo) t.c[lo] = ct[lo < n_levels ? lo : last];
+    }
   } else {
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
         const int e = (wave + h * NW) * 16 + k;
-        t.c[h * 16 + k] = ct[e < n_levels ? e : last];
+        const int ec = e < n_levels ? e : last;
+        t.c[h * 16 + k] = by_value ? ctv.v[ec] : ct[ec];
       }
   }
 }
@@ -151,7 +167,8 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
     const float* __restrict__ ct, int n_levels, uint32_t code_mask,
     const void* __restrict__ x, int64_t ldx, void* __restrict__ y, int64_t ldy,
-    const uint16_t* __restrict__ bias, int M, int N, int nb, uint32_t xs_addr, WLayout lay) {
+    const uint16_t* __restrict__ bias, int M, int N, int nb, uint32_t xs_addr, WLayout lay,
+    DecCtArg<NIB> ctv, int ct_by_value) {
   constexpr int NW = TN * KS;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -214,7 +231,7 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
   __builtin_amdgcn_sched_barrier(0);
   // codebook values (scalar loads: they do not queue behind the weight stream)
   DecTable<NIB> tab;
-  dec_table_load<NIB, NW>(tab, ct, n_levels, wave);
+  dec_table_load<NIB, NW>(tab, ct, ctv, ct_by_value != 0, n_levels, wave);
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
@@ -370,9 +387,13 @@ static int launch_dec(const DecArgs& a, hipStream_t st) {
   const int tiles = (a.N + TN * 16 - 1) / (TN * 16);
   const uint8_t mb = NIB ? (uint8_t)((a.n_levels - 1) * 0x11) : (uint8_t)(a.n_levels - 1);
   const uint32_t xs_addr = (uint32_t)table_entries(NIB, a.n_levels) * 256u;
+  DecCtArg<NIB> ctv;
+  constexpr int kCtv = (int)(sizeof(ctv.v) / sizeof(float));
+  for (int e = 0; e < kCtv; ++e) ctv.v[e] = a.ct_host ? a.ct_host[e < a.n_levels ? e : a.n_levels - 1] : 0.f;
   kern<<<dim3(tiles), dim3(NW * 64), lds, st>>>(a.codes, a.norms, a.ct, a.n_levels,
                                                0x01010101u * mb, a.x, a.ldx, a.y, a.ldy, a.bias,
-                                               a.M, a.N, a.nb, xs_addr, a.lay);
+                                               a.M, a.N, a.nb, xs_addr, a.lay, ctv,
+                                               a.ct_host ? 1 : 0);
   return launch_status();
 }
 

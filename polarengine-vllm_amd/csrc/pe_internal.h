@@ -103,6 +103,7 @@ struct DecArgs {
   const uint16_t* bias;
   int M, N, nb;
   WLayout lay;
+  const float* ct_host;  // nullable host copy of ct (n_levels floats): codebook by value
 };
 bool gemv_mfma_fits(bool nibble, int M, int N, int nb, int n_levels);
 int gemv_mfma(bool nibble, bool xraw, const DecArgs& a, hipStream_t st);

@@ -52,9 +52,9 @@ extern "C" size_t pe_linear_workspace_size(int64_t M, int in_f, int out_f, int b
 extern "C" int pe_linear_forward_xtf(const void* x_tf_pair, int64_t M, int in_f_padded,
                                      const void* codes, int bits, int packed,
                                      const uint16_t* norms_f16, const float* ct_scaled,
-                                     int n_levels, const void* bias, int out_dtype, void* y,
-                                     int out_f, void* workspace, size_t workspace_bytes,
-                                     void* stream) {
+                                     const float* ct_host, int n_levels, const void* bias,
+                                     int out_dtype, void* y, int out_f, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (!x_tf_pair || !codes || !norms_f16 || !ct_scaled || !y) return PE_ERR_NULL;
   if (M < 0 || out_f <= 0 || in_f_padded <= 0 || in_f_padded % kBlock) return PE_ERR_DIMS;
@@ -67,7 +67,7 @@ extern "C" int pe_linear_forward_xtf(const void* x_tf_pair, int64_t M, int in_f_
   if (M <= 16 && gemv_mfma_fits(nib, (int)M, out_f, nb, n_levels)) {
     DecArgs a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels,
               x_tf_pair, (int64_t)in_f_padded, y, out_f, reinterpret_cast<const uint16_t*>(bias),
-              (int)M, out_f, nb, wlayout(nib, tiled, nb)};
+              (int)M, out_f, nb, wlayout(nib, tiled, nb), ct_host};
     return gemv_mfma(nib, false, a, st);
   }
   return mm_xtf(nib, tiled, codes, norms_f16, ct_scaled, n_levels, x_tf_pair, M, out_f, nb, y,
@@ -77,9 +77,10 @@ extern "C" int pe_linear_forward_xtf(const void* x_tf_pair, int64_t M, int in_f_
 
 extern "C" int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f, int64_t ldx,
                                  const void* codes, int bits, int packed,
-                                 const uint16_t* norms_f16, const float* ct_scaled, int n_levels,
-                                 const void* bias, void* y, int out_f, void* workspace,
-                                 size_t workspace_bytes, void* stream) {
+                                 const uint16_t* norms_f16, const float* ct_scaled,
+                                 const float* ct_host, int n_levels, const void* bias, void* y,
+                                 int out_f, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (!x || !codes || !norms_f16 || !ct_scaled || !y) return PE_ERR_NULL;
   if (M < 0 || in_f <= 0 || out_f <= 0 || ldx < in_f) return PE_ERR_DIMS;
@@ -95,7 +96,7 @@ extern "C" int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f
   if (M <= 16 && gemv_mfma_fits(nib, (int)M, out_f, nb, n_levels)) {
     DecArgs a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels, x, ldx, y,
               out_f, reinterpret_cast<const uint16_t*>(bias), (int)M, out_f, nb,
-              wlayout(nib, tiled, nb)};
+              wlayout(nib, tiled, nb), ct_host};
     return gemv_mfma(nib, true, a, st);
   }
   if (M == 1 && !tiled && in_f <= gemv1_max_kp(nib)) {

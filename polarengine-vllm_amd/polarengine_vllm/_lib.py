@@ -38,10 +38,10 @@ _SIGNATURES = {
                                  _vp, _c_sz, _vp]),
     "pe_linear_workspace_size": (_c_sz, [_c_i64, _c_int, _c_int, _c_int, _c_int]),
     "pe_linear_forward": (_c_int, [_vp, _c_int, _c_i64, _c_int, _c_i64, _vp, _c_int, _c_int, _vp,
-                                   _vp, _c_int, _vp, _vp, _c_int, _vp, _c_sz, _vp]),
+                                   _vp, _vp, _c_int, _vp, _vp, _c_int, _vp, _c_sz, _vp]),
     "pe_linear_xtf_workspace_size": (_c_sz, [_c_i64, _c_int, _c_int, _c_int, _c_int]),
-    "pe_linear_forward_xtf": (_c_int, [_vp, _c_i64, _c_int, _vp, _c_int, _c_int, _vp, _vp, _c_int,
-                                       _vp, _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
+    "pe_linear_forward_xtf": (_c_int, [_vp, _c_i64, _c_int, _vp, _c_int, _c_int, _vp, _vp, _vp,
+                                       _c_int, _vp, _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
     "pe_pack_nibble": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
     "pe_unpack_q5": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
     "pe_tile_weights": (_c_int, [_vp, _vp, _c_i64, _c_int, _c_int, _vp, _vp, _vp]),

@@ -25,6 +25,7 @@ import logging
 import math
 from typing import Any, Dict, Optional
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 
@@ -93,6 +94,8 @@ class PolarQuantLinearMethod:
         block tile is one contiguous read for the decode and GEMM kernels)."""
         device = layer.codes.device if hasattr(layer, "codes") else layer.codes_packed.device
         layer.ct_scaled = layer.ct_scaled.to(device=device, dtype=torch.float32).contiguous()
+        # host copy of the codebook: the decode kernel takes it by value
+        layer.ct_host = np.ascontiguousarray(layer.ct_scaled.cpu().numpy(), dtype=np.float32)
         if layer.norms.dtype != torch.float16:
             layer.norms = layer.norms.to(torch.float16)
         layer.norms = layer.norms.contiguous()
@@ -134,6 +137,8 @@ class PolarQuantLinearMethod:
         st = _lib.stream_ptr(dev)
         n_levels = layer.ct_scaled.numel()
         kp = layer.in_f_padded
+        ct_host = getattr(layer, "ct_host", None)
+        ct_host = None if ct_host is None else ct_host.ctypes.data
         fmt = (_lib.PE_PACK_NIBBLE if packed else 0) | (
             _lib.PE_LAYOUT_TILE16 if getattr(layer, "tiled", False) else 0)
 
@@ -147,7 +152,7 @@ class PolarQuantLinearMethod:
             ws = _lib.workspace(dev, ws_bytes)
             rc = L.pe_linear_forward_xtf(
                 x_tf.data_ptr(), m, kp, codes.data_ptr(), layer.bits, fmt,
-                layer.norms.data_ptr(), layer.ct_scaled.data_ptr(), n_levels, _lib.ptr(b),
+                layer.norms.data_ptr(), layer.ct_scaled.data_ptr(), ct_host, n_levels, _lib.ptr(b),
                 _lib.PE_DTYPE_F16, y.data_ptr(), layer.out_f, _lib.ptr(ws), ws_bytes, st)
             _lib.check(rc, "pe_linear_forward_xtf")
         else:
@@ -157,7 +162,7 @@ class PolarQuantLinearMethod:
             ws = _lib.workspace(dev, ws_bytes)
             rc = L.pe_linear_forward(
                 xc.data_ptr(), _lib.PE_DTYPE_F16, m, kp, kp, codes.data_ptr(), layer.bits,
-                fmt, layer.norms.data_ptr(), layer.ct_scaled.data_ptr(), n_levels,
+                fmt, layer.norms.data_ptr(), layer.ct_scaled.data_ptr(), ct_host, n_levels,
                 _lib.ptr(b), y.data_ptr(), layer.out_f, _lib.ptr(ws), ws_bytes, st)
             _lib.check(rc, "pe_linear_forward")
         return y.view(*orig_shape[:-1], layer.out_f)

@@ -60,7 +60,10 @@ def test_argument_errors_without_gpu_work():
     # misaligned
     assert L.pe_pack_nibble(17, 16, 1, 128, None) == 4
     # bad bits / packing combination
-    assert L.pe_linear_forward(16, 0, 1, 128, 128, 16, 5, 1, 16, 16, 32, None, 16, 8,
+    assert L.pe_linear_forward(16, 0, 1, 128, 128, 16, 5, 1, 16, 16, None, 32, None, 16, 8,
+                               None, 0, None) == 3
+    # unknown weight-format flag
+    assert L.pe_linear_forward(16, 0, 1, 128, 128, 16, 4, 4, 16, 16, None, 16, None, 16, 8,
                                None, 0, None) == 3
 
 

@@ -193,7 +193,7 @@ def test_linear_forward_m1(n, k, bits):
     y = torch.empty(1, n, dtype=torch.float16, device=DEV)
     L = _lib.lib()
     rc = L.pe_linear_forward(xd.data_ptr(), 0, 1, kp, kp, dcodes.data_ptr(), bits, int(nib),
-                             nd.data_ptr(), cd.data_ptr(), 1 << bits, bd.data_ptr(),
+                             nd.data_ptr(), cd.data_ptr(), None, 1 << bits, bd.data_ptr(),
                              y.data_ptr(), n, None, 0, _lib.stream_ptr(torch.device(DEV)))
     torch.cuda.synchronize()
     _lib.check(rc, "pe_linear_forward")
@@ -238,18 +238,20 @@ def test_decode_linear_forward(m, n, k, bits):
     L = _lib.lib()
     wsb = L.pe_linear_workspace_size(m, k, n, bits, int(nib))
     ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+    ct_host = np.ascontiguousarray(ct, dtype=np.float32)  # codebook by value
     outs = []
-    for _ in range(2):
+    for host in (None, ct_host.ctypes.data, None):
         y = torch.empty(m, n, dtype=torch.float16, device=DEV)
         rc = L.pe_linear_forward(xd.data_ptr(), 0, m, k, ldx, dcodes.data_ptr(), bits, int(nib),
-                                 nd.data_ptr(), cd.data_ptr(), 1 << bits, bd.data_ptr(),
+                                 nd.data_ptr(), cd.data_ptr(), host, 1 << bits, bd.data_ptr(),
                                  y.data_ptr(), n, ws.data_ptr(), wsb,
                                  _lib.stream_ptr(torch.device(DEV)))
         torch.cuda.synchronize()
         _lib.check(rc, "pe_linear_forward")
         outs.append(y)
     check_close(outs[0].float().cpu().numpy(), want, f"decode {m}x{n}x{k} q{bits}")
-    assert torch.equal(outs[0], outs[1]), "non-deterministic"
+    assert torch.equal(outs[0], outs[2]), "non-deterministic"
+    assert torch.equal(outs[0], outs[1]), "codebook by value differs from the device codebook"
 
 
 @pytest.mark.parametrize("m,n,k,bits", [(1, 12288, 4096, 4), (4, 1000, 1408, 3),
@@ -270,7 +272,7 @@ def test_decode_linear_forward_xtf(m, n, k, bits):
     ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
     y = torch.empty(m, n, dtype=torch.float16, device=DEV)
     rc = L.pe_linear_forward_xtf(xp.data_ptr(), m, k, dcodes.data_ptr(), bits, int(nib),
-                                 nd.data_ptr(), cd.data_ptr(), 1 << bits, None, 0,
+                                 nd.data_ptr(), cd.data_ptr(), None, 1 << bits, None, 0,
                                  y.data_ptr(), n, ws.data_ptr(), wsb,
                                  _lib.stream_ptr(torch.device(DEV)))
     torch.cuda.synchronize()
@@ -289,6 +291,7 @@ def test_decode_indexing_probe_bit_exact(bits):
     norms = np.ones((n, kp // 128), dtype=np.float16)
     dcodes, nib = dev_codes(codes, bits)
     ct16 = ct.astype(np.float16)
+    ct_host = np.ascontiguousarray(ct, dtype=np.float32)  # codebook by value
     nd, cd = to_dev(norms), to_dev(ct)
     L = _lib.lib()
     ks = [0, 1, 15, 16, 17, 63, 64, 65, 100, 127, 133, 448, 575, 700, kp - 1]
@@ -299,7 +302,8 @@ def test_decode_indexing_probe_bit_exact(bits):
         xp = to_dev(pair_f16(x_tf))
         y = torch.empty(m, n, dtype=torch.float16, device=DEV)
         rc = L.pe_linear_forward_xtf(xp.data_ptr(), m, kp, dcodes.data_ptr(), bits, int(nib),
-                                     nd.data_ptr(), cd.data_ptr(), 1 << bits, None, 0,
+                                     nd.data_ptr(), cd.data_ptr(), ct_host.ctypes.data, 1 << bits,
+                                     None, 0,
                                      y.data_ptr(), n, None, 0, _lib.stream_ptr(torch.device(DEV)))
         torch.cuda.synchronize()
         _lib.check(rc, "pe_linear_forward_xtf")
@@ -368,8 +372,10 @@ def test_linear_forward_tiled_layout(m, n, k, bits):
     wsb = L.pe_linear_workspace_size(m, k, n, bits, fmt)
     ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
     y = torch.empty(m, n, dtype=torch.float16, device=DEV)
+    ct_host = np.ascontiguousarray(ct, dtype=np.float32)
     rc = L.pe_linear_forward(xd.data_ptr(), 0, m, k, k, dcodes.data_ptr(), bits, fmt,
-                             dnorms.data_ptr(), cd.data_ptr(), 1 << bits, bd.data_ptr(),
+                             dnorms.data_ptr(), cd.data_ptr(), ct_host.ctypes.data, 1 << bits,
+                             bd.data_ptr(),
                              y.data_ptr(), n, ws.data_ptr(), wsb, _lib.stream_ptr(torch.device(DEV)))
     torch.cuda.synchronize()
     _lib.check(rc, "pe_linear_forward")
@@ -417,7 +423,7 @@ def test_prefill_gemm_full_size_row_sample(m, n, k, bits):
     ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
     xd, nd, cd = to_dev(x), to_dev(norms), to_dev(ct)
     rc = L.pe_linear_forward(xd.data_ptr(), 0, m, k, k, dcodes.data_ptr(), bits, int(nib),
-                             nd.data_ptr(), cd.data_ptr(), 1 << bits, None,
+                             nd.data_ptr(), cd.data_ptr(), None, 1 << bits, None,
                              y.data_ptr(), n, ws.data_ptr(), wsb,
                              _lib.stream_ptr(torch.device(DEV)))
     torch.cuda.synchronize()
@@ -511,7 +517,8 @@ def test_graph_replay_matches_eager():
     def run(a):
         x, dc, nr, ct, y, ws, wsb, m, n, k, bits, nib = a
         _lib.check(L.pe_linear_forward(x.data_ptr(), 0, m, k, k, dc.data_ptr(), bits, int(nib),
-                                       nr.data_ptr(), ct.data_ptr(), 1 << bits, None, y.data_ptr(),
+                                       nr.data_ptr(), ct.data_ptr(), None, 1 << bits, None,
+                                       y.data_ptr(),
                                        n, ws.data_ptr(), wsb, st()), "pe_linear_forward")
 
     eager = []
