@@ -282,12 +282,45 @@ static int launch_gemm_t(const GemmArgs& a, hipStream_t st) {
   return launch_status();
 }
 
+// Tile shape: BM = 64 TMW, BN = 64 TNW. A workgroup's time grows with its
+// tile area, and tiles run in rounds of one workgroup per CU, so the cost of
+// a shape is rounds x area, plus a penalty for short tiles (the weight
+// dequantization is amortised over BM rows). Ties go to the larger tile.
+static void pick_gemm_tile(int M, int N, int* tmw, int* tnw) {
+  const int cus = num_cus();
+  double best = 0;
+  *tmw = 1;
+  *tnw = 4;
+  for (int tm : {4, 2, 1}) {
+    if (tm > 1 && M <= 64 * (tm / 2)) continue;  // no tile taller than needed
+    for (int tn : {4, 3, 2}) {
+      const int64_t tiles = (int64_t)((M + 64 * tm - 1) / (64 * tm)) * ((N + 64 * tn - 1) / (64 * tn));
+      const int64_t rounds = (tiles + cus - 1) / cus;
+      const double cost = (double)rounds * tm * tn * (1.0 + 0.25 * 4.0 / tm);
+      if (best == 0 || cost < best * 0.999) {
+        best = cost;
+        *tmw = tm;
+        *tnw = tn;
+      }
+    }
+  }
+}
+
 template <bool NIB, int OM>
 static int launch_gemm_shape(const GemmArgs& a, hipStream_t st) {
-  // tile shape by M: 256 x 256 for large M, narrower M tiles for small M
-  if (a.M > 128) return launch_gemm_t<NIB, 4, 4, OM>(a, st);
-  if (a.M > 64) return launch_gemm_t<NIB, 2, 4, OM>(a, st);
-  return launch_gemm_t<NIB, 1, 4, OM>(a, st);
+  int tm = 1, tn = 4;
+  pick_gemm_tile(a.M, a.N, &tm, &tn);
+  switch (tm * 8 + tn) {
+    case 4 * 8 + 4: return launch_gemm_t<NIB, 4, 4, OM>(a, st);
+    case 4 * 8 + 3: return launch_gemm_t<NIB, 4, 3, OM>(a, st);
+    case 4 * 8 + 2: return launch_gemm_t<NIB, 4, 2, OM>(a, st);
+    case 2 * 8 + 4: return launch_gemm_t<NIB, 2, 4, OM>(a, st);
+    case 2 * 8 + 3: return launch_gemm_t<NIB, 2, 3, OM>(a, st);
+    case 2 * 8 + 2: return launch_gemm_t<NIB, 2, 2, OM>(a, st);
+    case 1 * 8 + 3: return launch_gemm_t<NIB, 1, 3, OM>(a, st);
+    case 1 * 8 + 2: return launch_gemm_t<NIB, 1, 2, OM>(a, st);
+    default: return launch_gemm_t<NIB, 1, 4, OM>(a, st);
+  }
 }
 
 int gemm(bool nibble, int omode, const GemmArgs& a, hipStream_t st) {
