@@ -142,15 +142,18 @@ __device__ __forceinline__ void mma_ktile(float16v (&acc)[TMW][TNW], const BTile
   }
 }
 
-template <bool NIB, int TMW, int TNW, int OM>
-__global__ __launch_bounds__(256) void gemm_kernel(
+// WM x WN waves, wave tile 32 TMW x 32 TNW.
+template <bool NIB, int TMW, int TNW, int WM, int WN, int OM>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
     const float* __restrict__ ct, int n_levels, uint32_t code_mask, int tbl_entries,
     const uint32_t* __restrict__ xp, void* __restrict__ y, const uint16_t* __restrict__ bias,
     int M, int N, int nb, int64_t ldy, int tiles_m, int tiles_total, WLayout lay) {
-  constexpr int BM = 2 * TMW * 32;
-  constexpr int BN = 2 * TNW * 32;
-  constexpr int KA = BM * 8 / 256;  // uint4 of A per thread per half-block
+  constexpr int NT = WM * WN * 64;
+  constexpr int BM = WM * TMW * 32;
+  constexpr int BN = WN * TNW * 32;
+  constexpr int KA = BM * 8 / NT;  // uint4 of A per thread per half-block
+  static_assert(KA * NT == BM * 8, "A tile must split evenly over the threads");
   extern __shared__ uint4 smem4[];
   char* smem = reinterpret_cast<char*>(smem4);
   char* tbl = smem;
@@ -159,28 +162,27 @@ __global__ __launch_bounds__(256) void gemm_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   const int h = lane >> 5, l32 = lane & 31;
   const uint32_t lane4 = (uint32_t)lane << 2;
-  (void)BN;
 
   // XCD-aware tile order: ids are dealt round-robin to 8 XCDs; give each XCD a
   // contiguous range of logical tiles.
   int wid = blockIdx.x;
   if ((tiles_total & 7) == 0) wid = (wid & 7) * (tiles_total >> 3) + (wid >> 3);
   const int tm = wid % tiles_m, tn = wid / tiles_m;
-  const int m0 = tm * BM, n0 = tn * (2 * TNW * 32);
+  const int m0 = tm * BM, n0 = tn * BN;
 
-  if constexpr (NIB) fill_codebook<TBL_NIB_H2>(0, ct, n_levels, tbl_entries, 4);
-  else fill_codebook<TBL_F16>(0, ct, n_levels, tbl_entries, 4);
+  if constexpr (NIB) fill_codebook<TBL_NIB_H2>(0, ct, n_levels, tbl_entries, NT / 64);
+  else fill_codebook<TBL_F16>(0, ct, n_levels, tbl_entries, NT / 64);
 
-  // A loader: thread t moves uint4 q = t + 256 i (row q >> 3, 16-byte col q & 7)
+  // A loader: thread t moves uint4 q = t + NT i (row q >> 3, 16-byte col q & 7)
   const int64_t xrow_u32 = (int64_t)nb * 64;
   const uint32_t* a_src[KA];
   int a_dst[KA];
 #pragma unroll
   for (int i = 0; i < KA; ++i) {
-    const int q = tid + 256 * i;
+    const int q = tid + NT * i;
     const int r = q >> 3, c = q & 7;
     int m = m0 + r;
     if (m >= M) m = M - 1;  // clamped rows feed discarded outputs only
@@ -258,10 +260,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(
   }
 }
 
-template <bool NIB, int TMW, int TNW, int OM>
+template <bool NIB, int TMW, int TNW, int WM, int WN, int OM>
 static int launch_gemm_t(const GemmArgs& a, hipStream_t st) {
-  constexpr int BM = 2 * TMW * 32, BN = 2 * TNW * 32;
-  auto kern = gemm_kernel<NIB, TMW, TNW, OM>;
+  constexpr int BM = WM * TMW * 32, BN = WN * TNW * 32;
+  auto kern = gemm_kernel<NIB, TMW, TNW, WM, WN, OM>;
   const int entries = table_entries(NIB, a.n_levels);
   const size_t lds = (size_t)entries * 256 + 2 * (size_t)BM * kAStride;
   if (lds > 160 * 1024) return PE_ERR_DIMS;
@@ -275,7 +277,7 @@ static int launch_gemm_t(const GemmArgs& a, hipStream_t st) {
   const int64_t total = (int64_t)tiles_m * tiles_n;
   if (total > INT32_MAX) return PE_ERR_DIMS;
   const uint8_t mb = NIB ? (uint8_t)((a.n_levels - 1) * 0x11) : (uint8_t)(a.n_levels - 1);
-  kern<<<dim3((unsigned)total), dim3(256), lds, st>>>(
+  kern<<<dim3((unsigned)total), dim3(WM * WN * 64), lds, st>>>(
       a.codes, a.norms, a.ct, a.n_levels, 0x01010101u * mb, entries,
       reinterpret_cast<const uint32_t*>(a.xp), a.y, a.bias, a.M, a.N, a.nb, a.ldy, tiles_m,
       (int)total, a.lay);
@@ -311,15 +313,15 @@ static int launch_gemm_shape(const GemmArgs& a, hipStream_t st) {
   int tm = 1, tn = 4;
   pick_gemm_tile(a.M, a.N, &tm, &tn);
   switch (tm * 8 + tn) {
-    case 4 * 8 + 4: return launch_gemm_t<NIB, 4, 4, OM>(a, st);
-    case 4 * 8 + 3: return launch_gemm_t<NIB, 4, 3, OM>(a, st);
-    case 4 * 8 + 2: return launch_gemm_t<NIB, 4, 2, OM>(a, st);
-    case 2 * 8 + 4: return launch_gemm_t<NIB, 2, 4, OM>(a, st);
-    case 2 * 8 + 3: return launch_gemm_t<NIB, 2, 3, OM>(a, st);
-    case 2 * 8 + 2: return launch_gemm_t<NIB, 2, 2, OM>(a, st);
-    case 1 * 8 + 3: return launch_gemm_t<NIB, 1, 3, OM>(a, st);
-    case 1 * 8 + 2: return launch_gemm_t<NIB, 1, 2, OM>(a, st);
-    default: return launch_gemm_t<NIB, 1, 4, OM>(a, st);
+    case 4 * 8 + 4: return launch_gemm_t<NIB, 4, 2, 2, 4, OM>(a, st);  // 8 waves of 128 x 64
+    case 4 * 8 + 3: return launch_gemm_t<NIB, 4, 3, 2, 2, OM>(a, st);
+    case 4 * 8 + 2: return launch_gemm_t<NIB, 4, 2, 2, 2, OM>(a, st);
+    case 2 * 8 + 4: return launch_gemm_t<NIB, 2, 4, 2, 2, OM>(a, st);
+    case 2 * 8 + 3: return launch_gemm_t<NIB, 2, 3, 2, 2, OM>(a, st);
+    case 2 * 8 + 2: return launch_gemm_t<NIB, 2, 2, 2, 2, OM>(a, st);
+    case 1 * 8 + 3: return launch_gemm_t<NIB, 1, 3, 2, 2, OM>(a, st);
+    case 1 * 8 + 2: return launch_gemm_t<NIB, 1, 2, 2, 2, OM>(a, st);
+    default: return launch_gemm_t<NIB, 1, 4, 2, 2, OM>(a, st);
   }
 }
 
