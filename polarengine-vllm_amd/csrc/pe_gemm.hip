@@ -5,7 +5,8 @@
 // Replaces polar_gemm / polar_gemm_packed (kernels/polar_gemm.py:81-171,
 // 211-418), which gather ct per tile and run tl.dot on fp32 tiles.
 //
-// Structure (one 256-lane workgroup = 2 x 2 waves, wave tile 32*TMW x 32*TNW):
+// Structure (a workgroup of WM x WN waves, wave tile 32*TMW x 32*TNW; the
+// dispatcher uses 1 x WN rows of waves, see pick_gemm_tile):
 //  * K advances in half-blocks of 64 activations = 32 pairs; pair p of a
 //    128-block is (x[p], x[p + 64]), the two positions one nibble byte codes;
 //  * the activation tile (BM rows x 32 pairs, pair-f16) is staged global ->
@@ -284,44 +285,46 @@ static int launch_gemm_t(const GemmArgs& a, hipStream_t st) {
   return launch_status();
 }
 
-// Tile shape: BM = 64 TMW, BN = 64 TNW. A workgroup's time grows with its
-// tile area, and tiles run in rounds of one workgroup per CU, so the cost of
-// a shape is rounds x area, plus a penalty for short tiles (the weight
-// dequantization is amortised over BM rows). Ties go to the larger tile.
-static void pick_gemm_tile(int M, int N, int* tmw, int* tnw) {
+// Tile shape. Waves sit in one row (1 x WN), each owning 32 TMW rows x 32
+// columns, so every weight column is dequantized by exactly one wave and two
+// waves share a SIMD (8 waves). A workgroup's time grows with its tile area
+// and tiles run in rounds of one workgroup per CU: the cost of a shape is
+// rounds x area x a penalty for short tiles (the dequantization is amortised
+// over BM rows; measured ~13% per halving of BM) or for 4-wave workgroups
+// (one wave per SIMD hides no latency).
+struct GemmShape {
+  int tmw, wn;
+};
+static GemmShape pick_gemm_tile(int M, int N) {
   const int cus = num_cus();
-  double best = 0;
-  *tmw = 1;
-  *tnw = 4;
-  for (int tm : {4, 2, 1}) {
-    if (tm > 1 && M <= 64 * (tm / 2)) continue;  // no tile taller than needed
-    for (int tn : {4, 3, 2}) {
-      const int64_t tiles = (int64_t)((M + 64 * tm - 1) / (64 * tm)) * ((N + 64 * tn - 1) / (64 * tn));
-      const int64_t rounds = (tiles + cus - 1) / cus;
-      const double cost = (double)rounds * tm * tn * (1.0 + 0.25 * 4.0 / tm);
-      if (best == 0 || cost < best * 0.999) {
-        best = cost;
-        *tmw = tm;
-        *tnw = tn;
-      }
+  const GemmShape cand[] = {{8, 8}, {4, 8}, {2, 8}, {8, 4}, {4, 4}, {2, 4}};
+  GemmShape best = cand[0];
+  double best_cost = -1;
+  for (const GemmShape& c : cand) {
+    const int bm = 32 * c.tmw, bn = 32 * c.wn;
+    if (c.tmw > 2 && M <= bm / 2) continue;  // no tile more than twice as tall as needed
+    const int64_t tiles = (int64_t)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    const int64_t rounds = (tiles + cus - 1) / cus;
+    const double pen = (c.tmw == 8 ? 1.0 : c.tmw == 4 ? 1.13 : 1.3) * (c.wn == 8 ? 1.0 : 1.25);
+    const double cost = (double)rounds * bm * bn * pen;
+    if (best_cost < 0 || cost < best_cost * 0.999) {
+      best_cost = cost;
+      best = c;
     }
   }
+  return best;
 }
 
 template <bool NIB, int OM>
 static int launch_gemm_shape(const GemmArgs& a, hipStream_t st) {
-  int tm = 1, tn = 4;
-  pick_gemm_tile(a.M, a.N, &tm, &tn);
-  switch (tm * 8 + tn) {
-    case 4 * 8 + 4: return launch_gemm_t<NIB, 4, 2, 2, 4, OM>(a, st);  // 8 waves of 128 x 64
-    case 4 * 8 + 3: return launch_gemm_t<NIB, 4, 3, 2, 2, OM>(a, st);
-    case 4 * 8 + 2: return launch_gemm_t<NIB, 4, 2, 2, 2, OM>(a, st);
-    case 2 * 8 + 4: return launch_gemm_t<NIB, 2, 4, 2, 2, OM>(a, st);
-    case 2 * 8 + 3: return launch_gemm_t<NIB, 2, 3, 2, 2, OM>(a, st);
-    case 2 * 8 + 2: return launch_gemm_t<NIB, 2, 2, 2, 2, OM>(a, st);
-    case 1 * 8 + 3: return launch_gemm_t<NIB, 1, 3, 2, 2, OM>(a, st);
-    case 1 * 8 + 2: return launch_gemm_t<NIB, 1, 2, 2, 2, OM>(a, st);
-    default: return launch_gemm_t<NIB, 1, 4, 2, 2, OM>(a, st);
+  const GemmShape g = pick_gemm_tile(a.M, a.N);
+  switch (g.tmw * 16 + g.wn) {
+    case 8 * 16 + 8: return launch_gemm_t<NIB, 8, 1, 1, 8, OM>(a, st);
+    case 4 * 16 + 8: return launch_gemm_t<NIB, 4, 1, 1, 8, OM>(a, st);
+    case 2 * 16 + 8: return launch_gemm_t<NIB, 2, 1, 1, 8, OM>(a, st);
+    case 8 * 16 + 4: return launch_gemm_t<NIB, 8, 1, 1, 4, OM>(a, st);
+    case 4 * 16 + 4: return launch_gemm_t<NIB, 4, 1, 1, 4, OM>(a, st);
+    default: return launch_gemm_t<NIB, 2, 1, 1, 4, OM>(a, st);
   }
 }
 
