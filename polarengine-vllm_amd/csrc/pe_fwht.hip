@@ -31,7 +31,7 @@ __global__ __launch_bounds__(256) void fwht128_kernel(const void* x, void* y, in
   if constexpr (YL == PE_XTF_PAIR_F16) {
     float o[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = __shfl_xor(v[i], 8, 64);
+    for (int i = 0; i < 8; ++i) o[i] = lane_xor<8>(v[i]);
     if (!live) return;
     uint4 w;
     int p0;
