@@ -80,6 +80,11 @@ __device__ __forceinline__ void lds_st128(uint32_t addr, u32x4v v) {
 __device__ __forceinline__ void lds_st32(uint32_t addr, uint32_t v) {
   *reinterpret_cast<lds_u32*>(static_cast<uintptr_t>(addr)) = v;
 }
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) u32x2v lds_u32x2;
+__device__ __forceinline__ void lds_st64(uint32_t addr, u32x2v v) {
+  *reinterpret_cast<lds_u32x2*>(static_cast<uintptr_t>(addr)) = v;
+}
 __device__ __forceinline__ u32x4v lds_ld128(uint32_t addr) {
   return *reinterpret_cast<const lds_u32x4*>(static_cast<uintptr_t>(addr));
 }

@@ -23,6 +23,8 @@
 //    walks a contiguous range of tiles (M-tile fastest) and shares A/B in its
 //    own L2.
 
+#include <type_traits>
+
 #include "pe_internal.h"
 
 namespace pe {
@@ -261,6 +263,326 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Four-wave variant: one wave per SIMD, each wave owning BM = 32 TMW rows x 64
+// columns (two 32-column n-tiles), workgroup tile BM x 256. Per MFMA it moves
+// (TMW + 2) / (2 TMW) KB of operands through LDS instead of (TMW + 1) / TMW,
+// and every weight column is still dequantized by exactly one wave.
+//  * A half-block tiles sit in a ring of three LDS buffers: the tile of
+//    half-block kt + 1 is complete before the barrier that ends kt - 1, so the
+//    first slab of kt + 1 is read ahead while kt still computes.
+//  * Within a half-block every slab's operands (A fragments and codebook
+//    lookups) are issued one slab ahead of its MFMAs.
+//  * Codes ride a ring of four half-block slots (issued three half-blocks
+//    ahead), activations a ring of two register stages (two ahead); the loop
+//    body covers four half-blocks so every ring index is static. Loads past the
+//    end are clamped to the last half-block, so each wait count is static too.
+// Requires an even number of 128-blocks.
+// ---------------------------------------------------------------------------
+// Codes of one half-block for the wave's two n-tiles. Norms are kept
+// zero-extended to 32 bits: 16-bit members next to vectors made the compiler
+// keep the slot in memory.
+template <bool NIB>
+struct BSlot4 {
+  u32x4v lo[2];
+  u32x4v hi[NIB ? 1 : 2];  // int8 codes only: bytes at +64
+  uint32_t nrm[2];
+};
+
+template <bool NIB, int TMW>
+struct Frag4 {
+  half8v a[TMW];
+  uint32_t raw[2][NIB ? 4 : 8];
+};
+
+// A tiles of the four-wave kernel: 128-byte rows (32 pairs), 16-byte chunk c
+// of row r stored at chunk c ^ (r & 7), so the eight rows one ds_read_b128
+// phase touches cover all banks without padding.
+constexpr int kARow4 = 128;
+
+template <bool NIB, int TMW, bool MASK>
+__device__ __forceinline__ void issue_frag4(Frag4<NIB, TMW>& f, uint32_t aaddr, int t,
+                                            const BSlot4<NIB>& bt, uint32_t lane4,
+                                            uint32_t code_mask) {
+  // aaddr: this lane's row and swizzled chunk of slab t in m-tile 0
+#pragma unroll
+  for (int i = 0; i < TMW; ++i)
+    f.a[i] = __builtin_bit_cast(half8v, lds_ld128(aaddr + i * 32 * kARow4));
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    uint32_t wl = bt.lo[j][t];
+    if constexpr (MASK) wl &= code_mask;
+    f.raw[j][0] = lds_ld32(tbl_addr<0>(wl, lane4));
+    f.raw[j][1] = lds_ld32(tbl_addr<1>(wl, lane4));
+    f.raw[j][2] = lds_ld32(tbl_addr<2>(wl, lane4));
+    f.raw[j][3] = lds_ld32(tbl_addr<3>(wl, lane4));
+    if constexpr (!NIB) {
+      uint32_t wh = bt.hi[j][t];
+      if constexpr (MASK) wh &= code_mask;
+      f.raw[j][4] = lds_ld32(tbl_addr<0>(wh, lane4));
+      f.raw[j][5] = lds_ld32(tbl_addr<1>(wh, lane4));
+      f.raw[j][6] = lds_ld32(tbl_addr<2>(wh, lane4));
+      f.raw[j][7] = lds_ld32(tbl_addr<3>(wh, lane4));
+    }
+  }
+}
+
+template <bool NIB, int TMW>
+__device__ __forceinline__ void mma_frag4(float16v (&acc)[TMW][2], const Frag4<NIB, TMW>& f,
+                                          const BSlot4<NIB>& bt) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const _Float16 nh = __builtin_bit_cast(_Float16, (uint16_t)bt.nrm[j]);
+    const half2v nrm2{nh, nh};
+    half8v bf;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t p = f.raw[j][q];
+      // int8: (lo16 of the first-position entry, lo16 of the second)
+      if constexpr (!NIB) p = __builtin_amdgcn_perm(f.raw[j][4 + q], p, 0x05040100u);
+      const half2v v = as_h2(p) * nrm2;
+      bf[2 * q] = v[0];
+      bf[2 * q + 1] = v[1];
+    }
+    // weights as the MFMA's A operand: the accumulator comes out transposed,
+    // lane = output row, four consecutive output columns per register group
+#pragma unroll
+    for (int i = 0; i < TMW; ++i)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf, f.a[i], acc[i][j], 0, 0, 0);
+  }
+}
+
+// Output tile through LDS: the transposed accumulators (lane = row m, groups
+// of four consecutive columns) are written as 8- or 16-byte pieces into a
+// row-major staging tile, then copied to y in 16-byte coalesced stores.
+template <int TMW, int OM>
+__device__ __forceinline__ void store_tile4(const float16v (&acc)[TMW][2], void* __restrict__ y,
+                                            int64_t ldy, const uint16_t* __restrict__ bias, int M,
+                                            int N, int m0, int n0, int vec_ok) {
+  constexpr int BM = TMW * 32, BN = 256;
+  constexpr int ES = OM == OM_F16 ? 2 : 4;
+  constexpr uint32_t OSTR = BN * ES + 16;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+  __syncthreads();  // every wave is done with the ring and the table
+#pragma unroll
+  for (int i = 0; i < TMW; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const uint32_t addr =
+            (uint32_t)(32 * i + l32) * OSTR + (uint32_t)(wave * 64 + 32 * j + 8 * g + 4 * h) * ES;
+        // element values first: a bit_cast applied to a vector element
+        // lvalue reads element 0 of the vector with this compiler
+        const float v0 = acc[i][j][4 * g], v1 = acc[i][j][4 * g + 1];
+        const float v2 = acc[i][j][4 * g + 2], v3 = acc[i][j][4 * g + 3];
+        if constexpr (OM == OM_F16) {
+          lds_st64(addr, u32x2v{pack_h2(v0, v1), pack_h2(v2, v3)});
+        } else {
+          lds_st128(addr, u32x4v{__builtin_bit_cast(uint32_t, v0), __builtin_bit_cast(uint32_t, v1),
+                                 __builtin_bit_cast(uint32_t, v2), __builtin_bit_cast(uint32_t, v3)});
+        }
+      }
+  __syncthreads();
+  constexpr int CPR = BN * ES / 16;  // 16-byte chunks per row
+  constexpr int EPC = 16 / ES;       // elements per chunk
+  for (int q = tid; q < BM * CPR; q += 256) {
+    const int r = q / CPR, c = q % CPR;
+    const int m = m0 + r, n = n0 + c * EPC;
+    if (m >= M || n >= N) continue;
+    u32x4v v = lds_ld128((uint32_t)r * OSTR + (uint32_t)c * 16u);
+    if constexpr (OM == OM_F16) {
+      if (bias) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const half2v x = as_h2(v[e]);
+          const int nn = n + 2 * e;
+          const float b0 = nn < N ? h2f(bias[nn]) : 0.f;
+          const float b1 = nn + 1 < N ? h2f(bias[nn + 1]) : 0.f;
+          v[e] = pack_h2((float)x[0] + b0, (float)x[1] + b1);
+        }
+      }
+    }
+    char* dst = reinterpret_cast<char*>(y) + ((int64_t)m * ldy + n) * ES;
+    if (vec_ok && n + EPC <= N) {
+      *reinterpret_cast<u32x4v*>(dst) = v;
+    } else {
+      const int cnt = N - n < EPC ? N - n : EPC;
+      for (int e = 0; e < cnt; ++e) {
+        if constexpr (OM == OM_F16)
+          reinterpret_cast<uint16_t*>(dst)[e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+        else
+          reinterpret_cast<uint32_t*>(dst)[e] = v[e];
+      }
+    }
+  }
+}
+
+template <bool NIB, int TMW, bool MASK, int OM>
+__global__ __launch_bounds__(256) void gemm4_kernel(
+    const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
+    const float* __restrict__ ct, int n_levels, uint32_t code_mask, int tbl_entries,
+    const uint32_t* __restrict__ xp, void* __restrict__ y, const uint16_t* __restrict__ bias,
+    int M, int N, int nb, int64_t ldy, int tiles_m, int tiles_total, WLayout lay, int vec_ok) {
+  constexpr int NT = 256;
+  constexpr int BM = TMW * 32;
+  constexpr int BN = 256;
+  constexpr int KA = BM * 8 / NT;
+  constexpr uint32_t ABUF = BM * kARow4;
+  static_assert(KA * NT == BM * 8, "A tile must split evenly over the threads");
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+  const uint32_t lane4 = (uint32_t)lane << 2;
+
+  // XCD-aware tile order: ids are dealt round-robin to 8 XCDs; give each XCD a
+  // contiguous range of logical tiles (M-tile fastest).
+  int wid = blockIdx.x;
+  if ((tiles_total & 7) == 0) wid = (wid & 7) * (tiles_total >> 3) + (wid >> 3);
+  const int tm = wid % tiles_m, tn = wid / tiles_m;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  if constexpr (NIB) fill_codebook<TBL_NIB_H2>(0, ct, n_levels, tbl_entries, NT / 64);
+  else fill_codebook<TBL_F16>(0, ct, n_levels, tbl_entries, NT / 64);
+  const uint32_t abuf = (uint32_t)tbl_entries * 256u;
+
+  const int64_t xrow_u32 = (int64_t)nb * 64;
+  const uint32_t* a_src[KA];
+  uint32_t a_dst[KA];
+#pragma unroll
+  for (int i = 0; i < KA; ++i) {
+    const int q = tid + NT * i;
+    const int r = q >> 3, c = q & 7;
+    int m = m0 + r;
+    if (m >= M) m = M - 1;  // clamped rows feed discarded outputs only
+    a_src[i] = xp + (int64_t)m * xrow_u32 + c * 4;
+    a_dst[i] = (uint32_t)(r * kARow4 + ((c ^ (r & 7)) << 4));
+  }
+  const uint8_t* b_row[2];
+  const uint16_t* n_row[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    int n = n0 + wave * 64 + j * 32 + l32;
+    if (n >= N) n = N - 1;
+    b_row[j] = codes + lay.codes_off(n) + 16 * h;
+    n_row[j] = norms + lay.norms_off(n);
+  }
+  uint32_t a_off[4];  // lane's row l32, chunk 4h + t, swizzled
+#pragma unroll
+  for (int t = 0; t < 4; ++t) a_off[t] = (uint32_t)(l32 * kARow4 + (((4 * h + t) ^ (l32 & 7)) << 4));
+
+  const int nkt = 2 * nb;  // half-blocks, a multiple of 4
+  // loads past the last half-block re-read it (in bounds, never used)
+  auto ldb = [&](BSlot4<NIB>& sl, int kt) {
+    kt = kt < nkt ? kt : nkt - 1;
+    const int bk = kt >> 1, half = kt & 1;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint8_t* pc = b_row[j] + bk * lay.c_blk + half * 32;
+      sl.lo[j] = *reinterpret_cast<const u32x4v*>(pc);
+      if constexpr (!NIB) sl.hi[j] = *reinterpret_cast<const u32x4v*>(pc + 64);
+      sl.nrm[j] = (uint32_t)n_row[j][bk * lay.n_blk];
+    }
+  };
+  auto lda = [&](u32x4v (&rg)[KA], int kt) {
+    kt = kt < nkt ? kt : nkt - 1;
+    const int off = (kt >> 1) * 64 + (kt & 1) * 32;
+#pragma unroll
+    for (int i = 0; i < KA; ++i) rg[i] = *reinterpret_cast<const u32x4v*>(a_src[i] + off);
+  };
+  auto sta = [&](uint32_t buf, const u32x4v (&rg)[KA]) {
+#pragma unroll
+    for (int i = 0; i < KA; ++i) lds_st128(buf + a_dst[i], rg[i]);
+  };
+
+  float16v acc[TMW][2];
+#pragma unroll
+  for (int i = 0; i < TMW; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  BSlot4<NIB> slot[4];
+  u32x4v stg[2][KA];
+  lda(stg[0], 0);
+  lda(stg[1], 1);
+  ldb(slot[0], 0);
+  ldb(slot[1], 1);
+  ldb(slot[2], 2);
+  __syncthreads();  // codebook table written
+  sta(abuf, stg[0]);
+  sta(abuf + ABUF, stg[1]);
+  lda(stg[0], 2);
+  lda(stg[1], 3);
+  __syncthreads();
+
+  Frag4<NIB, TMW> f;
+  issue_frag4<NIB, TMW, MASK>(f, abuf + a_off[0], 0, slot[0], lane4, code_mask);
+  uint32_t bcur = 0;  // ring offset (bytes) of half-block kt's A buffer
+
+  auto half_step = [&](auto S_, int kt) {
+    constexpr int S = decltype(S_)::value;
+    const uint32_t bnext = bcur == 2 * ABUF ? 0u : bcur + ABUF;
+    const uint32_t bst = bnext == 2 * ABUF ? 0u : bnext + ABUF;
+    ldb(slot[(S + 3) & 3], kt + 3);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      Frag4<NIB, TMW> fn;
+      if (t < 3) issue_frag4<NIB, TMW, MASK>(fn, abuf + bcur + a_off[t + 1], t + 1, slot[S], lane4, code_mask);
+      else issue_frag4<NIB, TMW, MASK>(fn, abuf + bnext + a_off[0], 0, slot[(S + 1) & 3], lane4, code_mask);
+      // keep the next slab's reads ahead of this slab's MFMAs
+      __builtin_amdgcn_sched_barrier(0);
+      mma_frag4<NIB, TMW>(acc, f, slot[S]);
+      f = fn;
+    }
+    sta(abuf + bst, stg[S & 1]);  // A(kt + 2)
+    lda(stg[S & 1], kt + 4);
+    bcur = bnext;
+    __syncthreads();
+  };
+  for (int kt = 0; kt < nkt; kt += 4) {
+    half_step(std::integral_constant<int, 0>{}, kt);
+    half_step(std::integral_constant<int, 1>{}, kt + 1);
+    half_step(std::integral_constant<int, 2>{}, kt + 2);
+    half_step(std::integral_constant<int, 3>{}, kt + 3);
+  }
+
+  store_tile4<TMW, OM>(acc, y, ldy, bias, M, N, m0, n0, vec_ok);
+}
+
+template <bool NIB, int TMW, bool MASK, int OM>
+static int launch_gemm4_t(const GemmArgs& a, hipStream_t st) {
+  constexpr int BM = TMW * 32, BN = 256;
+  auto kern = gemm4_kernel<NIB, TMW, MASK, OM>;
+  const int entries = table_entries(NIB, a.n_levels);
+  constexpr size_t ES = OM == OM_F16 ? 2 : 4;
+  const size_t lds_loop = (size_t)entries * 256 + 3 * (size_t)BM * kARow4;
+  const size_t lds_out = (size_t)BM * (BN * ES + 16);
+  const size_t lds = lds_loop > lds_out ? lds_loop : lds_out;
+  if (lds > 160 * 1024) return PE_ERR_DIMS;
+  static const bool attr_ok = [&] {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+  }();
+  (void)attr_ok;
+  const int tiles_m = (a.M + BM - 1) / BM;
+  const int tiles_n = (a.N + BN - 1) / BN;
+  const int64_t total = (int64_t)tiles_m * tiles_n;
+  if (total > INT32_MAX) return PE_ERR_DIMS;
+  const uint8_t mb = NIB ? (uint8_t)((a.n_levels - 1) * 0x11) : (uint8_t)(a.n_levels - 1);
+  const int vec_ok = ((uintptr_t)a.y % 16 == 0) && ((a.ldy * (int64_t)ES) % 16 == 0);
+  kern<<<dim3((unsigned)total), dim3(256), lds, st>>>(
+      a.codes, a.norms, a.ct, a.n_levels, 0x01010101u * mb, entries,
+      reinterpret_cast<const uint32_t*>(a.xp), a.y, a.bias, a.M, a.N, a.nb, a.ldy, tiles_m,
+      (int)total, a.lay, vec_ok);
+  return launch_status();
+}
+
 template <bool NIB, int TMW, int TNW, int WM, int WN, int OM>
 static int launch_gemm_t(const GemmArgs& a, hipStream_t st) {
   constexpr int BM = WM * TMW * 32, BN = WN * TNW * 32;
@@ -315,8 +637,18 @@ static GemmShape pick_gemm_tile(int M, int N) {
   return best;
 }
 
+// The four-wave kernel (128 x 256 tiles) is the faster one when its tiles fill
+// the CUs for one to four rounds (measured on M = 2048 prefill shapes: 6-18%
+// ahead); with fewer tiles the eight-wave kernel's narrower tiles spread
+// wider, and with many rounds its two waves per SIMD hide more latency.
 template <bool NIB, int OM>
 static int launch_gemm_shape(const GemmArgs& a, hipStream_t st) {
+  const int cus = num_cus();
+  const int64_t tiles4 = (int64_t)((a.M + 127) / 128) * ((a.N + 255) / 256);
+  if ((a.nb & 1) == 0 && tiles4 >= cus && tiles4 <= 4 * (int64_t)cus) {
+    const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
+    return mask ? launch_gemm4_t<NIB, 4, true, OM>(a, st) : launch_gemm4_t<NIB, 4, false, OM>(a, st);
+  }
   const GemmShape g = pick_gemm_tile(a.M, a.N);
   switch (g.tmw * 16 + g.wn) {
     case 8 * 16 + 8: return launch_gemm_t<NIB, 8, 1, 1, 8, OM>(a, st);

@@ -436,6 +436,66 @@ def test_prefill_gemm_full_size_row_sample(m, n, k, bits):
     assert torch.isfinite(y).all()
 
 
+# Shapes whose 128 x 256 tile count fills the CUs for one to four rounds take
+# the four-wave prefill kernel: f16 and f32 outputs, nibble and int8 codes,
+# masked small codebooks, bias, M and N tails, both weight layouts.
+FOUR_WAVE_CASES = [(2048, 4096, 4096, 4, "f16", False, True), (2000, 4200, 4096, 6, "f16", True, False),
+                   (2048, 4096, 4096, 3, "f32", False, False), (2048, 4096, 2048, 8, "f32", False, False),
+                   (1950, 4352, 1024, 2, "f16", True, True)]
+
+
+@pytest.mark.parametrize("m,n,k,bits,out,with_bias,tiled", FOUR_WAVE_CASES)
+def test_four_wave_prefill_row_sample(m, n, k, bits, out, with_bias, tiled):
+    from polarengine_vllm import _lib
+    _say(f"four-wave prefill m={m} n={n} k={k} bits={bits} out={out} bias={with_bias} tiled={tiled}")
+    rng = np.random.default_rng(m + n + bits)
+    codes, norms, ct = rand_layer(rng, n, k, bits)
+    x = O.seeded_normal((m, k), 1.0, 23 + bits)
+    bias = O.seeded_normal((n,), 0.1, 24) if with_bias else None
+    if tiled:
+        dcodes, dnorms, nib = dev_tiled(codes, norms, bits)
+        fmt = (_lib.PE_PACK_NIBBLE if nib else 0) | _lib.PE_LAYOUT_TILE16
+    else:
+        dcodes, nib = dev_codes(codes, bits)
+        dnorms = to_dev(norms)
+        fmt = _lib.PE_PACK_NIBBLE if nib else 0
+    L = _lib.lib()
+    cd = to_dev(ct)
+    rows = np.sort(rng.choice(m, 24, replace=False))
+    rows[0], rows[-1] = 0, m - 1
+    if out == "f16":
+        y = torch.empty(m, n, dtype=torch.float16, device=DEV)
+        wsb = L.pe_linear_workspace_size(m, k, n, bits, fmt)
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+        xd = to_dev(x)
+        bd = to_dev(bias) if with_bias else None
+        rc = L.pe_linear_forward(xd.data_ptr(), 0, m, k, k, dcodes.data_ptr(), bits, fmt,
+                                 dnorms.data_ptr(), cd.data_ptr(), None, 1 << bits,
+                                 bd.data_ptr() if bd is not None else None,
+                                 y.data_ptr(), n, ws.data_ptr(), wsb,
+                                 _lib.stream_ptr(torch.device(DEV)))
+        torch.cuda.synchronize()
+        _lib.check(rc, "pe_linear_forward")
+        want = O.linear_apply(x[rows], codes, norms, ct, k, bias)
+    else:
+        # reference API: x_tf in f32, y in f32 (row-major weights only)
+        assert not tiled and not with_bias
+        x_tf = O.fwht_blocks(x)
+        y = torch.empty(m, n, dtype=torch.float32, device=DEV)
+        xt = to_dev(x_tf)
+        wsb = L.pe_polar_matmul_workspace_size(m, k)
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+        rc = L.pe_polar_matmul(dcodes.data_ptr(), int(nib), xt.data_ptr(), m, dnorms.data_ptr(),
+                               cd.data_ptr(), 1 << bits, y.data_ptr(), n, k,
+                               ws.data_ptr(), wsb, _lib.stream_ptr(torch.device(DEV)))
+        torch.cuda.synchronize()
+        _lib.check(rc, "pe_polar_matmul")
+        want = O.hadamard_domain_matmul(codes, norms, ct, x_tf[rows])
+    got = y[torch.from_numpy(rows).to(DEV)].float().cpu().numpy()
+    check_close(got, np.asarray(want, dtype=np.float32), f"four-wave {m}x{n}x{k} q{bits} {out}")
+    assert torch.isfinite(y).all()
+
+
 # ---------------------------------------------------------------------------
 # Plugin path: PolarQuantLinearMethod with quantizer output
 # ---------------------------------------------------------------------------
