@@ -52,6 +52,8 @@ __device__ __forceinline__ float h2f(uint16_t bits) {
 __device__ __forceinline__ uint16_t f2h_bits(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
+// host side fp32 -> fp16 bits, round to nearest even like v_cvt_f16_f32
+inline uint16_t host_f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
   return (uint32_t)f2h_bits(lo) | ((uint32_t)f2h_bits(hi) << 16);
 }

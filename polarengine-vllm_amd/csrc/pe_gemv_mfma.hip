@@ -11,18 +11,21 @@
 // as B) instead of v_dot2 cuts the VALU work per byte by ~2.5x, and the
 // weight rows then need no cross-lane reduction.
 //
-//  * one workgroup of NW waves per CU-sized share of rows: TN n-tiles of 16
-//    weight rows (TN chosen so the grid covers the CUs once); the NW waves
-//    split the 128-blocks of K (contiguous ranges) and combine through LDS;
+//  * one workgroup of NW = TN x KS waves per CU-sized share of rows: TN
+//    n-tiles of 16 weight rows (TN chosen so the grid covers the CUs once),
+//    KS contiguous K-slices of 128-blocks per tile; the slices combine
+//    through LDS at the end;
 //  * the prologue never waits behind the weight stream: each wave first
-//    issues its activation loads and ONE block of weights, fills its share of
-//    the codebook table from scalar loads of ct (SMEM, not the vector memory
-//    queue that the weight stream fills), transforms its activations, and
-//    only then streams the rest of its blocks with a two-deep prefetch;
-//  * fused FWHT: wave w transforms only its own blocks of x (one 16-lane
-//    group per block, DPP butterflies) into pair-f16 in LDS;
-//  * A = activation pairs (row m = lane % 16, rows >= M zero), B = table
-//    lookups half2(ct[lo], ct[hi]); block norms scale the fp32 block partial.
+//    issues its activation loads, takes the codebook (kernel arguments, or
+//    scalar loads of ct that do not queue behind the vector weight stream),
+//    issues its first D weight blocks, writes its share of the codebook
+//    table, transforms its activations, and only then streams the rest of
+//    its blocks D deep;
+//  * fused FWHT: each 16-lane group transforms one (row, block) of x (DPP
+//    butterflies) into pair-f16 in LDS;
+//  * A = activation pairs (row m = lane % 16; rows >= M repeat row M - 1 and
+//    are discarded), B = table lookups half2(ct[lo], ct[hi]); block norms
+//    scale the fp32 block partial.
 
 #include "pe_internal.h"
 
@@ -46,8 +49,8 @@ struct DecSrc {
   uint32_t voff_codes, voff_norms;
 };
 
-constexpr int kBufNT = 2;
-constexpr int kBufFlags = 0x00020000;  // raw buffer, 32-bit data format (dword 3 of the resource)  // buffer load cache policy: non-temporal (weights are read once)
+constexpr int kBufNT = 2;              // cache policy: non-temporal (weights are read once)
+constexpr int kBufFlags = 0x00020000;  // raw buffer, 32-bit data format (dword 3 of the resource)
 
 template <bool NIB, int TN>
 __device__ __forceinline__ void dec_load(DecBlk<NIB, TN>& k, const DecSrc& src, int b, bool valid,
@@ -84,39 +87,40 @@ __device__ __forceinline__ half8v dec_dequant(uint32_t wl, uint32_t wh, uint32_t
   return __builtin_bit_cast(half8v, u32x4v{p[0], p[1], p[2], p[3]});
 }
 
-// Codebook table. The values come either by value in the kernel arguments
-// (the host passed its copy of ct: they arrive with the other arguments, no
-// dependent memory read on the critical path) or from wave-uniform scalar
-// loads of the device ct (which at least do not queue behind the vector
-// weight stream). Every lane then writes its own copy of each entry.
+// Codebook table. The values come either by value in the kernel arguments,
+// already as fp16 (the host converted its copy of ct: no dependent memory
+// read, no conversion), or from wave-uniform scalar loads of the device ct
+// (which at least do not queue behind the vector weight stream). Every lane
+// then writes its own copy of each entry.
 // Nibble: entry (hi << 4) | lo = half2(ct[lo], ct[hi]) (the 16 values are the
 // whole codebook), wave w takes hi = w and w + NW; int8: entry e = fp16(ct[e])
 // in the low half, wave w takes e = 16 w .. 16 w + 15 and 16 (w + NW) .. + 15.
 // NW >= 8 covers 256 entries.
-template <bool NIB>
-struct DecTable {
-  float c[NIB ? 16 : 32];  // nibble: ct[0..15] (clamped); int8: two 16-entry chunks
-};
 
-// Codebook by value, entries past n_levels repeat the last one.
+// Codebook by value: fp16 bits, two per dword (v[i] = ct[2 i] | ct[2 i + 1] << 16);
+// entries past n_levels repeat the last one.
 template <bool NIB>
 struct DecCtArg {
-  float v[NIB ? 16 : 256];
+  uint32_t v[NIB ? 8 : 128];
 };
 
-template <bool NIB, int NW>
+template <bool NIB>
+struct DecTable {
+  uint32_t h[NIB ? 16 : 32];  // fp16 bits: nibble ct[0..15]; int8 the wave's two 16-entry chunks
+};
+
+template <bool NIB, int NW, bool CTV>
 __device__ __forceinline__ void dec_table_load(DecTable<NIB>& t, const float* __restrict__ ct,
-                                               const DecCtArg<NIB>& ctv, bool by_value,
-                                               int n_levels, int wave) {
+                                               const DecCtArg<NIB>& ctv, int n_levels, int wave) {
   const int last = n_levels - 1;
+  auto half_of = [&](int e) -> uint32_t {  // fp16 bits of entry e (uniform)
+    const uint32_t w = ctv.v[e >> 1];
+    return (e & 1) ? (w >> 16) : (w & 0xffffu);
+  };
   if constexpr (NIB) {
-    if (by_value) {
 #pragma unroll
-      for (int lo = 0; lo < 16; ++lo) t.c[lo] = ctv.v[lo];
-    } else {
-#pragma unroll
-      for (int lo = 0; lo < 16; ++lo) t.c[lo] = ct[lo < n_levels ? lo : last];
-    }
+    for (int lo = 0; lo < 16; ++lo)
+      t.h[lo] = CTV ? half_of(lo) : (uint32_t)f2h_bits(ct[lo < n_levels ? lo : last]);
   } else {
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -124,12 +128,13 @@ __device__ __forceinline__ void dec_table_load(DecTable<NIB>& t, const float* __
       for (int k = 0; k < 16; ++k) {
         const int e = (wave + h * NW) * 16 + k;
         const int ec = e < n_levels ? e : last;
-        t.c[h * 16 + k] = by_value ? ctv.v[ec] : ct[ec];
+        t.h[h * 16 + k] = CTV ? half_of(ec < 255 ? ec : 255) : (uint32_t)f2h_bits(ct[ec]);
       }
   }
 }
 
-template <bool NIB, int NW>
+// FULL: n_levels is the whole code range (16 or 256), every entry exists
+template <bool NIB, int NW, bool FULL>
 __device__ __forceinline__ void dec_table_write(const DecTable<NIB>& t, int n_levels, int wave,
                                                 uint32_t lane4) {
   if constexpr (NIB) {
@@ -137,13 +142,13 @@ __device__ __forceinline__ void dec_table_write(const DecTable<NIB>& t, int n_le
     for (int h = 0; h < 2; ++h) {
       const int hi = wave + h * NW;
       if (hi < n_levels) {
-        float chi = t.c[0];  // ct[hi] by a uniform select (no further load)
+        uint32_t chi = t.h[0];  // ct[hi] by a uniform select (no further load)
 #pragma unroll
-        for (int k = 1; k < 16; ++k) chi = hi == k ? t.c[k] : chi;
+        for (int k = 1; k < 16; ++k) chi = hi == k ? t.h[k] : chi;
+        const uint32_t base = ((uint32_t)hi << 12) | lane4;
 #pragma unroll
         for (int lo = 0; lo < 16; ++lo)
-          if (lo < n_levels)
-            lds_st32((uint32_t)((hi << 4) | lo) << 8 | lane4, pack_h2(t.c[lo], chi));
+          if (FULL || lo < n_levels) lds_st32(base + ((uint32_t)lo << 8), t.h[lo] | (chi << 16));
       }
     }
   } else {
@@ -152,7 +157,7 @@ __device__ __forceinline__ void dec_table_write(const DecTable<NIB>& t, int n_le
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
         const int e = (wave + h * NW) * 16 + k;
-        if (e < n_levels) lds_st32((uint32_t)e << 8 | lane4, (uint32_t)f2h_bits(t.c[h * 16 + k]));
+        if (FULL || e < n_levels) lds_st32((uint32_t)e << 8 | lane4, t.h[h * 16 + k]);
       }
   }
 }
@@ -162,13 +167,13 @@ __device__ __forceinline__ void dec_table_write(const DecTable<NIB>& t, int n_le
 // NW = TN * KS waves: wave w works on tile w % TN over the K-slice w / TN
 // (contiguous 128-blocks), streaming it D blocks deep. XC: activation
 // registers per lane.
-template <bool NIB, int TN, int KS, bool XRAW, bool MASK, int XC, int D>
+template <bool NIB, int TN, int KS, bool XRAW, bool MASK, int XC, int D, bool CTV>
 __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
     const float* __restrict__ ct, int n_levels, uint32_t code_mask,
     const void* __restrict__ x, int64_t ldx, void* __restrict__ y, int64_t ldy,
     const uint16_t* __restrict__ bias, int M, int N, int nb, uint32_t xs_addr, WLayout lay,
-    DecCtArg<NIB> ctv, int ct_by_value) {
+    DecCtArg<NIB> ctv) {
   constexpr int NW = TN * KS;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -190,8 +195,9 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
     int n = (blockIdx.x * TN + jt) * 16 + l16;
     n = n < N ? n : N - 1;
     // extents up to the last row's end (< 2 GiB: host check)
-    const int codes_bytes = (int)(lay.codes_off(N - 1) + (int64_t)nb * lay.c_blk);
-    const int norms_bytes = (int)(lay.norms_off(N - 1) + (int64_t)nb * lay.n_blk) * 2;
+    const int codes_bytes =
+        (int)(lay.codes_off(N - 1) + (int64_t)(nb - 1) * lay.c_blk + (NIB ? 64 : kBlock));
+    const int norms_bytes = (int)(lay.norms_off(N - 1) + (int64_t)(nb - 1) * lay.n_blk + 1) * 2;
     src.codes = __builtin_amdgcn_make_buffer_rsrc((void*)codes, (short)0, codes_bytes, kBufFlags);
     src.codes_none = __builtin_amdgcn_make_buffer_rsrc((void*)codes, (short)0, 0, kBufFlags);
     src.norms = __builtin_amdgcn_make_buffer_rsrc((void*)norms, (short)0, norms_bytes, kBufFlags);
@@ -231,7 +237,7 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
   __builtin_amdgcn_sched_barrier(0);
   // codebook values (scalar loads: they do not queue behind the weight stream)
   DecTable<NIB> tab;
-  dec_table_load<NIB, NW>(tab, ct, ctv, ct_by_value != 0, n_levels, wave);
+  dec_table_load<NIB, NW, CTV>(tab, ct, ctv, n_levels, wave);
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
@@ -245,7 +251,7 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
   }
 
   // ---- 1. codebook table (all waves)
-  dec_table_write<NIB, NW>(tab, n_levels, wave, lane4);
+  dec_table_write<NIB, NW, !MASK>(tab, n_levels, wave, lane4);
 
   // ---- 2. activations into LDS as pair f16: 256 B per (row, block), pair p
   // = (x_tf[128 b + p], x_tf[128 b + 64 + p]) at byte 4 p. XRAW: FWHT of the
@@ -372,11 +378,13 @@ static size_t dec_lds(bool nibble, int M, int nb, int n_levels, int nw) {
   return lds < red ? red : lds;
 }
 
-template <bool NIB, int TN, bool XRAW, bool MASK, int XC>
+template <bool NIB, int TN, bool XRAW, bool MASK, int XC, bool CTV>
 static int launch_dec(const DecArgs& a, hipStream_t st) {
   constexpr int KS = dec_ks<TN>(), NW = TN * KS;
-  constexpr int D = NIB ? 3 : 2;  // blocks in flight per wave (nibble 1 KB, int8 2 KB each)
-  auto kern = gemv_mfma_kernel<NIB, TN, KS, XRAW, MASK, XC, D>;
+  // blocks in flight per wave (nibble 1 KB, int8 2 KB each); deeper rings
+  // measured slower (3 -> 8: 7.6 -> 8.8 us on Q4 12288 x 4096)
+  constexpr int D = NIB ? 3 : 2;
+  auto kern = gemv_mfma_kernel<NIB, TN, KS, XRAW, MASK, XC, D, CTV>;
   const size_t lds = dec_lds(NIB, a.M, a.nb, a.n_levels, NW);
   if (lds > 160 * 1024 || dec_xc(a.M, a.nb, NW) > XC) return PE_ERR_DIMS;
   static const bool attr_ok = [&] {
@@ -388,22 +396,35 @@ static int launch_dec(const DecArgs& a, hipStream_t st) {
   const uint8_t mb = NIB ? (uint8_t)((a.n_levels - 1) * 0x11) : (uint8_t)(a.n_levels - 1);
   const uint32_t xs_addr = (uint32_t)table_entries(NIB, a.n_levels) * 256u;
   DecCtArg<NIB> ctv;
-  constexpr int kCtv = (int)(sizeof(ctv.v) / sizeof(float));
-  for (int e = 0; e < kCtv; ++e) ctv.v[e] = a.ct_host ? a.ct_host[e < a.n_levels ? e : a.n_levels - 1] : 0.f;
+  constexpr int kCtv = (int)(sizeof(ctv.v) / sizeof(uint32_t));
+  for (int i = 0; i < kCtv; ++i) {
+    uint32_t w = 0;
+    if (CTV)
+      for (int q = 0; q < 2; ++q) {
+        const int e = 2 * i + q;
+        w |= (uint32_t)host_f2h(a.ct_host[e < a.n_levels ? e : a.n_levels - 1]) << (16 * q);
+      }
+    ctv.v[i] = w;
+  }
   kern<<<dim3(tiles), dim3(NW * 64), lds, st>>>(a.codes, a.norms, a.ct, a.n_levels,
                                                0x01010101u * mb, a.x, a.ldx, a.y, a.ldy, a.bias,
-                                               a.M, a.N, a.nb, xs_addr, a.lay, ctv,
-                                               a.ct_host ? 1 : 0);
+                                               a.M, a.N, a.nb, xs_addr, a.lay, ctv);
   return launch_status();
 }
 
 template <bool NIB, int TN, bool XRAW, bool MASK>
 static int launch_dec_xc(const DecArgs& a, hipStream_t st) {
   const int xc = dec_xc(a.M, a.nb, TN * dec_ks<TN>());
-  if (xc <= 1) return launch_dec<NIB, TN, XRAW, MASK, 1>(a, st);
-  if (xc <= 2) return launch_dec<NIB, TN, XRAW, MASK, 2>(a, st);
-  if (xc <= 4) return launch_dec<NIB, TN, XRAW, MASK, 4>(a, st);
-  return launch_dec<NIB, TN, XRAW, MASK, 8>(a, st);
+  if (a.ct_host) {
+    if (xc <= 1) return launch_dec<NIB, TN, XRAW, MASK, 1, true>(a, st);
+    if (xc <= 2) return launch_dec<NIB, TN, XRAW, MASK, 2, true>(a, st);
+    if (xc <= 4) return launch_dec<NIB, TN, XRAW, MASK, 4, true>(a, st);
+    return launch_dec<NIB, TN, XRAW, MASK, 8, true>(a, st);
+  }
+  if (xc <= 1) return launch_dec<NIB, TN, XRAW, MASK, 1, false>(a, st);
+  if (xc <= 2) return launch_dec<NIB, TN, XRAW, MASK, 2, false>(a, st);
+  if (xc <= 4) return launch_dec<NIB, TN, XRAW, MASK, 4, false>(a, st);
+  return launch_dec<NIB, TN, XRAW, MASK, 8, false>(a, st);
 }
 
 // n-tiles per workgroup: the fewest rounds of one workgroup per CU, each
