@@ -16,11 +16,11 @@
 //    KS contiguous K-slices of 128-blocks per tile; the slices combine
 //    through LDS at the end;
 //  * the prologue never waits behind the weight stream: each wave first
-//    issues its activation loads, takes the codebook (kernel arguments, or
-//    scalar loads of ct that do not queue behind the vector weight stream),
-//    issues its first D weight blocks, writes its share of the codebook
-//    table, transforms its activations, and only then streams the rest of
-//    its blocks D deep;
+//    issues its activation loads and takes the codebook (kernel arguments,
+//    or scalar loads of ct that do not queue behind the vector weight
+//    stream); after a workgroup barrier (every activation load is queued)
+//    it issues its first D weight blocks, writes its share of the codebook
+//    table, transforms its activations, and streams the rest D deep;
 //  * fused FWHT: each 16-lane group transforms one (row, block) of x (DPP
 //    butterflies) into pair-f16 in LDS;
 //  * A = activation pairs (row m = lane % 16; rows >= M repeat row M - 1 and
@@ -133,7 +133,8 @@ __device__ __forceinline__ void dec_table_load(DecTable<NIB>& t, const float* __
   }
 }
 
-// FULL: n_levels is the whole code range (16 or 256), every entry exists
+// FULL: n_levels is the whole code range (16 or 256): every entry of a
+// chunk exists, no per-entry test
 template <bool NIB, int NW, bool FULL>
 __device__ __forceinline__ void dec_table_write(const DecTable<NIB>& t, int n_levels, int wave,
                                                 uint32_t lane4) {
@@ -153,12 +154,16 @@ __device__ __forceinline__ void dec_table_write(const DecTable<NIB>& t, int n_le
     }
   } else {
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < 2; ++h) {
+      const int chunk = wave + h * NW;  // entries 16 chunk .. 16 chunk + 15 (uniform)
+      if (chunk < 16) {                 // never past entry 255: the activations follow
 #pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const int e = (wave + h * NW) * 16 + k;
-        if (FULL || e < n_levels) lds_st32((uint32_t)e << 8 | lane4, t.h[h * 16 + k]);
+        for (int k = 0; k < 16; ++k) {
+          const int e = chunk * 16 + k;
+          if (FULL || e < n_levels) lds_st32((uint32_t)e << 8 | lane4, t.h[h * 16 + k]);
+        }
       }
+    }
   }
 }
 
@@ -209,7 +214,9 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
   // ---- 0. activations: the workgroup's M x nb (row, block) items are spread
   // over its 4 NW 16-lane groups: group gi = 4 wave + g takes items
   // gi + 4 NW i (i < XC), lane l16 holding elements 8 l16 .. 8 l16 + 7.
-  // Unconditional (clamped) loads, queued on the CU before any weight load.
+  // Unconditional (clamped) loads, queued on the CU before any weight load
+  // (the activations are on the critical path of the prologue; the weight
+  // blocks are not needed before the K loop).
   const int nitems = M * nb;
   const int gi = wave * 4 + g;
   int it_m, it_b;
@@ -242,7 +249,8 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- first D blocks of weights: the stream starts before the prologue
+  // ---- first D blocks of weights: the stream starts before the rest of the
+  // prologue
   DecBlk<NIB, 1> ring[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) {
