@@ -179,6 +179,16 @@ int pe_tile_weights(const void* codes, const uint16_t* norms, int64_t N, int row
 int pe_unpack_q5(const uint8_t* packed, int8_t* codes, int64_t rows, int64_t K, void* stream);
 
 /*
+ * HLWQ bit-packed codes (bitpack_5, MSB-first: 8 codes in 5 bytes) to int8
+ * codes, bit-exact: replaces unpack_codes_q5_hlwq (packing.py:229-271) as the
+ * loader uses it for the "hlwq-q5" format (loader.py:332-360). packed is the
+ * flat byte stream (packed_bytes a multiple of 5); the first `total` codes are
+ * written to codes int8 [total].
+ */
+int pe_unpack_q5_hlwq(const uint8_t* packed, int64_t packed_bytes, int8_t* codes, int64_t total,
+                      void* stream);
+
+/*
  * MoE routing: scores (softmax or sigmoid of logits + optional correction
  * bias) -> top-k (ties to the lower expert id) -> optional renormalise.
  * Semantics of the routing in nemotron_offload.py:172-189 with the argument

@@ -59,6 +59,26 @@ __global__ __launch_bounds__(256) void unpack_q5_kernel(const uint8_t* __restric
   *reinterpret_cast<uint2*>(codes + t * 8) = make_uint2(w0, w1);
 }
 
+// HLWQ bitpack_5, MSB-first: lane t turns 5 bytes into 8 codes; groups past
+// `total` codes are cut on the last group (codes beyond total are not written)
+__global__ __launch_bounds__(256) void unpack_q5_hlwq_kernel(const uint8_t* __restrict__ packed,
+                                                             int8_t* __restrict__ codes,
+                                                             int64_t total) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t first = t * 8;
+  if (first >= total) return;
+  const uint8_t* p = packed + t * 5;
+  const uint32_t b0 = p[0], b1 = p[1], b2 = p[2], b3 = p[3], b4 = p[4];
+  // the 40 bits b0..b4 read MSB-first; code j = bits 35 - 5 j .. 39 - 5 j
+  const uint64_t w = ((uint64_t)b0 << 32) | ((uint64_t)b1 << 24) | ((uint64_t)b2 << 16) |
+                     ((uint64_t)b3 << 8) | (uint64_t)b4;
+  int8_t c[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) c[j] = (int8_t)((w >> (35 - 5 * j)) & 0x1f);
+  const int64_t n = total - first < 8 ? total - first : 8;
+  for (int j = 0; j < n; ++j) codes[first + j] = c[j];
+}
+
 // lane t moves 16 bytes of codes: destination chunk t of codes_t
 // [tiles][nb][16][bpb], source row tile*16 + r, block b, bytes c*16 .. +15
 __global__ __launch_bounds__(256) void tile_codes_kernel(const uint8_t* __restrict__ codes,
@@ -138,5 +158,18 @@ extern "C" int pe_unpack_q5(const uint8_t* packed, int8_t* codes, int64_t rows, 
   if (groups > (int64_t(1) << 31)) return PE_ERR_DIMS;
   pe::unpack_q5_kernel<<<dim3((unsigned)((groups + 255) / 256)), dim3(256), 0,
                          reinterpret_cast<hipStream_t>(stream)>>>(packed, codes, groups);
+  return pe::launch_status();
+}
+
+extern "C" int pe_unpack_q5_hlwq(const uint8_t* packed, int64_t packed_bytes, int8_t* codes,
+                                 int64_t total, void* stream) {
+  if (!codes || !packed) return PE_ERR_NULL;
+  if (packed_bytes < 0 || packed_bytes % 5 || total < 0) return PE_ERR_DIMS;
+  if (total > packed_bytes / 5 * 8) return PE_ERR_DIMS;
+  if (total == 0) return PE_OK;
+  const int64_t groups = (total + 7) / 8;
+  if (groups > (int64_t(1) << 31)) return PE_ERR_DIMS;
+  pe::unpack_q5_hlwq_kernel<<<dim3((unsigned)((groups + 255) / 256)), dim3(256), 0,
+                              reinterpret_cast<hipStream_t>(stream)>>>(packed, codes, total);
   return pe::launch_status();
 }

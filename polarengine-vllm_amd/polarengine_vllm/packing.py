@@ -7,8 +7,9 @@
 * HLWQ ``bitpack_5``, MSB-first (packing.py:212-290).
 
 Device (GPU) tensors are packed/unpacked by the HIP kernels
-``pe_pack_nibble`` / ``pe_unpack_q5`` (bit-exact); CPU tensors, which only
-appear in offline checkpoint tooling, use the torch expressions below.
+``pe_pack_nibble`` / ``pe_unpack_q5`` / ``pe_unpack_q5_hlwq`` (bit-exact);
+CPU tensors, which only appear in offline checkpoint tooling, use the torch
+expressions below.
 """
 
 from __future__ import annotations
@@ -132,9 +133,21 @@ def unpack_codes_q5(packed: torch.Tensor, block_size: int = 128) -> torch.Tensor
 
 
 def unpack_codes_q5_hlwq(packed: torch.Tensor, total: int | None = None) -> torch.Tensor:
-    """HLWQ ``bitpack_5`` (MSB-first) -> int8 codes, optionally truncated."""
+    """HLWQ ``bitpack_5`` (MSB-first) -> int8 codes, optionally truncated
+    (reference: packing.py:229-271). GPU tensors: ``pe_unpack_q5_hlwq``."""
     *lead, kp = packed.shape
     assert kp % 5 == 0, f"HLWQ bit-packed codes require K_packed % 5 == 0, got {kp}"
+    if _on_gpu(packed) and not lead:
+        from polarengine_vllm import _lib
+        src = packed.contiguous()
+        n = kp * 8 // 5 if total is None else int(total)
+        if n > kp * 8 // 5:
+            raise ValueError(f"total={n} exceeds the {kp * 8 // 5} codes of the packed stream")
+        out = torch.empty(n, dtype=torch.int8, device=packed.device)
+        _lib.check(_lib.lib().pe_unpack_q5_hlwq(src.data_ptr(), kp, out.data_ptr(), n,
+                                                _lib.stream_ptr(packed.device)),
+                   "pe_unpack_q5_hlwq")
+        return out
     p = packed.to(torch.long).reshape(*lead, kp // 5, 5)
     b0, b1, b2, b3, b4 = p.unbind(-1)
     out = torch.stack([
