@@ -179,6 +179,19 @@ int pe_tile_weights(const void* codes, const uint16_t* norms, int64_t N, int row
 int pe_unpack_q5(const uint8_t* packed, int8_t* codes, int64_t rows, int64_t K, void* stream);
 
 /*
+ * PolarQuant quantizer: weight [N, K] (w_dtype PE_DTYPE_F16 / BF16 / F32, row
+ * stride ldw elements) -> codes and fp16 block norms [N, nb], nb = ceil(K/128).
+ * Replaces PolarQuantizer.quantize_tensor (quantizer.py:206-257): zero-pad K,
+ * per-block L2 norm clamped at 1e-10, unit block times the unnormalised
+ * Hadamard transform, code = first index of the nearest of ct[0..n_levels)
+ * (the raw Lloyd-Max centroids, device float32). pack = 0: int8 codes
+ * [N, nb*128]; pack = 1 (n_levels <= 16): half-block nibbles uint8 [N, nb*64].
+ * codes must be 8-byte aligned.
+ */
+int pe_quantize(const void* w, int w_dtype, int64_t N, int K, int64_t ldw, const float* ct,
+                int n_levels, int pack, void* codes, uint16_t* norms_f16, void* stream);
+
+/*
  * HLWQ bit-packed codes (bitpack_5, MSB-first: 8 codes in 5 bytes) to int8
  * codes, bit-exact: replaces unpack_codes_q5_hlwq (packing.py:229-271) as the
  * loader uses it for the "hlwq-q5" format (loader.py:332-360). packed is the

@@ -160,7 +160,8 @@ __device__ __forceinline__ void fwht_xstage(float v[8], int q) {
   for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(sgn, v[i], lane_xor<M>(v[i]));
 }
 
-__device__ __forceinline__ void fwht128_group16(float v[8], int q) {
+// Unnormalised: v <- H v with H[i][j] = (-1)^popcount(i & j) (entries +-1).
+__device__ __forceinline__ void fwht128_group16_raw(float v[8], int q) {
 #pragma unroll
   for (int h = 1; h < 8; h <<= 1) {
 #pragma unroll
@@ -176,6 +177,10 @@ __device__ __forceinline__ void fwht128_group16(float v[8], int q) {
   fwht_xstage<2>(v, q);
   fwht_xstage<4>(v, q);
   fwht_xstage<8>(v, q);
+}
+
+__device__ __forceinline__ void fwht128_group16(float v[8], int q) {
+  fwht128_group16_raw(v, q);
 #pragma unroll
   for (int i = 0; i < 8; ++i) v[i] *= kInvSqrt128;
 }

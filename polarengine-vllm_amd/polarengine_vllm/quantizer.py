@@ -3,8 +3,10 @@
 ``PolarQuantizer.quantize_tensor`` turns a weight matrix into the
 codes / fp16 norms / ct_scaled triple: pad K to the block, per-block L2 norm
 (clamped at 1e-10), unit blocks rotated by H and scaled by sqrt(bs), code =
-first index of the nearest centroid. Torch ops on whatever device the weight
-is on -- this is checkpoint tooling, not the inference path.
+first index of the nearest centroid. A weight on the GPU (block size 128) is
+quantized by the HIP kernel ``pe_quantize`` in one pass (``pack=True`` also
+writes the half-block nibbles for bits <= 4); a CPU weight takes the torch
+expressions below (offline checkpoint tooling).
 (``quantize_model`` of the reference downloads a model and is not provided.)
 """
 
@@ -37,9 +39,16 @@ class PolarQuantizer:
         self.bit_assignment = bit_assignment or dict(DEFAULT_BIT_ASSIGNMENT)
 
     @torch.no_grad()
-    def quantize_tensor(self, weight: torch.Tensor, bits: int) -> Dict[str, torch.Tensor]:
+    def quantize_tensor(self, weight: torch.Tensor, bits: int,
+                        pack: bool = False) -> Dict[str, torch.Tensor]:
+        """codes int8 [N, Kp] (or nibbles uint8 [N, Kp/2] with ``pack`` on the
+        GPU, bits <= 4), norms fp16 [N, nb], ct_scaled fp32 [2**bits]."""
         bs = self.block_size
         dev = weight.device
+        if dev.type == "cuda" and bs == 128:
+            return _quantize_gpu(weight, bits, pack)
+        if pack:
+            raise ValueError("pack=True needs a GPU weight (the pe_quantize kernel)")
         ct = get_centroids(bits).to(dev)
         H = _hadamard(bs, dev)
         out_f, in_f = weight.shape
@@ -61,3 +70,30 @@ class PolarQuantizer:
             d = (rot.view(e - i, nb, bs).unsqueeze(-1) - ct.view(1, 1, 1, -1)).abs()
             codes[i:e] = d.argmin(dim=-1).to(torch.int8)
         return {"codes": codes.reshape(out_f, kp), "norms": norms.half(), "ct_scaled": ct / scale}
+
+
+def _quantize_gpu(weight: torch.Tensor, bits: int, pack: bool) -> Dict[str, torch.Tensor]:
+    from polarengine_vllm import _lib
+    if weight.dim() != 2:
+        raise ValueError(f"weight must be 2-D, got shape {tuple(weight.shape)}")
+    if pack and bits > 4:
+        raise ValueError(f"nibble packing needs bits <= 4, got {bits}")
+    dtypes = {torch.float16: _lib.PE_DTYPE_F16, torch.bfloat16: _lib.PE_DTYPE_BF16,
+              torch.float32: _lib.PE_DTYPE_F32}
+    w = weight if weight.dtype in dtypes else weight.float()
+    if w.stride(1) != 1:
+        w = w.contiguous()
+    n, k = w.shape
+    kp = (k + 127) // 128 * 128
+    ct = get_centroids(bits).to(device=w.device, dtype=torch.float32).contiguous()
+    codes = torch.empty(n, kp // 2 if pack else kp, device=w.device,
+                        dtype=torch.uint8 if pack else torch.int8)
+    norms = torch.empty(n, kp // 128, device=w.device, dtype=torch.float16)
+    _lib.check(_lib.lib().pe_quantize(w.data_ptr(), dtypes[w.dtype], n, k, w.stride(0),
+                                      ct.data_ptr(), ct.numel(), int(pack), codes.data_ptr(),
+                                      norms.data_ptr(), _lib.stream_ptr(w.device)),
+               "pe_quantize")
+    # divided on the CPU, as the reference does (a GPU division by the scalar
+    # can round differently)
+    ct_scaled = (get_centroids(bits) / math.sqrt(128)).to(device=w.device, dtype=torch.float32)
+    return {"codes": codes, "norms": norms, "ct_scaled": ct_scaled}
