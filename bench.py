@@ -9,8 +9,9 @@ rotate over 16 independent copies (416 MB > the 256 MB Infinity Cache) so
 reads come from HBM; calls are captured in a HIP graph and replayed so the
 host does not gate the ~4 us kernels. Also measured: the same call with one
 weight copy (cache-hot), the M=2048 prefill GEMM (TFLOP/s vs dense fp16 MFMA
-peak), M=4/16 decode, and the oracle's CPU time for the headline call
-(cpu_baseline, numpy, 1 thread) on a bounded sample.
+peak), M=4/16 decode, KV-cache quantize / dequantize, and the oracle's CPU
+time for the headline call (cpu_baseline, numpy, 1 thread) on a bounded
+sample.
 """
 
 from __future__ import annotations
@@ -130,6 +131,26 @@ def time_eager(fn, warmup, steps, dev):
     e1.record()
     torch.cuda.synchronize(dev)
     return e0.elapsed_time(e1) * 1e-3 / steps
+
+
+def kv_extra(dev, n_vec=1 << 21, d=128, bits=3):
+    """KV-cache compression of 2M vectors (256K tokens x 8 KV heads) of
+    head_dim 128 at 3 bits: quantize (bf16 in; codes + bf16 norms out) and
+    dequantize (back to bf16), as HBM GB/s of algorithmic bytes."""
+    from polarengine_vllm.kv_cache import PolarKVQuantizer
+    qz = PolarKVQuantizer(d, bits, str(dev))
+    x = torch.randn(n_vec, d, device=dev, dtype=torch.bfloat16)
+    packed, norms = qz.quantize(x)
+    out = torch.empty_like(x)
+    t_q = time_eager(lambda: qz.quantize(x), 3, 20, dev)
+    t_d = time_eager(lambda: qz.dequantize(packed, norms, (n_vec, d), out=out), 3, 20, dev)
+    b = n_vec * (d * 2 + d * bits // 8 + 2)  # bf16 vectors + codes + bf16 norms
+    res = {}
+    for name, t in (("kv_quantize", t_q), ("kv_dequantize", t_d)):
+        res[name] = {"us_per_call": round(t * 1e6, 1), "GB/s": round(b / t / 1e9, 1),
+                     "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4),
+                     "vectors": n_vec, "head_dim": d, "bits": bits}
+    return res
 
 
 def cpu_baseline(budget_s=15.0):
@@ -266,6 +287,7 @@ def main():
     extra["cache_hot_m1"] = {"us_per_call": round(t_hot * 1e6, 2),
                              "GB/s": round(B / t_hot / 1e9, 1),
                              "note": "one weight copy, Infinity-Cache resident"}
+    extra.update(kv_extra(dev))
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     traffic = None  # HBM bytes per launch from the committed pmc summary, if any

@@ -192,6 +192,24 @@ int pe_quantize(const void* w, int w_dtype, int64_t N, int K, int64_t ldw, const
                 int n_levels, int pack, void* codes, uint16_t* norms_f16, void* stream);
 
 /*
+ * KV-cache compression (replaces PolarKVQuantizer.quantize / dequantize,
+ * kv_cache/cache.py:201-256, and the hybrid ops of kv_cache/triton_kernels.py:
+ * 139-228). head_dim 64, 128 or 256, nbits 2..4, ct = the 2^nbits KV centroids
+ * (device float32, kv_cache/cache.py:27-54).
+ *   pe_kv_quantize:   x [n_vec, head_dim] (x_dtype BF16 / F16 / F32, row
+ *                     stride ldx elements) -> packed uint8 [n_vec,
+ *                     head_dim*nbits/8] in BitPacker order + norms bf16 [n_vec]
+ *   pe_kv_dequantize: packed + norms -> out bf16 [n_vec, head_dim], row stride
+ *                     ldo elements (16-byte aligned rows)
+ */
+int pe_kv_quantize(const void* x, int x_dtype, int64_t n_vec, int head_dim, int64_t ldx,
+                   const float* ct, int nbits, uint8_t* packed, uint16_t* norms_bf16,
+                   void* stream);
+int pe_kv_dequantize(const uint8_t* packed, const uint16_t* norms_bf16, int64_t n_vec,
+                     int head_dim, const float* ct, int nbits, uint16_t* out_bf16, int64_t ldo,
+                     void* stream);
+
+/*
  * HLWQ bit-packed codes (bitpack_5, MSB-first: 8 codes in 5 bytes) to int8
  * codes, bit-exact: replaces unpack_codes_q5_hlwq (packing.py:229-271) as the
  * loader uses it for the "hlwq-q5" format (loader.py:332-360). packed is the

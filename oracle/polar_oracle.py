@@ -35,6 +35,16 @@ hadamard_domain_matmul      equals x @ dequant_weight(...).T (two routes,
                             different algebra); one-hot probe returns
                             ct_scaled[code]*norm
 linear_apply                equals the dense route; bias/half cast semantics
+kv_centroids                golden vectors from the reference's
+                            kv_cache/cache.py get_centroids (tests/golden/
+                            golden_kv.npz); symmetry, monotone levels
+kv_pack / kv_unpack         golden bytes from the reference BitPacker, round
+                            trips, hand-computed KATs of each bit order
+kv_quantize / kv_dequantize golden packed codes, bf16 norms and bf16 outputs
+                            of the reference PolarKVQuantizer (codes up to
+                            fp32 near-ties of the rotation, outputs to 1 bf16
+                            ulp: numpy's and torch's fp32 matmuls round
+                            differently)
 moe_forward                 parity unpinned against vLLM (the reference's MoE
                             compute lives in an absent dependency); pinned
                             against a per-token brute-force loop and the
@@ -464,6 +474,127 @@ def moe_forward(x: np.ndarray, topk_w: np.ndarray, topk_ids: np.ndarray,
                                    block_size)
         out[rows] += topk_w[rows, slots][:, None] * d[:, :hdim]
     return out.astype(np.float16)
+
+
+# ---------------------------------------------------------------------------
+# KV-cache quantizer (reference: polarengine_vllm/kv_cache/cache.py)
+# ---------------------------------------------------------------------------
+
+_KV_CT: Dict[int, np.ndarray] = {}
+
+
+def kv_centroids(nbits: int) -> np.ndarray:
+    """Lloyd-Max levels of the KV cache, float32.
+
+    Reference: kv_cache/cache.py:27-54. Unlike the weight codebook
+    (utils.py:21-68) the interval ends are the finite +-4 of
+    ``linspace(-4, 4, n + 1)``; centroids and boundaries live in float32
+    tensors, so every iteration rounds them to float32; an interval with
+    probability below 1e-12 takes its midpoint.
+    """
+    if nbits in _KV_CT:
+        return _KV_CT[nbits]
+    from scipy.stats import norm as sp_norm
+    n = 1 << nbits
+    bnd = np.linspace(-4.0, 4.0, n + 1).astype(np.float32)
+    ct = np.zeros(n, dtype=np.float32)
+    for _ in range(100):
+        for i in range(n):
+            a, b = float(bnd[i]), float(bnd[i + 1])
+            pa, pb = sp_norm.cdf(a), sp_norm.cdf(b)
+            if pb - pa < 1e-12:
+                ct[i] = np.float32((a + b) / 2)
+            else:
+                ct[i] = np.float32((sp_norm.pdf(a) - sp_norm.pdf(b)) / (pb - pa))
+        for i in range(1, n):
+            bnd[i] = (ct[i - 1] + ct[i]) / np.float32(2)
+    _KV_CT[nbits] = ct
+    return ct
+
+
+def kv_pack(codes: np.ndarray, nbits: int) -> np.ndarray:
+    """BitPacker.pack (kv_cache/cache.py:98-128), rows of D codes, MSB first:
+    2 bits 4 per byte ``c0<<6|c1<<4|c2<<2|c3``; 3 bits 8 codes in 3 bytes;
+    4 bits ``c[2i]<<4 | c[2i+1]`` (the even code in the HIGH nibble, the
+    reverse of the weights' half-block nibbles)."""
+    c = np.asarray(codes).astype(np.int64)
+    n = c.shape[0]
+    if nbits == 2:
+        g = c.reshape(n, -1, 4)
+        out = (g[..., 0] << 6) | (g[..., 1] << 4) | (g[..., 2] << 2) | g[..., 3]
+    elif nbits == 3:
+        g = c.reshape(n, -1, 8)
+        b0 = (g[..., 0] << 5) | (g[..., 1] << 2) | (g[..., 2] >> 1)
+        b1 = ((g[..., 2] & 1) << 7) | (g[..., 3] << 4) | (g[..., 4] << 1) | (g[..., 5] >> 2)
+        b2 = ((g[..., 5] & 3) << 6) | (g[..., 6] << 3) | g[..., 7]
+        out = np.stack([b0, b1, b2], axis=-1).reshape(n, -1)
+    elif nbits == 4:
+        out = (c[:, 0::2] << 4) | c[:, 1::2]
+    else:
+        raise ValueError(f"nbits must be 2, 3 or 4, got {nbits}")
+    return (out & 0xFF).astype(np.uint8)
+
+
+def kv_unpack(packed: np.ndarray, nbits: int, d: int) -> np.ndarray:
+    """BitPacker.unpack (kv_cache/cache.py:130-165) -> int64 codes [N, d]."""
+    p = np.asarray(packed).astype(np.int64)
+    n = p.shape[0]
+    if nbits == 2:
+        out = np.stack([(p >> 6) & 3, (p >> 4) & 3, (p >> 2) & 3, p & 3], axis=-1)
+    elif nbits == 3:
+        g = p.reshape(n, -1, 3)
+        b0, b1, b2 = g[..., 0], g[..., 1], g[..., 2]
+        out = np.stack([(b0 >> 5) & 7, (b0 >> 2) & 7, ((b0 & 3) << 1) | ((b1 >> 7) & 1),
+                        (b1 >> 4) & 7, (b1 >> 1) & 7, ((b1 & 1) << 2) | ((b2 >> 6) & 3),
+                        (b2 >> 3) & 7, b2 & 7], axis=-1)
+    elif nbits == 4:
+        out = np.stack([(p >> 4) & 0xF, p & 0xF], axis=-1)
+    else:
+        raise ValueError(f"nbits must be 2, 3 or 4, got {nbits}")
+    return out.reshape(n, d)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """float32 -> bfloat16 bit patterns, round to nearest even (torch's cast)."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    rounded = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    nan = (u & 0x7F800000) == 0x7F800000
+    rounded = np.where(nan & ((u & 0x7FFFFF) != 0), (u >> 16) | 0x40, rounded)
+    return rounded.astype(np.uint16)
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def kv_rotate(x: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
+    """Per-vector norm (clamped at 1e-10) and ``(x / norm) @ H * sqrt(D)``
+    in float32 (kv_cache/cache.py:216-219)."""
+    flat = np.asarray(x, dtype=np.float32)
+    d = flat.shape[1]
+    nrm = np.maximum(np.sqrt((flat * flat).sum(axis=1, dtype=np.float32)), np.float32(1e-10))
+    rot = ((flat / nrm[:, None]) @ hadamard(d)) * np.float32(math.sqrt(d))
+    return nrm.astype(np.float32), rot.astype(np.float32)
+
+
+def kv_quantize(x: np.ndarray, nbits: int) -> Tuple[np.ndarray, np.ndarray]:
+    """PolarKVQuantizer.quantize (kv_cache/cache.py:201-233) on x [N, D]:
+    codes = first-index argmin |rot - ct|, BitPacker-packed; norms as bf16
+    bit patterns. Returns (packed uint8, norms uint16)."""
+    nrm, rot = kv_rotate(x)
+    ct = kv_centroids(nbits)
+    codes = np.abs(rot[:, :, None] - ct[None, None, :]).argmin(axis=-1)
+    return kv_pack(codes, nbits), f32_to_bf16_bits(nrm)
+
+
+def kv_dequantize(packed: np.ndarray, norms_bf16: np.ndarray, nbits: int, d: int) -> np.ndarray:
+    """PolarKVQuantizer.dequantize (kv_cache/cache.py:235-256):
+    ``((ct[codes] / sqrt(D)) @ H) * norm`` in float32, cast to bf16.
+    Returns bf16 bit patterns [N, d]."""
+    codes = kv_unpack(packed, nbits, d)
+    vals = kv_centroids(nbits)[codes] / np.float32(math.sqrt(d))
+    out = (vals.astype(np.float32) @ hadamard(d)) * bf16_bits_to_f32(norms_bf16)[:, None]
+    return f32_to_bf16_bits(out)
 
 
 # ---------------------------------------------------------------------------

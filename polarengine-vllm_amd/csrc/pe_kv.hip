@@ -1,0 +1,264 @@
+// PolarQuant KV-cache compression on gfx950: quantize K/V vectors into
+// packed codes + bf16 norms, and expand them back to bf16.
+//
+// Replaces PolarKVQuantizer.quantize / dequantize (polarengine_vllm/kv_cache/
+// cache.py:201-256) and the hybrid torch/Triton ops of kv_cache/
+// triton_kernels.py:139-228: per vector of head_dim D (64, 128 or 256), L2 norm
+// clamped at 1e-10, unit vector times the unnormalised Hadamard transform (=
+// (x / |x|) @ H * sqrt(D)), code = first index of the nearest of the 2^nbits
+// KV centroids, codes packed MSB-first exactly as BitPacker does
+// (cache.py:98-128): 2 bits -> c0<<6|c1<<4|c2<<2|c3, 3 bits -> 8 codes in 3
+// bytes, 4 bits -> c[2i]<<4 | c[2i+1]; norms stored as bf16. Dequantize:
+// (ct[code] / sqrt(D)) @ H * norm, cast to bf16.
+//
+// One vector per D/8 lanes, 8 consecutive positions per lane; the transform
+// is the in-lane butterfly plus DPP/swizzle exchanges (inside one 32-lane
+// half), so one wave handles 8, 4 or 2 vectors (D = 64, 128, 256).
+
+#include "pe_internal.h"
+
+namespace pe {
+
+template <int L>  // lanes per vector: 8, 16 or 32 (D = 64, 128, 256)
+__device__ __forceinline__ void fwht_lanes_raw(float v[8], int q) {
+#pragma unroll
+  for (int h = 1; h < 8; h <<= 1) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if ((i & h) == 0) {
+        const float a = v[i], b = v[i + h];
+        v[i] = a + b;
+        v[i + h] = a - b;
+      }
+    }
+  }
+  fwht_xstage<1>(v, q);
+  fwht_xstage<2>(v, q);
+  fwht_xstage<4>(v, q);
+  if constexpr (L >= 16) fwht_xstage<8>(v, q);
+  if constexpr (L >= 32) fwht_xstage<16>(v, q);  // ds_swizzle inside 32 lanes
+}
+
+template <int L>
+__device__ __forceinline__ float lanes_sum(float s) {
+  s += lane_xor<1>(s);
+  s += lane_xor<2>(s);
+  s += lane_xor<4>(s);
+  if constexpr (L >= 16) s += lane_xor<8>(s);
+  if constexpr (L >= 32) s += lane_xor<16>(s);
+  return s;
+}
+
+template <int DT>
+__device__ __forceinline__ float kv_load(const void* x, int64_t i) {
+  if constexpr (DT == PE_DTYPE_F16) return h2f(reinterpret_cast<const uint16_t*>(x)[i]);
+  else if constexpr (DT == PE_DTYPE_BF16) return bf2f(reinterpret_cast<const uint16_t*>(x)[i]);
+  else return reinterpret_cast<const float*>(x)[i];
+}
+
+// 8 codes of one lane -> NB bytes (the lane's share of the row), MSB first
+template <int NB>
+__device__ __forceinline__ void kv_pack8(const uint32_t (&c)[8], uint8_t (&b)[NB]) {
+  if constexpr (NB == 2) {
+    b[0] = (uint8_t)((c[0] << 6) | (c[1] << 4) | (c[2] << 2) | c[3]);
+    b[1] = (uint8_t)((c[4] << 6) | (c[5] << 4) | (c[6] << 2) | c[7]);
+  } else if constexpr (NB == 3) {
+    b[0] = (uint8_t)((c[0] << 5) | (c[1] << 2) | (c[2] >> 1));
+    b[1] = (uint8_t)(((c[2] & 1) << 7) | (c[3] << 4) | (c[4] << 1) | (c[5] >> 2));
+    b[2] = (uint8_t)(((c[5] & 3) << 6) | (c[6] << 3) | c[7]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) b[i] = (uint8_t)((c[2 * i] << 4) | c[2 * i + 1]);
+  }
+}
+
+template <int NB>
+__device__ __forceinline__ void kv_unpack8(const uint8_t (&b)[NB], uint32_t (&c)[8]) {
+  if constexpr (NB == 2) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      c[4 * j] = (b[j] >> 6) & 3;
+      c[4 * j + 1] = (b[j] >> 4) & 3;
+      c[4 * j + 2] = (b[j] >> 2) & 3;
+      c[4 * j + 3] = b[j] & 3;
+    }
+  } else if constexpr (NB == 3) {
+    c[0] = (b[0] >> 5) & 7;
+    c[1] = (b[0] >> 2) & 7;
+    c[2] = ((b[0] & 3) << 1) | ((b[1] >> 7) & 1);
+    c[3] = (b[1] >> 4) & 7;
+    c[4] = (b[1] >> 1) & 7;
+    c[5] = ((b[1] & 1) << 2) | ((b[2] >> 6) & 3);
+    c[6] = (b[2] >> 3) & 7;
+    c[7] = b[2] & 7;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      c[2 * i] = (b[i] >> 4) & 15;
+      c[2 * i + 1] = b[i] & 15;
+    }
+  }
+}
+
+template <int D, int NBITS, int DT>
+__global__ __launch_bounds__(256) void kv_quantize_kernel(const void* __restrict__ x, int64_t ldx,
+                                                          int64_t n_vec,
+                                                          const float* __restrict__ ct,
+                                                          uint8_t* __restrict__ packed,
+                                                          uint16_t* __restrict__ norms) {
+  constexpr int L = D / 8;
+  constexpr int RB = D * NBITS / 8;  // packed bytes per vector
+  const int q = threadIdx.x & (L - 1);
+  const int64_t vec = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / L;
+  const bool live = vec < n_vec;
+  const int64_t vr = live ? vec : 0;  // dead groups work on vector 0, store nothing
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = kv_load<DT>(x, vr * ldx + 8 * q + i);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(v[i], v[i], ss);
+  ss = lanes_sum<L>(ss);
+  float nrm = __builtin_sqrtf(ss);
+  nrm = nrm > 1e-10f ? nrm : 1e-10f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = v[i] / nrm;
+  fwht_lanes_raw<L>(v, q);
+  uint32_t c[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float best = __builtin_fabsf(v[i] - ct[0]);
+    uint32_t bi = 0;
+#pragma unroll
+    for (int l = 1; l < (1 << NBITS); ++l) {
+      const float d = __builtin_fabsf(v[i] - ct[l]);
+      if (d < best) {
+        best = d;
+        bi = (uint32_t)l;
+      }
+    }
+    c[i] = bi;
+  }
+  if (!live) return;
+  uint8_t b[NBITS];
+  kv_pack8<NBITS>(c, b);
+  uint8_t* dst = packed + vec * RB + q * NBITS;
+#pragma unroll
+  for (int i = 0; i < NBITS; ++i) dst[i] = b[i];
+  if (q == 0) norms[vec] = f2bf_bits(nrm);
+}
+
+template <int D, int NBITS>
+__global__ __launch_bounds__(256) void kv_dequantize_kernel(const uint8_t* __restrict__ packed,
+                                                            const uint16_t* __restrict__ norms,
+                                                            int64_t n_vec,
+                                                            const float* __restrict__ ct,
+                                                            uint16_t* __restrict__ out,
+                                                            int64_t ldo) {
+  constexpr int L = D / 8;
+  constexpr int RB = D * NBITS / 8;
+  const int q = threadIdx.x & (L - 1);
+  const int64_t vec = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / L;
+  const bool live = vec < n_vec;
+  const int64_t vr = live ? vec : 0;
+  uint8_t b[NBITS];
+  const uint8_t* src = packed + vr * RB + q * NBITS;
+#pragma unroll
+  for (int i = 0; i < NBITS; ++i) b[i] = src[i];
+  uint32_t c[8];
+  kv_unpack8<NBITS>(b, c);
+  // (ct[c] / sqrt(D)) @ H: the division as the reference does it (fp32 by
+  // fp32(sqrt(D))), the normalised transform as the raw one times 1/sqrt(D)
+  const float sq = D == 64 ? 8.f : D == 128 ? 11.313708498984761f : 16.f;
+  const float inv = D == 64 ? 0.125f : D == 128 ? kInvSqrt128 : 0.0625f;
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = ct[c[i]] / sq;
+  fwht_lanes_raw<L>(v, q);
+  const float nrm = bf2f(norms[vr]);
+  if (!live) return;
+  uint16_t o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = f2bf_bits(v[i] * inv * nrm);
+  *reinterpret_cast<uint4*>(out + vec * ldo + 8 * q) =
+      make_uint4((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16),
+                 (uint32_t)o[4] | ((uint32_t)o[5] << 16), (uint32_t)o[6] | ((uint32_t)o[7] << 16));
+}
+
+template <int D, int NBITS>
+static int launch_kv_q(const void* x, int dt, int64_t ldx, int64_t n, const float* ct,
+                       uint8_t* packed, uint16_t* norms, hipStream_t st) {
+  const int64_t threads = n * (D / 8);
+  const unsigned grid = (unsigned)((threads + 255) / 256);
+  switch (dt) {
+    case PE_DTYPE_BF16: kv_quantize_kernel<D, NBITS, PE_DTYPE_BF16><<<grid, 256, 0, st>>>(x, ldx, n, ct, packed, norms); break;
+    case PE_DTYPE_F16: kv_quantize_kernel<D, NBITS, PE_DTYPE_F16><<<grid, 256, 0, st>>>(x, ldx, n, ct, packed, norms); break;
+    case PE_DTYPE_F32: kv_quantize_kernel<D, NBITS, PE_DTYPE_F32><<<grid, 256, 0, st>>>(x, ldx, n, ct, packed, norms); break;
+    default: return PE_ERR_DTYPE;
+  }
+  return launch_status();
+}
+
+template <int D, int NBITS>
+static int launch_kv_d(const uint8_t* packed, const uint16_t* norms, int64_t n, const float* ct,
+                       uint16_t* out, int64_t ldo, hipStream_t st) {
+  const int64_t threads = n * (D / 8);
+  const unsigned grid = (unsigned)((threads + 255) / 256);
+  kv_dequantize_kernel<D, NBITS><<<grid, 256, 0, st>>>(packed, norms, n, ct, out, ldo);
+  return launch_status();
+}
+
+template <int D>
+static int kv_q_bits(int nbits, const void* x, int dt, int64_t ldx, int64_t n, const float* ct,
+                     uint8_t* packed, uint16_t* norms, hipStream_t st) {
+  switch (nbits) {
+    case 2: return launch_kv_q<D, 2>(x, dt, ldx, n, ct, packed, norms, st);
+    case 3: return launch_kv_q<D, 3>(x, dt, ldx, n, ct, packed, norms, st);
+    case 4: return launch_kv_q<D, 4>(x, dt, ldx, n, ct, packed, norms, st);
+    default: return PE_ERR_BITS;
+  }
+}
+
+template <int D>
+static int kv_d_bits(int nbits, const uint8_t* packed, const uint16_t* norms, int64_t n,
+                     const float* ct, uint16_t* out, int64_t ldo, hipStream_t st) {
+  switch (nbits) {
+    case 2: return launch_kv_d<D, 2>(packed, norms, n, ct, out, ldo, st);
+    case 3: return launch_kv_d<D, 3>(packed, norms, n, ct, out, ldo, st);
+    case 4: return launch_kv_d<D, 4>(packed, norms, n, ct, out, ldo, st);
+    default: return PE_ERR_BITS;
+  }
+}
+
+}  // namespace pe
+
+extern "C" int pe_kv_quantize(const void* x, int x_dtype, int64_t n_vec, int head_dim,
+                              int64_t ldx, const float* ct, int nbits, uint8_t* packed,
+                              uint16_t* norms_bf16, void* stream) {
+  if (!x || !ct || !packed || !norms_bf16) return PE_ERR_NULL;
+  if (n_vec < 0 || (head_dim != 64 && head_dim != 128 && head_dim != 256) || ldx < head_dim)
+    return PE_ERR_DIMS;
+  if (nbits < 2 || nbits > 4) return PE_ERR_BITS;
+  if (n_vec == 0) return PE_OK;
+  if (n_vec * (head_dim / 8) > ((int64_t)1 << 38)) return PE_ERR_DIMS;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (head_dim == 64) return pe::kv_q_bits<64>(nbits, x, x_dtype, ldx, n_vec, ct, packed, norms_bf16, st);
+  if (head_dim == 128) return pe::kv_q_bits<128>(nbits, x, x_dtype, ldx, n_vec, ct, packed, norms_bf16, st);
+  return pe::kv_q_bits<256>(nbits, x, x_dtype, ldx, n_vec, ct, packed, norms_bf16, st);
+}
+
+extern "C" int pe_kv_dequantize(const uint8_t* packed, const uint16_t* norms_bf16, int64_t n_vec,
+                                int head_dim, const float* ct, int nbits, uint16_t* out_bf16,
+                                int64_t ldo, void* stream) {
+  if (!packed || !norms_bf16 || !ct || !out_bf16) return PE_ERR_NULL;
+  if (n_vec < 0 || (head_dim != 64 && head_dim != 128 && head_dim != 256) || ldo < head_dim)
+    return PE_ERR_DIMS;
+  if (nbits < 2 || nbits > 4) return PE_ERR_BITS;
+  if (!pe::aligned16(out_bf16) || (ldo * 2) % 16) return PE_ERR_ALIGN;
+  if (n_vec == 0) return PE_OK;
+  if (n_vec * (head_dim / 8) > ((int64_t)1 << 38)) return PE_ERR_DIMS;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (head_dim == 64) return pe::kv_d_bits<64>(nbits, packed, norms_bf16, n_vec, ct, out_bf16, ldo, st);
+  if (head_dim == 128) return pe::kv_d_bits<128>(nbits, packed, norms_bf16, n_vec, ct, out_bf16, ldo, st);
+  return pe::kv_d_bits<256>(nbits, packed, norms_bf16, n_vec, ct, out_bf16, ldo, st);
+}

@@ -48,6 +48,8 @@ _SIGNATURES = {
     "pe_pack_nibble": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
     "pe_unpack_q5": (_c_int, [_vp, _vp, _c_i64, _c_i64, _vp]),
     "pe_unpack_q5_hlwq": (_c_int, [_vp, _c_i64, _vp, _c_i64, _vp]),
+    "pe_kv_quantize": (_c_int, [_vp, _c_int, _c_i64, _c_int, _c_i64, _vp, _c_int, _vp, _vp, _vp]),
+    "pe_kv_dequantize": (_c_int, [_vp, _vp, _c_i64, _c_int, _vp, _c_int, _vp, _c_i64, _vp]),
     "pe_quantize": (_c_int, [_vp, _c_int, _c_i64, _c_int, _c_i64, _vp, _c_int, _c_int, _vp, _vp,
                              _vp]),
     "pe_tile_weights": (_c_int, [_vp, _vp, _c_i64, _c_int, _c_int, _vp, _vp, _vp]),
