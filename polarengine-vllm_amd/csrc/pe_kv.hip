@@ -121,23 +121,25 @@ __global__ __launch_bounds__(256) void kv_quantize_kernel(const void* __restrict
   ss = lanes_sum<L>(ss);
   float nrm = __builtin_sqrtf(ss);
   nrm = nrm > 1e-10f ? nrm : 1e-10f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = v[i] / nrm;
+  // rotated = (x / |x|) @ H * sqrt(D) = (raw transform of x) / |x|: the
+  // transform runs on x and one reciprocal scales the result
   fwht_lanes_raw<L>(v, q);
+  const float inv = 1.f / nrm;
+  // First-index argmin of |r - ct[l]| over ascending centroids = the number
+  // of midpoints (ct[l] + ct[l+1]) / 2 strictly below r (a tie at a midpoint
+  // keeps the lower index); 2 VALU ops per level instead of a distance scan.
+  constexpr int NL = 1 << NBITS;
+  float mid[NL - 1];
+#pragma unroll
+  for (int l = 0; l < NL - 1; ++l) mid[l] = (ct[l] + ct[l + 1]) * 0.5f;
   uint32_t c[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    float best = __builtin_fabsf(v[i] - ct[0]);
-    uint32_t bi = 0;
+    const float r = v[i] * inv;
+    uint32_t k = 0;
 #pragma unroll
-    for (int l = 1; l < (1 << NBITS); ++l) {
-      const float d = __builtin_fabsf(v[i] - ct[l]);
-      if (d < best) {
-        best = d;
-        bi = (uint32_t)l;
-      }
-    }
-    c[i] = bi;
+    for (int l = 0; l < NL - 1; ++l) k += r > mid[l] ? 1u : 0u;
+    c[i] = k;
   }
   if (!live) return;
   uint8_t b[NBITS];
@@ -147,6 +149,10 @@ __global__ __launch_bounds__(256) void kv_quantize_kernel(const void* __restrict
   for (int i = 0; i < NBITS; ++i) dst[i] = b[i];
   if (q == 0) norms[vec] = f2bf_bits(nrm);
 }
+
+// bf16 pair; the conversion from float is gfx950's round-to-nearest-even
+// v_cvt_pk_bf16_f32
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 
 template <int D, int NBITS>
 __global__ __launch_bounds__(256) void kv_dequantize_kernel(const uint8_t* __restrict__ packed,
@@ -168,21 +174,28 @@ __global__ __launch_bounds__(256) void kv_dequantize_kernel(const uint8_t* __res
   uint32_t c[8];
   kv_unpack8<NBITS>(b, c);
   // (ct[c] / sqrt(D)) @ H: the division as the reference does it (fp32 by
-  // fp32(sqrt(D))), the normalised transform as the raw one times 1/sqrt(D)
+  // fp32(sqrt(D))), the normalised transform as the raw one times 1/sqrt(D).
+  // Lane j holds ct[j mod 2^NBITS] / sqrt(D); a code's value is fetched from
+  // lane `code` with ds_bpermute (every lane of the wave takes part).
   const float sq = D == 64 ? 8.f : D == 128 ? 11.313708498984761f : 16.f;
   const float inv = D == 64 ? 0.125f : D == 128 ? kInvSqrt128 : 0.0625f;
+  const int lane = threadIdx.x & 63;
+  const int ctv = __builtin_bit_cast(int, ct[lane & ((1 << NBITS) - 1)] / sq);
   float v[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = ct[c[i]] / sq;
+  for (int i = 0; i < 8; ++i) v[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((int)(c[i] << 2), ctv));
   fwht_lanes_raw<L>(v, q);
   const float nrm = bf2f(norms[vr]);
   if (!live) return;
-  uint16_t o[8];
+  bf16x2v o[4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = f2bf_bits(v[i] * inv * nrm);
+  for (int i = 0; i < 4; ++i) {
+    o[i].x = (__bf16)(v[2 * i] * inv * nrm);
+    o[i].y = (__bf16)(v[2 * i + 1] * inv * nrm);
+  }
   *reinterpret_cast<uint4*>(out + vec * ldo + 8 * q) =
-      make_uint4((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16),
-                 (uint32_t)o[4] | ((uint32_t)o[5] << 16), (uint32_t)o[6] | ((uint32_t)o[7] << 16));
+      make_uint4(__builtin_bit_cast(uint32_t, o[0]), __builtin_bit_cast(uint32_t, o[1]),
+                 __builtin_bit_cast(uint32_t, o[2]), __builtin_bit_cast(uint32_t, o[3]));
 }
 
 template <int D, int NBITS>
