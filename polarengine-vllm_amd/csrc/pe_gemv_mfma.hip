@@ -18,9 +18,12 @@
 //  * the prologue never waits behind the weight stream: each wave first
 //    issues its activation loads and takes the codebook (kernel arguments,
 //    or scalar loads of ct that do not queue behind the vector weight
-//    stream); after a workgroup barrier (every activation load is queued)
-//    it issues its first D weight blocks, writes its share of the codebook
-//    table, transforms its activations, and streams the rest D deep;
+//    stream), then issues its first D weight blocks, writes its share of
+//    the codebook table, transforms its activations, and streams the rest D
+//    deep. D stays small: the CU's memory pipeline is full at about three
+//    1 KB blocks per wave, and a deeper ring only stalls the issuing wave
+//    (its prologue finishes later); a workgroup barrier before the first
+//    weight block (every activation load queued first) measured 3% slower;
 //  * fused FWHT: each 16-lane group transforms one (row, block) of x (DPP
 //    butterflies) into pair-f16 in LDS;
 //  * A = activation pairs (row m = lane % 16; rows >= M repeat row M - 1 and
@@ -245,8 +248,6 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
   // codebook values (scalar loads: they do not queue behind the weight stream)
   DecTable<NIB> tab;
   dec_table_load<NIB, NW, CTV>(tab, ct, ctv, n_levels, wave);
-  __builtin_amdgcn_sched_barrier(0);
-  __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- first D blocks of weights: the stream starts before the rest of the
