@@ -244,6 +244,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--profile-traffic", action="store_true",
                     help="run only the workload of the FETCH_SIZE / WRITE_SIZE pmc passes")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="time only the headline call (for a rocprofv3 kernel trace whose "
+                         "average covers exactly the headline dispatches)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print the traffic JSON from the two pmc passes and exit")
     args = ap.parse_args()
@@ -267,6 +270,10 @@ def main():
     t_call, calls_timed = time_graph(layers, 8, args.warmup, args.steps, dev)
     B = algo_bytes(m, n, k, bits)
     gbs = B / t_call / 1e9
+    if args.headline_only:
+        print(json.dumps({"workload": "headline only", "us_per_call": round(t_call * 1e6, 3),
+                          "GB/s": round(gbs, 1), "calls_timed": calls_timed}))
+        return
     t_hot, _ = time_graph(layers[:1], 128, args.warmup, args.steps, dev)
 
     extra = {}
