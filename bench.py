@@ -9,9 +9,9 @@ rotate over 16 independent copies (416 MB > the 256 MB Infinity Cache) so
 reads come from HBM; calls are captured in a HIP graph and replayed so the
 host does not gate the ~4 us kernels. Also measured: the same call with one
 weight copy (cache-hot), the M=2048 prefill GEMM (TFLOP/s vs dense fp16 MFMA
-peak), M=4/16 decode, KV-cache quantize / dequantize, and the oracle's CPU
-time for the headline call (cpu_baseline, numpy, 1 thread) on a bounded
-sample.
+peak), M=4/16 decode, KV-cache quantize / dequantize, the grouped MoE experts,
+and the oracle's CPU time for the headline call (cpu_baseline, numpy, 1
+thread) on a bounded sample.
 """
 
 from __future__ import annotations
@@ -151,6 +151,42 @@ def kv_extra(dev, n_vec=1 << 21, d=128, bits=3):
                      "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4),
                      "vectors": n_vec, "head_dim": d, "bits": bits}
     return res
+
+
+def moe_extra(dev, t=128, e=64, h=2048, inter=1408, k=8, b13=3, b2=4):
+    """Grouped quantized experts (routing, SwiGLU w13, w2, weighted combine)
+    through PolarQuantMoEMethod.apply: 64 experts, top-8, H=2048, I=1408,
+    w13 Q3 and w2 Q4 nibbles, 128 tokens (1024 token-expert pairs). The
+    stored expert bytes over the call time, as HBM GB/s."""
+    from polarengine_vllm.moe_method import PolarQuantMoEMethod
+    meth = PolarQuantMoEMethod(128, b13, b2)
+    g = torch.Generator(device=dev).manual_seed(11)
+    layers = []
+    for _ in range(2):  # two weight copies in turn: 571 MB > the 256 MB Infinity Cache
+        layer = torch.nn.Module()
+        meth.create_weights(layer, e, h, inter, torch.float16)
+        layer.to(dev)
+        layer.w13_codes.copy_(torch.randint(0, 1 << b13, layer.w13_codes.shape, generator=g, device=dev))
+        layer.w2_codes.copy_(torch.randint(0, 1 << b2, layer.w2_codes.shape, generator=g, device=dev))
+        layer.w13_norms.copy_(torch.rand(layer.w13_norms.shape, generator=g, device=dev) * 0.3 + 0.05)
+        layer.w2_norms.copy_(torch.rand(layer.w2_norms.shape, generator=g, device=dev) * 0.3 + 0.05)
+        meth.process_weights_after_loading(layer)
+        layers.append(layer)
+    x = torch.randn(t, h, generator=g, device=dev).half()
+    logits = torch.randn(t, e, generator=g, device=dev)
+    wbytes = sum(b.numel() * b.element_size() for b in
+                 (layers[0].w13_codes, layers[0].w13_norms, layers[0].w2_codes, layers[0].w2_norms))
+    _, ids = meth.select_experts(logits, k, True)
+    active = int(torch.unique(ids).numel())
+    # replayed from a HIP graph, the two copies in turn, so the host does not
+    # gate the ~60 us call
+    calls = [lambda ly=ly: meth.apply(ly, x, logits, k, True) for ly in layers]
+    tm, _ = time_graph(calls, 4, 16, 64, dev)
+    return {"moe_t128_e64_top8": {"us_per_call": round(tm * 1e6, 1),
+                                  "GB/s": round(wbytes * active / e / tm / 1e9, 1),
+                                  "hbm_frac": round(wbytes * active / e / tm / 1e9 / HBM_PEAK_GBS, 4),
+                                  "expert_bytes": wbytes, "active_experts": active,
+                                  "includes": "routing + align + w13 SwiGLU + w2 + combine"}}
 
 
 def cpu_baseline(budget_s=15.0):
@@ -295,6 +331,7 @@ def main():
                              "GB/s": round(B / t_hot / 1e9, 1),
                              "note": "one weight copy, Infinity-Cache resident"}
     extra.update(kv_extra(dev))
+    extra.update(moe_extra(dev))
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     traffic = None  # HBM bytes per launch from the committed pmc summary, if any

@@ -241,6 +241,10 @@ int pe_moe_route(const float* logits, int64_t T, int E, int top_k, int renormali
  *   w13     : codes [E, 2I, ...] in the runtime layout for (bits13, packed13),
  *             norms float16 [E, 2I, H/128], ct13 float32 [2**bits13];
  *             rows [0, I) are gate, rows [I, 2I) are up
+ *   packed13 / packed2: 1 = nibble codes (bits <= 4), | PE_LAYOUT_TILE16 = each
+ *             expert's codes and norms in the tiled-16 layout (pe_tile_weights
+ *             over the [E * rows, row_bytes] matrix; rows per expert, 2I and H,
+ *             must then be multiples of 16)
  *   w2      : codes [E, H, ...] over in_f = I padded to Ip = ceil(I/128)*128,
  *             norms float16 [E, H, Ip/128], ct2 float32 [2**bits2]
  *   out     : float16 [T, H] = sum_k topk_w[t,k] * expert_{ids[t,k]}(x_t)

@@ -290,6 +290,236 @@ static int launch_small_ep(const SmallArgs& a, int groups, hipStream_t st) {
   return one ? launch_small_t<NIB, 1, EP, 1>(a, groups, st) : launch_small_t<NIB, 1, EP, 2>(a, groups, st);
 }
 
+// ---------------------------------------------------------------------------
+// Grouped expert products for the MoE path: one workgroup of 8 waves per
+// (expert, 128 weight rows); wave w owns the 16-row n-tile 8 x + w (and, for
+// SwiGLU, the matching "up" tile at row n + I) over the WHOLE K range, so its
+// accumulators are final: no cross-wave reduction, the epilogue runs in
+// registers. The expert's activation rows (up to 32 per pass) are staged one
+// 128-block at a time into a two-stage LDS ring shared by the 8 waves (chunk c
+// of row r at chunk c ^ (r & 15): the 16 rows one ds_read_b128 phase touches
+// hit distinct banks); the codes stream through a D-deep register ring.
+// ---------------------------------------------------------------------------
+constexpr int kMoeWaves = 8;
+constexpr int kMoeThreads = 64 * kMoeWaves;
+constexpr int kMoeRows = 32;  // activation rows per pass (two 16-row m-tiles)
+
+template <int NT>
+struct MoeBlk {
+  u32x4v lo[NT];
+  u32x4v hi[NT];
+  uint32_t nbits[NT];  // 32-bit: 16-bit members next to vectors were kept in memory
+};
+
+// Weight source of one lane: buffer resources over this expert's codes and
+// norms (a real one and a zero-length one) and the lane's row offsets. A
+// block past the end reads through the zero-length resource, which returns
+// zeros without touching memory, so every ring slot issues the same loads and
+// the compiler's vmcnt waits stay exact.
+template <int NT>
+struct MoeSrc {
+  __amdgpu_buffer_rsrc_t codes, codes_none, norms, norms_none;
+  uint32_t voff_codes[NT], voff_norms[NT];
+};
+
+constexpr int kMoeBufNT = 2;              // non-temporal: every expert block is read once
+constexpr int kMoeBufFlags = 0x00020000;  // raw buffer, 32-bit data format
+
+template <bool NIB, int NT>
+__device__ __forceinline__ void moe_load_w(MoeBlk<NT>& k, const MoeSrc<NT>& src, int b, int nb,
+                                           const WLayout& lay) {
+  const bool valid = b < nb;
+  const __amdgpu_buffer_rsrc_t rc = valid ? src.codes : src.codes_none;
+  const __amdgpu_buffer_rsrc_t rn = valid ? src.norms : src.norms_none;
+  const int cb = (int)(b * lay.c_blk), nbk = (int)(b * lay.n_blk * 2);
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    k.lo[j] = __builtin_bit_cast(
+        u32x4v, __builtin_amdgcn_raw_buffer_load_b128(rc, src.voff_codes[j], cb, kMoeBufNT));
+    if constexpr (!NIB)
+      k.hi[j] = __builtin_bit_cast(
+          u32x4v, __builtin_amdgcn_raw_buffer_load_b128(rc, src.voff_codes[j], cb + 64, kMoeBufNT));
+    k.nbits[j] = __builtin_amdgcn_raw_buffer_load_b16(rn, src.voff_norms[j], nbk, kMoeBufNT);
+  }
+}
+
+template <bool NIB, int EP, int D>
+__global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint32_t code_mask,
+                                                               int tbl_entries, uint32_t abuf) {
+  constexpr int NT = EP == SE_SWIGLU ? 2 : 1;
+  constexpr uint32_t kStage = kMoeRows * 256;  // bytes per LDS stage
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, g = lane >> 4;
+  const uint32_t lane4 = (uint32_t)lane << 2;
+
+  const int row0 = a.group_off[blockIdx.y];
+  const int M = a.group_off[blockIdx.y + 1] - row0;
+  if (M <= 0) return;  // whole workgroup (uniform)
+  const uint8_t* codes = a.codes + (int64_t)blockIdx.y * a.codes_stride;
+  const uint16_t* norms = a.norms + (int64_t)blockIdx.y * a.norms_stride;
+
+  // this lane's weight rows (clamped; clamped rows are never stored); the
+  // resources cover exactly this expert's codes and norms (< 2 GiB: host check)
+  const int nt = blockIdx.x * kMoeWaves + wave;
+  const int wrows = EP == SE_SWIGLU ? 2 * a.N : a.N;
+  MoeSrc<NT> src;
+  src.codes = __builtin_amdgcn_make_buffer_rsrc((void*)codes, (short)0, (int)a.codes_stride, kMoeBufFlags);
+  src.codes_none = __builtin_amdgcn_make_buffer_rsrc((void*)codes, (short)0, 0, kMoeBufFlags);
+  src.norms = __builtin_amdgcn_make_buffer_rsrc((void*)norms, (short)0, (int)(a.norms_stride * 2), kMoeBufFlags);
+  src.norms_none = __builtin_amdgcn_make_buffer_rsrc((void*)norms, (short)0, 0, kMoeBufFlags);
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    int n = nt * 16 + l16;
+    if (n >= a.N) n = a.N - 1;
+    if (EP == SE_SWIGLU && j == 1) n += a.N;
+    if (n >= wrows) n = wrows - 1;
+    src.voff_codes[j] = (uint32_t)(a.lay.codes_off(n) + 16 * g);
+    src.voff_norms[j] = (uint32_t)(a.lay.norms_off(n) * 2);
+  }
+
+  if constexpr (NIB)
+    fill_codebook<TBL_NIB_H2>(0, a.ct, a.n_levels, tbl_entries, kMoeWaves);
+  else
+    fill_codebook<TBL_F16>(0, a.ct, a.n_levels, tbl_entries, kMoeWaves);
+
+  // staging role of this thread: row sr, 16-byte chunk sc of the 256-byte block row
+  const int sr = tid >> 4, sc = tid & 15;
+  const uint32_t sdst = (uint32_t)sr * 256u + ((uint32_t)(sc ^ (sr & 15)) << 4);
+  const int64_t xrow = (int64_t)a.nb * 64;  // uint32 per activation row
+
+  for (int mbase = 0; mbase < M; mbase += kMoeRows) {
+    const int mrem = M - mbase;
+    const int MT = mrem > 16 ? 2 : 1;
+    const bool salive = sr < kMoeRows && mbase + sr < M;
+    const uint32_t* ssrc = nullptr;
+    if (salive) {
+      int r = row0 + mbase + sr;
+      if (a.a_rows) r = a.a_rows[r];
+      ssrc = a.xp + (int64_t)r * xrow + sc * 4;
+    }
+    auto lda = [&](int b) -> u32x4v {
+      return salive ? *reinterpret_cast<const u32x4v*>(ssrc + (int64_t)b * 64)
+                    : u32x4v{0u, 0u, 0u, 0u};
+    };
+    float4v acc[2][NT];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < NT; ++j) acc[i][j] = float4v{0.f, 0.f, 0.f, 0.f};
+
+    MoeBlk<NT> ring[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      moe_load_w<NIB, NT>(ring[d], src, d, a.nb, a.lay);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    u32x4v sreg = lda(0);
+    if (sr < kMoeRows) lds_st128(abuf + sdst, sreg);
+    if (a.nb > 1) sreg = lda(1);
+    __syncthreads();  // codebook table and stage 0 written
+
+    // A row of this lane in m-tile i: activation row 16 i + l16 of the stage
+    for (int b0 = 0; b0 < a.nb; b0 += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        const int b = b0 + d;
+        if (b < a.nb) {  // uniform
+          const uint32_t st = abuf + (uint32_t)(b & 1) * kStage;
+#pragma unroll
+          for (int j = 0; j < NT; ++j) {
+            float4v blk[2] = {float4v{0.f, 0.f, 0.f, 0.f}, float4v{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const uint32_t wl = ring[d].lo[j][t] & code_mask;
+              const uint32_t wh = NIB ? 0u : (ring[d].hi[j][t] & code_mask);
+              const half8v bf = dequant_slab_raw<NIB>(nullptr, wl, wh, lane4);
+#pragma unroll
+              for (int i = 0; i < 2; ++i) {
+                if (i < MT) {
+                  const int r = 16 * i + l16;
+                  const u32x4v af = lds_ld128(st + (uint32_t)r * 256u +
+                                              ((uint32_t)((4 * g + t) ^ (r & 15)) << 4));
+                  blk[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, af),
+                                                                  bf, blk[i], 0, 0, 0);
+                }
+              }
+            }
+            const float nrm = h2f((uint16_t)ring[d].nbits[j]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) acc[i][j] += blk[i] * nrm;
+          }
+          moe_load_w<NIB, NT>(ring[d], src, b + D, a.nb, a.lay);
+          // next stage: block b + 1 into the other buffer (its readers, block
+          // b - 1, finished before the previous barrier); prefetch b + 2
+          if (b + 1 < a.nb) {
+            if (sr < kMoeRows) lds_st128(abuf + (uint32_t)((b + 1) & 1) * kStage + sdst, sreg);
+            if (b + 2 < a.nb) sreg = lda(b + 2);
+          }
+          __syncthreads();
+        }
+      }
+    }
+
+    // epilogue from registers: D element (lane, e) of m-tile i is row
+    // 16 i + 4 (lane / 16) + e, column 16 nt + lane % 16
+    const int n = nt * 16 + l16;
+    if (n < a.N) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        if (i >= MT) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int m = mbase + 16 * i + 4 * g + e;
+          if (m >= M) continue;
+          const int64_t row = row0 + m;
+          const float s = acc[i][0][e];
+          if constexpr (EP == SE_F32) {
+            reinterpret_cast<float*>(a.y)[row * a.ldy + n] = s;
+          } else {
+            const float u = acc[i][NT - 1][e];
+            const float act = s / (1.f + __expf(-s)) * u;
+            reinterpret_cast<_Float16*>(a.y)[row * a.ldy + n] = (_Float16)act;
+          }
+        }
+      }
+    }
+    __syncthreads();  // stage buffers free before the next pass
+  }
+}
+
+template <bool NIB, int EP>
+static int launch_moe_t(const SmallArgs& a, int groups, hipStream_t st) {
+  constexpr int D = EP == SE_SWIGLU ? 2 : 3;
+  auto kern = moe_gemv_kernel<NIB, EP, D>;
+  const int entries = table_entries(NIB, a.n_levels);
+  const uint32_t abuf = (uint32_t)round_up((size_t)entries * 256, 256);
+  const size_t lds = abuf + 2 * (size_t)kMoeRows * 256;
+  if (lds > 160 * 1024) return PE_ERR_DIMS;
+  static const bool attr_ok = [&] {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+  }();
+  (void)attr_ok;
+  const int wgs = (a.N + 16 * kMoeWaves - 1) / (16 * kMoeWaves);
+  const uint8_t mb = NIB ? (uint8_t)((a.n_levels - 1) * 0x11) : (uint8_t)(a.n_levels - 1);
+  kern<<<dim3(wgs, groups), dim3(kMoeThreads), lds, st>>>(a, 0x01010101u * mb, entries, abuf);
+  return launch_status();
+}
+
+int moe_grouped(bool nibble, int epilogue, const SmallArgs& a, int groups, hipStream_t st) {
+  if (!a.group_off || a.nb <= 0 || a.N <= 0) return PE_ERR_DIMS;
+  // one expert's codes and norms are addressed by 32-bit buffer offsets
+  if (a.codes_stride >= ((int64_t)1 << 31) || a.norms_stride * 2 >= ((int64_t)1 << 31))
+    return PE_ERR_DIMS;
+  switch (epilogue) {
+    case SE_F32: return nibble ? launch_moe_t<true, SE_F32>(a, groups, st) : launch_moe_t<false, SE_F32>(a, groups, st);
+    case SE_SWIGLU: return nibble ? launch_moe_t<true, SE_SWIGLU>(a, groups, st) : launch_moe_t<false, SE_SWIGLU>(a, groups, st);
+    default: return PE_ERR_DTYPE;
+  }
+}
+
 int gemm_small(bool nibble, int epilogue, const SmallArgs& a, int groups, hipStream_t st) {
   switch (epilogue) {
     case SE_F32: return nibble ? launch_small_ep<true, SE_F32>(a, groups, st) : launch_small_ep<false, SE_F32>(a, groups, st);

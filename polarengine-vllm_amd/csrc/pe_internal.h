@@ -89,6 +89,8 @@ struct SmallArgs {
 // pe_gemm_small.hip: M <= kSmallMaxRows per pass is cheapest (larger M loops)
 constexpr int kSmallMaxRows = 64;
 int gemm_small(bool nibble, int epilogue, const SmallArgs& a, int groups, hipStream_t st);
+// grouped expert products (group_off required; epilogue SE_F32 or SE_SWIGLU)
+int moe_grouped(bool nibble, int epilogue, const SmallArgs& a, int groups, hipStream_t st);
 
 // pe_gemv_mfma.hip: decode GEMV, 1 <= M <= 16, fp16 out (+ fp16 bias)
 struct DecArgs {

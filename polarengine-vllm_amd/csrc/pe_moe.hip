@@ -239,9 +239,13 @@ extern "C" int pe_moe_forward(const void* x, int64_t T, int H, int I, int E, int
   for (int which = 0; which < 2; ++which) {
     const int bits = which ? bits2 : bits13, packed = which ? packed2 : packed13;
     const int nl = which ? n_levels2 : n_levels13;
-    if (bits < 2 || bits > 8 || (packed & ~1) || (packed && bits > 4) || nl != (1 << bits))
-      return PE_ERR_BITS;  // experts stay row-major (no PE_LAYOUT_TILE16)
+    if (bits < 2 || bits > 8 || (packed & ~(1 | PE_LAYOUT_TILE16)) || ((packed & 1) && bits > 4) ||
+        nl != (1 << bits))
+      return PE_ERR_BITS;
   }
+  // tiled-16 experts: every expert's rows are whole 16-row tiles
+  if (((packed13 & PE_LAYOUT_TILE16) && (2 * I) % 16) || ((packed2 & PE_LAYOUT_TILE16) && H % 16))
+    return PE_ERR_DIMS;
   if (!aligned16(x) || !aligned16(w13_codes) || !aligned16(w2_codes) || !aligned16(out))
     return PE_ERR_ALIGN;
   if (T == 0) return PE_OK;
@@ -256,7 +260,8 @@ extern "C" int pe_moe_forward(const void* x, int64_t T, int H, int I, int E, int
   int32_t* pair_pos = reinterpret_cast<int32_t*>(ws + L.pair_pos);
   const int Ip = (I + kBlock - 1) / kBlock * kBlock;
   const int nb13 = H / kBlock, nb2 = Ip / kBlock;
-  const bool nib13 = packed13 != 0, nib2 = packed2 != 0;
+  const bool nib13 = (packed13 & 1) != 0, nib2 = (packed2 & 1) != 0;
+  const bool tiled13 = (packed13 & PE_LAYOUT_TILE16) != 0, tiled2 = (packed2 & PE_LAYOUT_TILE16) != 0;
   const int64_t row13 = nib13 ? (int64_t)nb13 * 64 : (int64_t)nb13 * kBlock;
   const int64_t row2 = nib2 ? (int64_t)nb2 * 64 : (int64_t)nb2 * kBlock;
 
@@ -277,8 +282,8 @@ extern "C" int pe_moe_forward(const void* x, int64_t T, int H, int I, int E, int
     SmallArgs a{reinterpret_cast<const uint8_t*>(w13_codes), w13_norms, ct13, n_levels13,
                 reinterpret_cast<const uint32_t*>(ws + L.xtf), sorted_token, offsets,
                 2 * (int64_t)I * row13, 2 * (int64_t)I * nb13, ws + L.h, Ip, nullptr, 0, I,
-                nb13, wlayout(nib13, false, nb13)};
-    if (int rc = gemm_small(nib13, SE_SWIGLU, a, E, st)) return rc;
+                nb13, wlayout(nib13, tiled13, nb13)};
+    if (int rc = moe_grouped(nib13, SE_SWIGLU, a, E, st)) return rc;
   }
   // 4. h -> pair f16
   if (int rc = fwht128(ws + L.h, PE_DTYPE_F16, P, Ip, Ip, ws + L.htf, PE_XTF_PAIR_F16, st)) return rc;
@@ -287,8 +292,8 @@ extern "C" int pe_moe_forward(const void* x, int64_t T, int H, int I, int E, int
     SmallArgs a{reinterpret_cast<const uint8_t*>(w2_codes), w2_norms, ct2, n_levels2,
                 reinterpret_cast<const uint32_t*>(ws + L.htf), nullptr, offsets,
                 (int64_t)H * row2, (int64_t)H * nb2, ws + L.y2, H, nullptr, 0, H, nb2,
-                wlayout(nib2, false, nb2)};
-    if (int rc = gemm_small(nib2, SE_F32, a, E, st)) return rc;
+                wlayout(nib2, tiled2, nb2)};
+    if (int rc = moe_grouped(nib2, SE_F32, a, E, st)) return rc;
   }
   // 6. weighted combine -> out fp16
   const int64_t work = T * (H / 8);

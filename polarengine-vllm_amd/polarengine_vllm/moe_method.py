@@ -13,6 +13,9 @@
 Expert weight layout follows the reference's fallback layout
 (moe_method.py:56-72): w13 [E, 2I, H] (rows [0, I) gate, [I, 2I) up) and
 w2 [E, H, I], here as PolarQuant codes / fp16 norms / ct_scaled per matrix.
+After loading, codes with bits <= 4 are nibble-packed and, when each expert's
+row count is a multiple of 16, both matrices are rearranged into the tiled-16
+runtime layout (one 16-row x 128-block tile of codes is one contiguous read).
 """
 
 from __future__ import annotations
@@ -26,15 +29,22 @@ from polarengine_vllm import _lib
 from polarengine_vllm.utils import get_centroids
 
 
+def _layout(packed: bool, tiled: bool) -> int:
+    """The packed argument of pe_moe_forward: 1 = nibbles, | 2 = tiled-16."""
+    return int(bool(packed)) | (_lib.PE_LAYOUT_TILE16 if tiled else 0)
+
+
 class PolarQuantMoEMethod:
     """Quantized fused-MoE method (vLLM FusedMoEMethodBase interface)."""
 
-    def __init__(self, block_size: int = 128, bits13: int = 3, bits2: int = 4) -> None:
+    def __init__(self, block_size: int = 128, bits13: int = 3, bits2: int = 4,
+                 tile: bool = True) -> None:
         if block_size != 128:
             raise ValueError("the gfx950 kernels implement block_size 128")
         self.block_size = block_size
         self.bits13 = bits13
         self.bits2 = bits2
+        self.tile = tile  # tiled-16 expert layout after loading (else row-major)
 
     def create_weights(self, layer: torch.nn.Module, num_experts: int, hidden_size: int,
                        intermediate_size_per_partition: int, params_dtype: torch.dtype,
@@ -56,10 +66,15 @@ class PolarQuantMoEMethod:
         layer.intermediate_size = i
         layer.w13_packed = False
         layer.w2_packed = False
+        layer.w13_tiled = False
+        layer.w2_tiled = False
 
     def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
-        """ct to the codes' device; nibble-pack matrices with bits <= 4."""
-        from polarengine_vllm.packing import pack_codes_half_block
+        """ct to the codes' device; nibble-pack matrices with bits <= 4; then
+        the tiled-16 layout per expert (``pe_tile_weights`` over the
+        [E * rows, row_bytes] matrix: with rows a multiple of 16 no tile spans
+        two experts)."""
+        from polarengine_vllm.packing import pack_codes_half_block, tile_weights_16
         dev = layer.w13_codes.device
         layer.w13_ct_scaled = layer.w13_ct_scaled.to(dev, torch.float32).contiguous()
         layer.w2_ct_scaled = layer.w2_ct_scaled.to(dev, torch.float32).contiguous()
@@ -69,6 +84,17 @@ class PolarQuantMoEMethod:
         if self.bits2 <= 4 and not layer.w2_packed:
             layer.w2_codes = pack_codes_half_block(layer.w2_codes.contiguous(), self.block_size)
             layer.w2_packed = True
+        if self.tile and dev.type == "cuda":
+            for name in ("w13", "w2"):
+                codes, norms = getattr(layer, f"{name}_codes"), getattr(layer, f"{name}_norms")
+                e, rows, row_bytes = codes.shape
+                if getattr(layer, f"{name}_tiled") or rows % 16:
+                    continue
+                ct, nt = tile_weights_16(codes.reshape(e * rows, row_bytes),
+                                         norms.reshape(e * rows, norms.shape[2]))
+                setattr(layer, f"{name}_codes", ct.view(e, rows, row_bytes))
+                setattr(layer, f"{name}_norms", nt.view(e, rows, norms.shape[2]))
+                setattr(layer, f"{name}_tiled", True)
 
     def select_experts(self, router_logits: torch.Tensor, top_k: int, renormalize: bool,
                        scoring_func: str = "softmax",
@@ -121,9 +147,9 @@ class PolarQuantMoEMethod:
         ws = _lib.workspace(dev, wsb)
         rc = L.pe_moe_forward(
             xs.data_ptr(), t, h, i, e, top_k, w.data_ptr(), ids.data_ptr(),
-            layer.w13_codes.data_ptr(), self.bits13, int(layer.w13_packed),
+            layer.w13_codes.data_ptr(), self.bits13, _layout(layer.w13_packed, layer.w13_tiled),
             layer.w13_norms.data_ptr(), layer.w13_ct_scaled.data_ptr(), 1 << self.bits13,
-            layer.w2_codes.data_ptr(), self.bits2, int(layer.w2_packed),
+            layer.w2_codes.data_ptr(), self.bits2, _layout(layer.w2_packed, layer.w2_tiled),
             layer.w2_norms.data_ptr(), layer.w2_ct_scaled.data_ptr(), 1 << self.bits2,
             out.data_ptr(), _lib.ptr(ws), wsb, _lib.stream_ptr(dev))
         _lib.check(rc, "pe_moe_forward")

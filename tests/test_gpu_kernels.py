@@ -625,14 +625,14 @@ def test_moe_route_matches_oracle(scoring, renorm, with_bias):
     np.testing.assert_allclose(w.cpu().numpy(), w_ref, rtol=2e-6, atol=1e-7)
 
 
-def _moe_layer(rng, e, hdim, inter, b13, b2):
+def _moe_layer(rng, e, hdim, inter, b13, b2, tile=True):
     from polarengine_vllm.moe_method import PolarQuantMoEMethod
     ip = (inter + 127) // 128 * 128
     c13 = rng.integers(0, 1 << b13, (e, 2 * inter, hdim)).astype(np.int8)
     n13 = (np.abs(rng.standard_normal((e, 2 * inter, hdim // 128))) * 0.3 + 0.05).astype(np.float16)
     c2 = rng.integers(0, 1 << b2, (e, hdim, ip)).astype(np.int8)
     n2 = (np.abs(rng.standard_normal((e, hdim, ip // 128))) * 0.3 + 0.05).astype(np.float16)
-    meth = PolarQuantMoEMethod(128, b13, b2)
+    meth = PolarQuantMoEMethod(128, b13, b2, tile=tile)
     layer = torch.nn.Module()
     meth.create_weights(layer, e, hdim, inter, torch.float16)
     layer.to(DEV)
@@ -645,16 +645,20 @@ def _moe_layer(rng, e, hdim, inter, b13, b2):
     return meth, layer, oracle_w
 
 
+@pytest.mark.parametrize("tile", [True, False])
 @pytest.mark.parametrize("t,e,hdim,inter,k,b13,b2", [
     (128, 64, 2048, 1408, 8, 3, 4),   # the MoE config of BASELINE (C5)
     (5, 8, 256, 200, 2, 3, 4),        # I not a multiple of 128 (zero-padded h)
     (80, 4, 256, 256, 2, 4, 5),       # ~40 tokens per expert: several passes
     (3, 16, 512, 384, 1, 5, 6),       # most experts empty; int8 experts
+    (40, 4, 384, 132, 3, 4, 3),       # 2I = 264 rows: w13 stays row-major
 ])
-def test_moe_forward_matches_oracle(t, e, hdim, inter, k, b13, b2):
-    _say(f"moe forward t={t} e={e} h={hdim} i={inter} k={k} q{b13}/q{b2}")
+def test_moe_forward_matches_oracle(t, e, hdim, inter, k, b13, b2, tile):
+    _say(f"moe forward t={t} e={e} h={hdim} i={inter} k={k} q{b13}/q{b2} tile={tile}")
     rng = np.random.default_rng(t + e + hdim)
-    meth, layer, (w13, w2) = _moe_layer(rng, e, hdim, inter, b13, b2)
+    meth, layer, (w13, w2) = _moe_layer(rng, e, hdim, inter, b13, b2, tile)
+    assert layer.w13_tiled == (tile and (2 * inter) % 16 == 0)
+    assert layer.w2_tiled == tile
     x = O.seeded_normal((t, hdim), 1.0, 72)
     logits = O.seeded_normal((t, e), 1.0, 73, np.float32)
     y = meth.apply(layer, to_dev(x), to_dev(logits), k, True)
