@@ -82,6 +82,10 @@ __device__ __forceinline__ void lds_st128(uint32_t addr, u32x4v v) {
 __device__ __forceinline__ void lds_st32(uint32_t addr, uint32_t v) {
   *reinterpret_cast<lds_u32*>(static_cast<uintptr_t>(addr)) = v;
 }
+typedef __attribute__((address_space(3))) uint16_t lds_u16;
+__device__ __forceinline__ void lds_st16(uint32_t addr, uint16_t v) {
+  *reinterpret_cast<lds_u16*>(static_cast<uintptr_t>(addr)) = v;
+}
 typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) u32x2v lds_u32x2;
 __device__ __forceinline__ void lds_st64(uint32_t addr, u32x2v v) {

@@ -346,7 +346,8 @@ __device__ __forceinline__ void moe_load_w(MoeBlk<NT>& k, const MoeSrc<NT>& src,
 template <bool NIB, int EP, int D>
 __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint32_t code_mask,
                                                                int tbl_entries, uint32_t abuf) {
-  constexpr int NT = EP == SE_SWIGLU ? 2 : 1;
+  constexpr bool SWI = EP == SE_SWIGLU || EP == SE_SWIGLU_XTF;
+  constexpr int NT = SWI ? 2 : 1;
   constexpr uint32_t kStage = kMoeRows * 256;  // bytes per LDS stage
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -363,7 +364,7 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
   // this lane's weight rows (clamped; clamped rows are never stored); the
   // resources cover exactly this expert's codes and norms (< 2 GiB: host check)
   const int nt = blockIdx.x * kMoeWaves + wave;
-  const int wrows = EP == SE_SWIGLU ? 2 * a.N : a.N;
+  const int wrows = SWI ? 2 * a.N : a.N;
   MoeSrc<NT> src;
   src.codes = __builtin_amdgcn_make_buffer_rsrc((void*)codes, (short)0, (int)a.codes_stride, kMoeBufFlags);
   src.codes_none = __builtin_amdgcn_make_buffer_rsrc((void*)codes, (short)0, 0, kMoeBufFlags);
@@ -373,7 +374,7 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
   for (int j = 0; j < NT; ++j) {
     int n = nt * 16 + l16;
     if (n >= a.N) n = a.N - 1;
-    if (EP == SE_SWIGLU && j == 1) n += a.N;
+    if (SWI && j == 1) n += a.N;
     if (n >= wrows) n = wrows - 1;
     src.voff_codes[j] = (uint32_t)(a.lay.codes_off(n) + 16 * g);
     src.voff_norms[j] = (uint32_t)(a.lay.norms_off(n) * 2);
@@ -462,6 +463,56 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
       }
     }
 
+    if constexpr (EP == SE_SWIGLU_XTF) {
+      // The workgroup's 128 columns are one 128-block of h: silu(gate) * up
+      // as fp16 into an LDS tile [32 rows][128] (over the stage buffers; the
+      // barrier above ended their reads), then one 16-lane group per row
+      // transforms its block and writes pair f16 (x_tf[p], x_tf[p + 64]) at
+      // dword p of row (row0 + m), block blockIdx.x. Columns >= N are zero
+      // (the padding up to a whole block).
+      const int n = nt * 16 + l16;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 16 * i + 4 * g + e;
+          const float s = acc[i][0][e], u = acc[i][1][e];
+          const _Float16 hv = n < a.N ? (_Float16)(s / (1.f + __expf(-s)) * u) : (_Float16)0.f;
+          lds_st16(abuf + (uint32_t)r * 256u + (uint32_t)(wave * 16 + l16) * 2u,
+                   __builtin_bit_cast(uint16_t, hv));
+        }
+      }
+      __syncthreads();
+      const int r = tid >> 4, q = tid & 15;  // 32 groups of 16 lanes: one row each
+      float v[8];
+      {
+        const u32x4v w = lds_ld128(abuf + (uint32_t)r * 256u + (uint32_t)q * 16u);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          v[2 * k] = h2f((uint16_t)(w[k] & 0xffff));
+          v[2 * k + 1] = h2f((uint16_t)(w[k] >> 16));
+        }
+      }
+      fwht128_group16(v, q);
+      float o[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) o[k] = lane_xor<8>(v[k]);
+      const int m = mbase + r;
+      if (r < 16 * MT && m < M) {
+        u32x4v w;
+        int p0;
+        if (q < 8) {
+          p0 = 8 * q;
+          w = u32x4v{pack_h2(v[0], o[0]), pack_h2(v[1], o[1]), pack_h2(v[2], o[2]), pack_h2(v[3], o[3])};
+        } else {
+          p0 = 8 * (q - 8) + 4;
+          w = u32x4v{pack_h2(o[4], v[4]), pack_h2(o[5], v[5]), pack_h2(o[6], v[6]), pack_h2(o[7], v[7])};
+        }
+        uint32_t* dst = reinterpret_cast<uint32_t*>(a.y) + (int64_t)(row0 + m) * (a.ldy / 2) +
+                        (int64_t)blockIdx.x * 64 + p0;
+        *reinterpret_cast<u32x4v*>(dst) = w;
+      }
+    } else {
     // epilogue from registers: D element (lane, e) of m-tile i is row
     // 16 i + 4 (lane / 16) + e, column 16 nt + lane % 16
     const int n = nt * 16 + l16;
@@ -485,13 +536,14 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
         }
       }
     }
+    }
     __syncthreads();  // stage buffers free before the next pass
   }
 }
 
 template <bool NIB, int EP>
 static int launch_moe_t(const SmallArgs& a, int groups, hipStream_t st) {
-  constexpr int D = EP == SE_SWIGLU ? 2 : 3;
+  constexpr int D = 2;  // 2 blocks in flight per wave: measured faster than 3 or 4
   auto kern = moe_gemv_kernel<NIB, EP, D>;
   const int entries = table_entries(NIB, a.n_levels);
   const uint32_t abuf = (uint32_t)round_up((size_t)entries * 256, 256);
@@ -516,6 +568,9 @@ int moe_grouped(bool nibble, int epilogue, const SmallArgs& a, int groups, hipSt
   switch (epilogue) {
     case SE_F32: return nibble ? launch_moe_t<true, SE_F32>(a, groups, st) : launch_moe_t<false, SE_F32>(a, groups, st);
     case SE_SWIGLU: return nibble ? launch_moe_t<true, SE_SWIGLU>(a, groups, st) : launch_moe_t<false, SE_SWIGLU>(a, groups, st);
+    case SE_SWIGLU_XTF:
+      if (a.ldy % 128) return PE_ERR_DIMS;  // rows of whole 128-blocks
+      return nibble ? launch_moe_t<true, SE_SWIGLU_XTF>(a, groups, st) : launch_moe_t<false, SE_SWIGLU_XTF>(a, groups, st);
     default: return PE_ERR_DTYPE;
   }
 }

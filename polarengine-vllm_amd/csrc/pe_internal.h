@@ -65,7 +65,10 @@ int gemv1(bool nibble, int xmode, int omode, const Gemv1Args& a, hipStream_t st)
 int gemv1_max_kp(bool nibble);
 
 // small-M epilogues
-enum { SE_F32 = 0, SE_F16 = 1, SE_SWIGLU = 2 };
+// SE_SWIGLU_XTF (grouped experts only): the SwiGLU output of a 128-column
+// block goes straight through the FWHT-128 into pair-f16 rows (the next
+// product's activation operand) instead of fp16 h
+enum { SE_F32 = 0, SE_F16 = 1, SE_SWIGLU = 2, SE_SWIGLU_XTF = 3 };
 
 struct SmallArgs {
   const uint8_t* codes;
@@ -89,7 +92,8 @@ struct SmallArgs {
 // pe_gemm_small.hip: M <= kSmallMaxRows per pass is cheapest (larger M loops)
 constexpr int kSmallMaxRows = 64;
 int gemm_small(bool nibble, int epilogue, const SmallArgs& a, int groups, hipStream_t st);
-// grouped expert products (group_off required; epilogue SE_F32 or SE_SWIGLU)
+// grouped expert products (group_off required; epilogue SE_F32, SE_SWIGLU or
+// SE_SWIGLU_XTF)
 int moe_grouped(bool nibble, int epilogue, const SmallArgs& a, int groups, hipStream_t st);
 
 // pe_gemv_mfma.hip: decode GEMV, 1 <= M <= 16, fp16 out (+ fp16 bias)

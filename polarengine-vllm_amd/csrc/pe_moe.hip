@@ -139,12 +139,6 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
   }
 }
 
-// zero a byte range in 16-byte units (graph-safe replacement for a memset)
-__global__ __launch_bounds__(256) void zero16_kernel(uint4* __restrict__ p, int64_t n16) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < n16) p[i] = make_uint4(0, 0, 0, 0);
-}
-
 // out[t, h] = sum_k w[t, k] * y2[pos(t, k), h], k in order; 8 columns per lane
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ y2,
                                                           const float* __restrict__ topk_w,
@@ -175,7 +169,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
 }
 
 struct MoeWs {
-  size_t offsets, sorted_token, pair_pos, xtf, h, htf, y2, total;
+  size_t offsets, sorted_token, pair_pos, xtf, htf, y2, total;
 };
 
 static MoeWs moe_ws_layout(int64_t T, int top_k, int E, int H, int I) {
@@ -192,7 +186,6 @@ static MoeWs moe_ws_layout(int64_t T, int top_k, int E, int H, int I) {
   w.sorted_token = take((size_t)P * 4);
   w.pair_pos = take((size_t)P * 4);
   w.xtf = take((size_t)T * H * 2);
-  w.h = take((size_t)P * Ip * 2);
   w.htf = take((size_t)P * Ip * 2);
   w.y2 = take((size_t)P * H * 4);
   w.total = o;
@@ -271,22 +264,15 @@ extern "C" int pe_moe_forward(const void* x, int64_t T, int H, int I, int E, int
   if (int rc = launch_status()) return rc;
   // 2. x -> pair f16
   if (int rc = fwht128(x, PE_DTYPE_F16, T, H, H, ws + L.xtf, PE_XTF_PAIR_F16, st)) return rc;
-  // 3. gate/up + SwiGLU -> h [P, Ip] fp16 (padding columns zeroed first)
-  if (Ip != I) {
-    const int64_t n16 = (int64_t)P * Ip * 2 / 16;
-    zero16_kernel<<<dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, st>>>(
-        reinterpret_cast<uint4*>(ws + L.h), n16);
-    if (int rc = launch_status()) return rc;
-  }
+  // 3. gate/up + SwiGLU, each 128-column block of h transformed in the same
+  // kernel -> htf [P, Ip] pair f16 (columns past I are zero)
   {
     SmallArgs a{reinterpret_cast<const uint8_t*>(w13_codes), w13_norms, ct13, n_levels13,
                 reinterpret_cast<const uint32_t*>(ws + L.xtf), sorted_token, offsets,
-                2 * (int64_t)I * row13, 2 * (int64_t)I * nb13, ws + L.h, Ip, nullptr, 0, I,
+                2 * (int64_t)I * row13, 2 * (int64_t)I * nb13, ws + L.htf, Ip, nullptr, 0, I,
                 nb13, wlayout(nib13, tiled13, nb13)};
-    if (int rc = moe_grouped(nib13, SE_SWIGLU, a, E, st)) return rc;
+    if (int rc = moe_grouped(nib13, SE_SWIGLU_XTF, a, E, st)) return rc;
   }
-  // 4. h -> pair f16
-  if (int rc = fwht128(ws + L.h, PE_DTYPE_F16, P, Ip, Ip, ws + L.htf, PE_XTF_PAIR_F16, st)) return rc;
   // 5. down -> y2 [P, H] fp32
   {
     SmallArgs a{reinterpret_cast<const uint8_t*>(w2_codes), w2_norms, ct2, n_levels2,
