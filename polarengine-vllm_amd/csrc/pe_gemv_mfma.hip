@@ -174,8 +174,10 @@ __device__ __forceinline__ void dec_table_write(const DecTable<NIB>& t, int n_le
 // row stride ldx fp16 elements. The workgroup covers TN 16-row tiles with
 // NW = TN * KS waves: wave w works on tile w % TN over the K-slice w / TN
 // (contiguous 128-blocks), streaming it D blocks deep. XC: activation
-// registers per lane.
-template <bool NIB, int TN, int KS, bool XRAW, bool MASK, int XC, int D, bool CTV>
+// registers per lane. SPLIT: the K blocks are divided into gridDim.y groups,
+// blockIdx.y's group only (its activations alone in LDS); y then receives
+// fp32 partial sums [gridDim.y][M][N], added by dec_split_reduce_kernel.
+template <bool NIB, int TN, int KS, bool XRAW, bool MASK, int XC, int D, bool CTV, bool SPLIT>
 __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
     const float* __restrict__ ct, int n_levels, uint32_t code_mask,
@@ -192,8 +194,11 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
   // after the K loop the reduction buffer reuses the start of LDS.
 
   const int jt = wave % TN, ks = wave / TN;
-  const int b_begin = (int)((int64_t)nb * ks / KS);
-  const int b_end = (int)((int64_t)nb * (ks + 1) / KS);
+  // K blocks of this workgroup: [kb0, kb0 + nbr)
+  const int kb0 = SPLIT ? (int)((int64_t)nb * blockIdx.y / gridDim.y) : 0;
+  const int nbr = SPLIT ? (int)((int64_t)nb * (blockIdx.y + 1) / gridDim.y) - kb0 : nb;
+  const int b_begin = kb0 + (int)((int64_t)nbr * ks / KS);
+  const int b_end = kb0 + (int)((int64_t)nbr * (ks + 1) / KS);
   const int nbw = b_end - b_begin;  // blocks of this wave (uniform)
 
   // weight row of this lane (clamped; clamped rows are never stored)
@@ -220,13 +225,18 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
   // Unconditional (clamped) loads, queued on the CU before any weight load
   // (the activations are on the critical path of the prologue; the weight
   // blocks are not needed before the K loop).
-  const int nitems = M * nb;
+  const int nitems = M * nbr;
+  // LDS bytes per activation row: 256 per block plus 16, so that the 16 rows
+  // one ds_read_b128 phase reads (lanes l16 = rows) start in 16 different
+  // bank groups; without the pad every row began in the same bank (row sizes
+  // are multiples of 256 B) and M > 1 reads conflicted 16 ways
+  const uint32_t xrow_b = (uint32_t)nbr * 256u + 16u;
   const int gi = wave * 4 + g;
   int it_m, it_b;
   {
     const int it = gi < nitems ? gi : 0;
-    it_m = it / nb;
-    it_b = it - it_m * nb;
+    it_m = it / nbr;
+    it_b = it - it_m * nbr;
   }
   u32x4v xr[XC];
   {
@@ -235,11 +245,11 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
 #pragma unroll
     for (int i = 0; i < XC; ++i) {
       const bool ok = gi + 4 * NW * i < nitems;
-      const int64_t off = ok ? ((int64_t)m * ldx + (int64_t)b * kBlock) * 2 + l16 * 16 : 0;
+      const int64_t off = ok ? ((int64_t)m * ldx + (int64_t)(kb0 + b) * kBlock) * 2 + l16 * 16 : 0;
       xr[i] = *reinterpret_cast<const u32x4v*>(xb + off);
       b += 4 * NW;
-      while (b >= nb) {
-        b -= nb;
+      while (b >= nbr) {
+        b -= nbr;
         ++m;
       }
     }
@@ -270,7 +280,7 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
 #pragma unroll
     for (int i = 0; i < XC; ++i) {
       if (gi + 4 * NW * i < nitems) {  // uniform inside the group
-        const uint32_t blk = xs_addr + (uint32_t)(m * nb + b) * 256u;
+        const uint32_t blk = xs_addr + (uint32_t)m * xrow_b + (uint32_t)b * 256u;
         if constexpr (XRAW) {
           const int q = l16;
           float v[8];
@@ -301,8 +311,8 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
         }
       }
       b += 4 * NW;
-      while (b >= nb) {
-        b -= nb;
+      while (b >= nbr) {
+        b -= nbr;
         ++m;
       }
     }
@@ -315,7 +325,10 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
   float4v acc = float4v{0.f, 0.f, 0.f, 0.f};
   // A row of this lane: rows past M repeat row M-1; they only feed D rows
   // >= M, which are never stored
-  const uint32_t arow = xs_addr + (uint32_t)((l16 < M ? l16 : M - 1) * nb) * 256u + 64u * g;
+  // (item (m, b) of the group sits at m * xrow_b + (b - kb0) * 256: the base
+  // wraps below zero and comes back with b >= kb0)
+  const uint32_t arow = xs_addr + (uint32_t)(l16 < M ? l16 : M - 1) * xrow_b -
+                        (uint32_t)kb0 * 256u + 64u * g;
   auto do_block = [&](const DecBlk<NIB, 1>& k, int b) {
     u32x4v af[4];
 #pragma unroll
@@ -360,10 +373,31 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
 #pragma unroll
     for (int w = 0; w < KS; ++w)
       s += __builtin_bit_cast(float, lds_ld32((uint32_t)((((w * TN + j) * 64) * 4 + le) * 4)));
-    _Float16 hv = (_Float16)s;
-    if (bias) hv = (_Float16)((float)hv + h2f(bias[n]));
-    reinterpret_cast<_Float16*>(y)[(int64_t)m * ldy + n] = hv;
+    if constexpr (SPLIT) {
+      reinterpret_cast<float*>(y)[((int64_t)blockIdx.y * M + m) * N + n] = s;
+    } else {
+      _Float16 hv = (_Float16)s;
+      if (bias) hv = (_Float16)((float)hv + h2f(bias[n]));
+      reinterpret_cast<_Float16*>(y)[(int64_t)m * ldy + n] = hv;
+    }
   }
+}
+
+// y[m, n] = fp16(sum over the groups g = 0.. in order of part[g][m][n]) (+ bias
+// as the direct epilogue adds it)
+__global__ __launch_bounds__(256) void dec_split_reduce_kernel(const float* __restrict__ part,
+                                                               int G, int M, int N,
+                                                               const uint16_t* __restrict__ bias,
+                                                               _Float16* __restrict__ y,
+                                                               int64_t ldy) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)M * N) return;
+  const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
+  float s = 0.f;
+  for (int g = 0; g < G; ++g) s += part[((int64_t)g * M + m) * N + n];
+  _Float16 hv = (_Float16)s;
+  if (bias) hv = (_Float16)((float)hv + h2f(bias[n]));
+  y[(int64_t)m * ldy + n] = hv;
 }
 
 // ---------------------------------------------------------------------------
@@ -382,20 +416,21 @@ constexpr int dec_ks() { return kDecW / TN; }
 static int dec_xc(int M, int nb, int nw) { return (M * nb + 4 * nw - 1) / (4 * nw); }
 
 static size_t dec_lds(bool nibble, int M, int nb, int n_levels, int nw) {
-  size_t lds = (size_t)table_entries(nibble, n_levels) * 256 + (size_t)M * nb * 256;
+  size_t lds = (size_t)table_entries(nibble, n_levels) * 256 + (size_t)M * (nb * 256 + 16);
   const size_t red = (size_t)nw * 64 * 16;
   return lds < red ? red : lds;
 }
 
-template <bool NIB, int TN, bool XRAW, bool MASK, int XC, bool CTV>
-static int launch_dec(const DecArgs& a, hipStream_t st) {
+template <bool NIB, int TN, bool XRAW, bool MASK, int XC, bool CTV, bool SPLIT = false>
+static int launch_dec(const DecArgs& a, hipStream_t st, int groups = 1) {
   constexpr int KS = dec_ks<TN>(), NW = TN * KS;
   // blocks in flight per wave (nibble 1 KB, int8 2 KB each); deeper rings
   // measured slower (3 -> 8: 7.6 -> 8.8 us on Q4 12288 x 4096)
   constexpr int D = NIB ? 3 : 2;
-  auto kern = gemv_mfma_kernel<NIB, TN, KS, XRAW, MASK, XC, D, CTV>;
-  const size_t lds = dec_lds(NIB, a.M, a.nb, a.n_levels, NW);
-  if (lds > 160 * 1024 || dec_xc(a.M, a.nb, NW) > XC) return PE_ERR_DIMS;
+  auto kern = gemv_mfma_kernel<NIB, TN, KS, XRAW, MASK, XC, D, CTV, SPLIT>;
+  const int nbg = (a.nb + groups - 1) / groups;  // most blocks of one group
+  const size_t lds = dec_lds(NIB, a.M, nbg, a.n_levels, NW);
+  if (lds > 160 * 1024 || dec_xc(a.M, nbg, NW) > XC) return PE_ERR_DIMS;
   static const bool attr_ok = [&] {
     return hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
@@ -415,9 +450,16 @@ static int launch_dec(const DecArgs& a, hipStream_t st) {
       }
     ctv.v[i] = w;
   }
-  kern<<<dim3(tiles), dim3(NW * 64), lds, st>>>(a.codes, a.norms, a.ct, a.n_levels,
-                                               0x01010101u * mb, a.x, a.ldx, a.y, a.ldy, a.bias,
-                                               a.M, a.N, a.nb, xs_addr, a.lay, ctv);
+  kern<<<dim3(tiles, groups), dim3(NW * 64), lds, st>>>(
+      a.codes, a.norms, a.ct, a.n_levels, 0x01010101u * mb, a.x, a.ldx, SPLIT ? a.ws : a.y, a.ldy,
+      a.bias, a.M, a.N, a.nb, xs_addr, a.lay, ctv);
+  if constexpr (SPLIT) {
+    if (int rc = launch_status()) return rc;
+    const int64_t total = (int64_t)a.M * a.N;
+    dec_split_reduce_kernel<<<dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st>>>(
+        reinterpret_cast<const float*>(a.ws), groups, a.M, a.N, a.bias,
+        reinterpret_cast<_Float16*>(a.y), a.ldy);
+  }
   return launch_status();
 }
 
@@ -464,19 +506,66 @@ static int launch_dec_tn(const DecArgs& a, hipStream_t st) {
   }
 }
 
+// K split over workgroups: 12 row tiles per workgroup (one K range per wave),
+// gridDim.y groups sized for about one workgroup per CU. Returns the group
+// count, or 0 when the split does not apply (fewer than 2 groups, or one
+// group's activations still do not fit).
+constexpr int kSplitTN = 12;
+static int dec_split_groups(bool nibble, int M, int N, int nb, int n_levels) {
+  const int wgn = ((N + 15) / 16 + kSplitTN - 1) / kSplitTN;
+  int G = (num_cus() + wgn / 2) / wgn;
+  if (G > nb) G = nb;
+  if (G < 2) return 0;
+  const int nbg = (nb + G - 1) / G;
+  if (dec_xc(M, nbg, kDecW) > 8 || dec_lds(nibble, M, nbg, n_levels, kDecW) > 160 * 1024) return 0;
+  return G;
+}
+
+// the split path where the whole activation set does not fit in LDS (each
+// workgroup then transforms and holds only its K range of the activations;
+// where it fits, one launch without the partial-sum pass measured faster),
+// for M >= 2 (M = 1 takes no workspace: it keeps its own paths)
+static bool dec_use_split(bool nibble, int M, int N, int nb, int n_levels) {
+  const bool whole = dec_xc(M, nb, kDecW) <= 8 && dec_lds(nibble, M, nb, n_levels, kDecW) <= 160 * 1024;
+  return M >= 2 && !whole && dec_split_groups(nibble, M, N, nb, n_levels) > 0;
+}
+
+template <bool NIB, bool XRAW, bool MASK>
+static int launch_dec_split(const DecArgs& a, hipStream_t st) {
+  const int G = dec_split_groups(NIB, a.M, a.N, a.nb, a.n_levels);
+  if (!a.ws || a.ws_bytes < (size_t)G * a.M * a.N * 4) return PE_ERR_WORKSPACE;
+  const int xc = dec_xc(a.M, (a.nb + G - 1) / G, kDecW);
+  if (a.ct_host) {
+    if (xc <= 2) return launch_dec<NIB, kSplitTN, XRAW, MASK, 2, true, true>(a, st, G);
+    if (xc <= 4) return launch_dec<NIB, kSplitTN, XRAW, MASK, 4, true, true>(a, st, G);
+    return launch_dec<NIB, kSplitTN, XRAW, MASK, 8, true, true>(a, st, G);
+  }
+  if (xc <= 2) return launch_dec<NIB, kSplitTN, XRAW, MASK, 2, false, true>(a, st, G);
+  if (xc <= 4) return launch_dec<NIB, kSplitTN, XRAW, MASK, 4, false, true>(a, st, G);
+  return launch_dec<NIB, kSplitTN, XRAW, MASK, 8, false, true>(a, st, G);
+}
+
 template <bool NIB, bool XRAW>
 static int launch_dec_m(const DecArgs& a, hipStream_t st) {
   const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
+  if (dec_use_split(NIB, a.M, a.N, a.nb, a.n_levels))
+    return mask ? launch_dec_split<NIB, XRAW, true>(a, st) : launch_dec_split<NIB, XRAW, false>(a, st);
   return mask ? launch_dec_tn<NIB, XRAW, true>(a, st) : launch_dec_tn<NIB, XRAW, false>(a, st);
 }
 
+size_t gemv_mfma_workspace(bool nibble, int M, int N, int nb, int n_levels) {
+  if (M < 1 || M > 16 || !dec_use_split(nibble, M, N, nb, n_levels)) return 0;
+  return (size_t)dec_split_groups(nibble, M, N, nb, n_levels) * M * N * 4;
+}
+
 bool gemv_mfma_fits(bool nibble, int M, int N, int nb, int n_levels) {
-  // the workgroup's 4 * kDecW lane groups hold the activations in <= 8 registers
-  if (M < 1 || M > 16 || dec_xc(M, nb, kDecW) > 8) return false;
+  if (M < 1 || M > 16) return false;
   // buffer resources address codes and norms with 31-bit offsets (tiled
   // layouts round N up to 16 rows)
   if ((int64_t)(N + 15) * nb * (nibble ? 64 : kBlock) >= (int64_t)1 << 31) return false;
-  return dec_lds(nibble, M, nb, n_levels, kDecW) <= 160 * 1024;
+  if (dec_use_split(nibble, M, N, nb, n_levels)) return true;
+  // the workgroup's 4 * kDecW lane groups hold the activations in <= 8 registers
+  return dec_xc(M, nb, kDecW) <= 8 && dec_lds(nibble, M, nb, n_levels, kDecW) <= 160 * 1024;
 }
 
 int gemv_mfma(bool nibble, bool xraw, const DecArgs& a, hipStream_t st) {

@@ -110,8 +110,11 @@ struct DecArgs {
   int M, N, nb;
   WLayout lay;
   const float* ct_host;  // nullable host copy of ct (n_levels floats): codebook by value
+  void* ws;              // fp32 partial sums of the K-split path (gemv_mfma_workspace bytes)
+  size_t ws_bytes;
 };
 bool gemv_mfma_fits(bool nibble, int M, int N, int nb, int n_levels);
+size_t gemv_mfma_workspace(bool nibble, int M, int N, int nb, int n_levels);
 int gemv_mfma(bool nibble, bool xraw, const DecArgs& a, hipStream_t st);
 
 // pe_gemm.hip

@@ -3,9 +3,11 @@
 // (polar_matmul, kernels/polar_gemm.py:425-534).
 //
 // Routing by M (rows of the activation):
-//   M <= 16 (when x fits in LDS beside the codebook table)
+//   M <= 16 (when x, or for M >= 8 one K group of it, fits in LDS beside the
+//   codebook table)
 //                     -> gemv_mfma: decode GEMV on 16x16x32 MFMA, FWHT fused
-//                        into its prologue (one launch per linear);
+//                        into its prologue (one launch per linear; with the K
+//                        split over workgroups, plus a partial-sum reduction);
 //   M == 1 otherwise  -> gemv1 (register-resident dot2 GEMV, LDS activations);
 //   2 <= M <= 64      -> FWHT-128 to pair-f16 x_tf, then the small-M MFMA
 //                        kernel (16x16x32 f16, K split across waves);
@@ -34,19 +36,30 @@ static int check_format(int bits, int packed, int n_levels, bool* nibble, bool* 
 
 using namespace pe;
 
+// fp32 partial sums of the K-split decode path (M <= 16), 0 otherwise
+static size_t decode_workspace(int64_t M, int kp, int out_f, int bits, int packed) {
+  if (M < 1 || M > 16 || bits < 2 || bits > 8) return 0;
+  const bool nib = (packed & PE_PACK_NIBBLE) != 0 && bits <= 4;
+  return round_up(gemv_mfma_workspace(nib, (int)M, out_f, kp / kBlock, 1 << bits), 256);
+}
+
 extern "C" size_t pe_linear_xtf_workspace_size(int64_t M, int in_f_padded, int out_f, int bits,
                                                int packed) {
   if (M <= 1 || in_f_padded <= 0 || out_f <= 0) return 0;
-  return mm_xtf_workspace((packed & PE_PACK_NIBBLE) != 0 && bits <= 4, M, out_f,
-                          in_f_padded / kBlock);
+  const size_t mm = mm_xtf_workspace((packed & PE_PACK_NIBBLE) != 0 && bits <= 4, M, out_f,
+                                     in_f_padded / kBlock);
+  const size_t dec = decode_workspace(M, in_f_padded, out_f, bits, packed);
+  return mm > dec ? mm : dec;
 }
 
 extern "C" size_t pe_linear_workspace_size(int64_t M, int in_f, int out_f, int bits, int packed) {
   if (M <= 1 || in_f <= 0 || out_f <= 0) return 0;
   const int kp = (in_f + kBlock - 1) / kBlock * kBlock;
-  // pair-f16 x_tf, then whatever the matmul needs
-  return round_up((size_t)M * kp * 2, 256) +
-         pe_linear_xtf_workspace_size(M, kp, out_f, bits, packed);
+  // pair-f16 x_tf, then whatever the matmul needs; or the decode path's partials
+  const size_t mm = round_up((size_t)M * kp * 2, 256) +
+                    pe_linear_xtf_workspace_size(M, kp, out_f, bits, packed);
+  const size_t dec = decode_workspace(M, kp, out_f, bits, packed);
+  return mm > dec ? mm : dec;
 }
 
 extern "C" int pe_linear_forward_xtf(const void* x_tf_pair, int64_t M, int in_f_padded,
@@ -65,9 +78,10 @@ extern "C" int pe_linear_forward_xtf(const void* x_tf_pair, int64_t M, int in_f_
   if (M == 0) return PE_OK;
   const int nb = in_f_padded / kBlock;
   if (M <= 16 && gemv_mfma_fits(nib, (int)M, out_f, nb, n_levels)) {
+    if (workspace && !aligned16(workspace)) return PE_ERR_ALIGN;
     DecArgs a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels,
               x_tf_pair, (int64_t)in_f_padded, y, out_f, reinterpret_cast<const uint16_t*>(bias),
-              (int)M, out_f, nb, wlayout(nib, tiled, nb), ct_host};
+              (int)M, out_f, nb, wlayout(nib, tiled, nb), ct_host, workspace, workspace_bytes};
     return gemv_mfma(nib, false, a, st);
   }
   return mm_xtf(nib, tiled, codes, norms_f16, ct_scaled, n_levels, x_tf_pair, M, out_f, nb, y,
@@ -94,9 +108,10 @@ extern "C" int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f
   if (M == 0) return PE_OK;
   const int nb = in_f / kBlock;
   if (M <= 16 && gemv_mfma_fits(nib, (int)M, out_f, nb, n_levels)) {
+    if (workspace && !aligned16(workspace)) return PE_ERR_ALIGN;
     DecArgs a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels, x, ldx, y,
               out_f, reinterpret_cast<const uint16_t*>(bias), (int)M, out_f, nb,
-              wlayout(nib, tiled, nb), ct_host};
+              wlayout(nib, tiled, nb), ct_host, workspace, workspace_bytes};
     return gemv_mfma(nib, true, a, st);
   }
   if (M == 1 && !tiled && in_f <= gemv1_max_kp(nib)) {

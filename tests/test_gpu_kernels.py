@@ -218,7 +218,11 @@ DECODE_CASES = [(1, 12288, 4096, 4), (1, 4096, 4096, 5), (2, 1000, 1408, 3),
                 (3, 4096, 12288, 4), (4, 257, 384, 2), (5, 96, 640, 8), (7, 2816, 2048, 6),
                 (8, 12288, 4096, 4), (12, 333, 1024, 7), (16, 4096, 2048, 4),
                 (16, 1536, 1536, 5), (16, 4096, 4096, 4), (1, 512, 20480, 4),
-                (1, 64, 128, 3), (2, 48, 256, 8)]
+                (1, 64, 128, 3), (2, 48, 256, 8),
+                # K split over workgroups (M >= 8, or activations too large for
+                # LDS): fp32 partials reduced by a second kernel
+                (16, 12288, 4096, 4), (16, 4096, 12288, 3), (6, 2048, 24576, 4),
+                (2, 700, 40960, 2), (10, 50, 640, 6)]
 
 
 @pytest.mark.parametrize("m,n,k,bits", DECODE_CASES)
