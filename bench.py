@@ -9,9 +9,10 @@ rotate over 16 independent copies (416 MB > the 256 MB Infinity Cache) so
 reads come from HBM; calls are captured in a HIP graph and replayed so the
 host does not gate the ~4 us kernels. Also measured: the same call with one
 weight copy (cache-hot), the M=2048 prefill GEMM (TFLOP/s vs dense fp16 MFMA
-peak), M=4/16 decode, KV-cache quantize / dequantize, the grouped MoE experts,
-and the oracle's CPU time for the headline call (cpu_baseline, numpy, 1
-thread) on a bounded sample.
+peak), M=4/8/16 decode, the gate/up Q3 12288x4096 and down Q4 4096x12288 decode
+shapes at M=1 and 16, the Q3 4096x12288 prefill, KV-cache quantize / dequantize,
+the grouped MoE experts, and the oracle's CPU time for the headline call
+(cpu_baseline, numpy, 1 thread) on a bounded sample.
 """
 
 from __future__ import annotations
@@ -313,12 +314,21 @@ def main():
     t_hot, _ = time_graph(layers[:1], 128, args.warmup, args.steps, dev)
 
     extra = {}
-    for mm in (4, 16):
+    for mm in (4, 8, 16):
         lay = [Linear(n, k, bits, mm, dev, seed=200 + i) for i in range(N_COPIES)]
         t, _ = time_graph(lay, 4, 64, 512, dev)
         extra[f"decode_m{mm}"] = {"us_per_call": round(t * 1e6, 2),
                                   "GB/s": round(algo_bytes(mm, n, k, bits) / t / 1e9, 1)}
         del lay
+    # the MLP's other shapes: gate/up Q3 12288x4096 and down Q4 4096x12288
+    for name, (nn, kk, bb) in (("gateup_q3", (12288, 4096, 3)), ("down_q4", (4096, 12288, 4))):
+        for mm in (1, 16):
+            lay = [Linear(nn, kk, bb, mm, dev, seed=400 + i) for i in range(N_COPIES)]
+            t, _ = time_graph(lay, 4, 64, 512, dev)
+            gb = algo_bytes(mm, nn, kk, bb) / t / 1e9
+            extra[f"decode_{name}_m{mm}"] = {"us_per_call": round(t * 1e6, 2), "GB/s": round(gb, 1),
+                                             "hbm_frac": round(gb / HBM_PEAK_GBS, 4)}
+            del lay
     pf = Linear(n, k, bits, 2048, dev, seed=300)
     t_pf = time_eager(pf, 3, 20, dev)
     flops = 2.0 * 2048 * n * k
@@ -326,6 +336,12 @@ def main():
                               "TFLOP/s": round(flops / t_pf / 1e12, 1),
                               "mfma_frac": round(flops / t_pf / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
                               "includes": "FWHT-128 of x (pair f16) + MFMA GEMM"}
+    del pf
+    pf = Linear(4096, 12288, 3, 2048, dev, seed=301)
+    t_pf = time_eager(pf, 3, 20, dev)
+    extra["prefill_down_q3_m2048"] = {"us_per_call": round(t_pf * 1e6, 1),
+                                      "TFLOP/s": round(flops / t_pf / 1e12, 1),
+                                      "mfma_frac": round(flops / t_pf / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
     del pf
     extra["cache_hot_m1"] = {"us_per_call": round(t_hot * 1e6, 2),
                              "GB/s": round(B / t_hot / 1e9, 1),

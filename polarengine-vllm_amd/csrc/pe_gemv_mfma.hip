@@ -507,13 +507,15 @@ static int launch_dec_tn(const DecArgs& a, hipStream_t st) {
 }
 
 // K split over workgroups: 12 row tiles per workgroup (one K range per wave),
-// gridDim.y groups sized for about one workgroup per CU. Returns the group
+// gridDim.y groups sized for at most one workgroup per CU. Returns the group
 // count, or 0 when the split does not apply (fewer than 2 groups, or one
 // group's activations still do not fit).
 constexpr int kSplitTN = 12;
 static int dec_split_groups(bool nibble, int M, int N, int nb, int n_levels) {
   const int wgn = ((N + 15) / 16 + kSplitTN - 1) / kSplitTN;
-  int G = (num_cus() + wgn / 2) / wgn;
+  // at most one round of workgroups (one per CU: the LDS holds one): a 257th
+  // workgroup would run as a second round of its own
+  int G = num_cus() / wgn;
   if (G > nb) G = nb;
   if (G < 2) return 0;
   const int nbg = (nb + G - 1) / G;
