@@ -296,9 +296,13 @@ struct Frag4 {
 };
 
 // A tiles of the four-wave kernel: 128-byte rows (32 pairs), 16-byte chunk c
-// of row r stored at chunk c ^ (r & 7), so the eight rows one ds_read_b128
-// phase touches cover all banks without padding.
+// of row r stored at chunk c ^ ((r >> 1) & 7). A ds_read_b128 phase serves 16
+// lanes (rows r0..r0+15, one chunk each) from the 64 four-byte banks: a row
+// spans half the banks (even rows the low half, odd rows the high half), so
+// the eight rows of each parity need eight distinct chunks. The plain
+// c ^ (r & 7) repeats after eight rows and made every A read a 2-way conflict.
 constexpr int kARow4 = 128;
+__device__ __forceinline__ uint32_t a4_swz(int r) { return (uint32_t)((r >> 1) & 7); }
 
 template <bool NIB, int TMW, bool MASK>
 __device__ __forceinline__ void issue_frag4(Frag4<NIB, TMW>& f, uint32_t aaddr, int t,
@@ -459,7 +463,7 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
     int m = m0 + r;
     if (m >= M) m = M - 1;  // clamped rows feed discarded outputs only
     a_src[i] = xp + (int64_t)m * xrow_u32 + c * 4;
-    a_dst[i] = (uint32_t)(r * kARow4 + ((c ^ (r & 7)) << 4));
+    a_dst[i] = (uint32_t)(r * kARow4 + (((uint32_t)c ^ a4_swz(r)) << 4));
   }
   const uint8_t* b_row[2];
   const uint16_t* n_row[2];
@@ -472,7 +476,7 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
   }
   uint32_t a_off[4];  // lane's row l32, chunk 4h + t, swizzled
 #pragma unroll
-  for (int t = 0; t < 4; ++t) a_off[t] = (uint32_t)(l32 * kARow4 + (((4 * h + t) ^ (l32 & 7)) << 4));
+  for (int t = 0; t < 4; ++t) a_off[t] = (uint32_t)(l32 * kARow4 + (((uint32_t)(4 * h + t) ^ a4_swz(l32)) << 4));
 
   const int nkt = 2 * nb;  // half-blocks, a multiple of 4
   // loads past the last half-block re-read it (in bounds, never used)
