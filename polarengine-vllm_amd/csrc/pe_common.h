@@ -189,6 +189,28 @@ __device__ __forceinline__ void fwht128_group16(float v[8], int q) {
   for (int i = 0; i < 8; ++i) v[i] *= kInvSqrt128;
 }
 
+// Pair-f16 store of one 128-block held by a 16-lane group (lane q holds
+// elements 8q..8q+7): dword p of the block's 64 dwords at `blk` is
+// (x[p], x[p + 64]). Lanes q < 8 write dwords 8q..8q+3, lanes q >= 8 dwords
+// 8(q-8)+4..8(q-8)+7, each as one 16-byte store. Every lane of the group must
+// take part (cross-lane exchange); only `live` lanes store.
+__device__ __forceinline__ void store_pair_block(const float v[8], int q, uint32_t* blk, bool live) {
+  float o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = lane_xor<8>(v[i]);
+  if (!live) return;
+  u32x4v w;
+  int p0;
+  if (q < 8) {
+    p0 = 8 * q;
+    w = u32x4v{pack_h2(v[0], o[0]), pack_h2(v[1], o[1]), pack_h2(v[2], o[2]), pack_h2(v[3], o[3])};
+  } else {
+    p0 = 8 * (q - 8) + 4;
+    w = u32x4v{pack_h2(o[4], v[4]), pack_h2(o[5], v[5]), pack_h2(o[6], v[6]), pack_h2(o[7], v[7])};
+  }
+  *reinterpret_cast<u32x4v*>(blk + p0) = w;
+}
+
 // ---------------------------------------------------------------------------
 // Per-lane replicated codebook table in LDS: dword e*64 + lane holds entry e.
 //   TBL_NIB_H2: entry e = half2(ct[e & 15], ct[e >> 4]) (nibble byte e)

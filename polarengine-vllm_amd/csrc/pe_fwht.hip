@@ -29,23 +29,7 @@ __global__ __launch_bounds__(256) void fwht128_kernel(const void* x, void* y, in
   if constexpr (XFORM) fwht128_group16(v, q);
 
   if constexpr (YL == PE_XTF_PAIR_F16) {
-    float o[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = lane_xor<8>(v[i]);
-    if (!live) return;
-    uint4 w;
-    int p0;
-    if (q < 8) {
-      p0 = 8 * q;
-      w.x = pack_h2(v[0], o[0]); w.y = pack_h2(v[1], o[1]);
-      w.z = pack_h2(v[2], o[2]); w.w = pack_h2(v[3], o[3]);
-    } else {
-      p0 = 8 * (q - 8) + 4;
-      w.x = pack_h2(o[4], v[4]); w.y = pack_h2(o[5], v[5]);
-      w.z = pack_h2(o[6], v[6]); w.w = pack_h2(o[7], v[7]);
-    }
-    uint32_t* dst = reinterpret_cast<uint32_t*>(y) + (bid * 64 + p0);
-    *reinterpret_cast<uint4*>(dst) = w;
+    store_pair_block(v, q, reinterpret_cast<uint32_t*>(y) + bid * 64, live);
   } else if constexpr (YL == PE_XTF_F32) {
     if (!live) return;
     float* dst = reinterpret_cast<float*>(y) + (r * (int64_t)nbc * kBlock + (int64_t)cb * kBlock + q * 8);

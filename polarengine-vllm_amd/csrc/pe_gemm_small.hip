@@ -298,7 +298,8 @@ static int launch_small_ep(const SmallArgs& a, int groups, hipStream_t st) {
 // registers. The expert's activation rows (up to 32 per pass) are staged one
 // 128-block at a time into a two-stage LDS ring shared by the 8 waves (chunk c
 // of row r at chunk c ^ (r & 15): the 16 rows one ds_read_b128 phase touches
-// hit distinct banks); the codes stream through a D-deep register ring.
+// hit distinct banks), each block loaded D blocks before it is staged; the
+// codes stream through a D-deep register ring.
 // ---------------------------------------------------------------------------
 constexpr int kMoeWaves = 8;
 constexpr int kMoeThreads = 64 * kMoeWaves;
@@ -416,9 +417,14 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
       moe_load_w<NIB, NT>(ring[d], src, d, a.nb, a.lay);
       __builtin_amdgcn_sched_barrier(0);
     }
-    u32x4v sreg = lda(0);
-    if (sr < kMoeRows) lds_st128(abuf + sdst, sreg);
-    if (a.nb > 1) sreg = lda(1);
+    // activation FIFO: block k is loaded D blocks before it is staged and
+    // waits in sreg[k % D]
+    u32x4v sreg[D];
+    sreg[0] = lda(0);
+    if (sr < kMoeRows) lds_st128(abuf + sdst, sreg[0]);
+#pragma unroll
+    for (int k = 1; k <= D; ++k)
+      if (k < a.nb) sreg[k % D] = lda(k);
     __syncthreads();  // codebook table and stage 0 written
 
     // A row of this lane in m-tile i: activation row 16 i + l16 of the stage
@@ -428,35 +434,45 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
         const int b = b0 + d;
         if (b < a.nb) {  // uniform
           const uint32_t st = abuf + (uint32_t)(b & 1) * kStage;
+          // each activation fragment is read from LDS once and feeds the
+          // gate and up tiles alike
+          float4v blk[NT][2];
 #pragma unroll
-          for (int j = 0; j < NT; ++j) {
-            float4v blk[2] = {float4v{0.f, 0.f, 0.f, 0.f}, float4v{0.f, 0.f, 0.f, 0.f}};
+          for (int j = 0; j < NT; ++j)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
+            for (int i = 0; i < 2; ++i) blk[j][i] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            u32x4v af[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+              const int r = 16 * i + l16;
+              if (i < MT) af[i] = lds_ld128(st + (uint32_t)r * 256u + ((uint32_t)((4 * g + t) ^ (r & 15)) << 4));
+            }
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
               const uint32_t wl = ring[d].lo[j][t] & code_mask;
               const uint32_t wh = NIB ? 0u : (ring[d].hi[j][t] & code_mask);
               const half8v bf = dequant_slab_raw<NIB>(nullptr, wl, wh, lane4);
 #pragma unroll
-              for (int i = 0; i < 2; ++i) {
-                if (i < MT) {
-                  const int r = 16 * i + l16;
-                  const u32x4v af = lds_ld128(st + (uint32_t)r * 256u +
-                                              ((uint32_t)((4 * g + t) ^ (r & 15)) << 4));
-                  blk[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, af),
-                                                                  bf, blk[i], 0, 0, 0);
-                }
-              }
+              for (int i = 0; i < 2; ++i)
+                if (i < MT)
+                  blk[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, af[i]), bf,
+                                                                     blk[j][i], 0, 0, 0);
             }
+          }
+#pragma unroll
+          for (int j = 0; j < NT; ++j) {
             const float nrm = h2f((uint16_t)ring[d].nbits[j]);
 #pragma unroll
-            for (int i = 0; i < 2; ++i) acc[i][j] += blk[i] * nrm;
+            for (int i = 0; i < 2; ++i) acc[i][j] += blk[j][i] * nrm;
           }
           moe_load_w<NIB, NT>(ring[d], src, b + D, a.nb, a.lay);
           // next stage: block b + 1 into the other buffer (its readers, block
-          // b - 1, finished before the previous barrier); prefetch b + 2
+          // b - 1, finished before the previous barrier); load block b + 1 + D
           if (b + 1 < a.nb) {
-            if (sr < kMoeRows) lds_st128(abuf + (uint32_t)((b + 1) & 1) * kStage + sdst, sreg);
-            if (b + 2 < a.nb) sreg = lda(b + 2);
+            if (sr < kMoeRows) lds_st128(abuf + (uint32_t)((b + 1) & 1) * kStage + sdst, sreg[(d + 1) % D]);
+            if (b + 1 + D < a.nb) sreg[(d + 1) % D] = lda(b + 1 + D);
           }
           __syncthreads();
         }
@@ -494,24 +510,10 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
         }
       }
       fwht128_group16(v, q);
-      float o[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) o[k] = lane_xor<8>(v[k]);
       const int m = mbase + r;
-      if (r < 16 * MT && m < M) {
-        u32x4v w;
-        int p0;
-        if (q < 8) {
-          p0 = 8 * q;
-          w = u32x4v{pack_h2(v[0], o[0]), pack_h2(v[1], o[1]), pack_h2(v[2], o[2]), pack_h2(v[3], o[3])};
-        } else {
-          p0 = 8 * (q - 8) + 4;
-          w = u32x4v{pack_h2(o[4], v[4]), pack_h2(o[5], v[5]), pack_h2(o[6], v[6]), pack_h2(o[7], v[7])};
-        }
-        uint32_t* dst = reinterpret_cast<uint32_t*>(a.y) + (int64_t)(row0 + m) * (a.ldy / 2) +
-                        (int64_t)blockIdx.x * 64 + p0;
-        *reinterpret_cast<u32x4v*>(dst) = w;
-      }
+      const bool live = r < 16 * MT && m < M;
+      const int64_t prow = live ? (int64_t)(row0 + m) : 0;  // no address past the rows
+      store_pair_block(v, q, reinterpret_cast<uint32_t*>(a.y) + prow * (a.ldy / 2) + (int64_t)blockIdx.x * 64, live);
     } else {
     // epilogue from registers: D element (lane, e) of m-tile i is row
     // 16 i + 4 (lane / 16) + e, column 16 nt + lane % 16

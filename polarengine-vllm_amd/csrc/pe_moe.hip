@@ -8,16 +8,15 @@
 // h = silu(gate) * up, y = h W2^T, out = sum_k w_k y_k.
 //
 // Launch sequence of pe_moe_forward (no host synchronisation):
-//   1. moe_align: bucket the T*top_k (token, slot) pairs by expert (one
-//      workgroup; LDS histogram + scan + scatter) -> per-expert offsets,
+//   1. moe_prep: FWHT-128 of x into pair f16 (shared by every expert) and, in
+//      the grid's last workgroup, the bucketing of the T*top_k (token, slot)
+//      pairs by expert (LDS histogram + scan + scatter) -> per-expert offsets,
 //      token of each sorted pair, sorted position of each pair;
-//   2. FWHT-128 of x into pair-f16 (shared by every expert);
-//   3. grouped small-M MFMA over (n-tile, expert): gate and up tiles of W13
-//      with the SwiGLU epilogue -> h [pairs, I] fp16 (A rows gathered by
-//      token id);
-//   4. FWHT-128 of h (zero-padded to a multiple of 128) into pair-f16;
-//   5. grouped small-M MFMA with W2 -> y2 [pairs, H] fp32;
-//   6. combine: out[t] = sum_k w[t, k] * y2[pos(t, k)] in fixed k order, fp16.
+//   2. grouped experts, W13: gate and up tiles with SwiGLU; each 128-column
+//      block of h goes through the FWHT in the same kernel -> pair-f16 h
+//      [pairs, Ip] (A rows gathered by token id; columns past I are zero);
+//   3. grouped experts, W2 -> y2 [pairs, H] fp32;
+//   4. combine: out[t] = sum_k w[t, k] * y2[pos(t, k)] in fixed k order, fp16.
 // Each output row depends only on its own inputs, so bucket order inside an
 // expert (set by LDS atomics) does not change any result bit.
 
@@ -26,23 +25,38 @@
 namespace pe {
 
 // ---------------------------------------------------------------------------
-// routing: one wave per token, up to 256 experts (4 per lane)
+// routing: one wave per token, up to 256 experts (expert e = lane + 64 i).
+// Each expert gets a 64-bit key: the score's bits mapped to an unsigned order
+// above, the inverted expert id below, so a larger key is a higher score and
+// equal scores rank the lower id first. The keys go to LDS; each lane counts
+// the keys above its own (its rank), and ranks 0..top_k-1 are the selection
+// in descending order, the order of the reference's repeated arg-max / topk.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ logits, int64_t T,
-                                                        int E, int top_k, int renormalize,
-                                                        int scoring, const float* __restrict__ bias,
-                                                        float* __restrict__ topk_w,
-                                                        int32_t* __restrict__ topk_ids) {
-  const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;  // whole wave
+constexpr int kRouteWaves = 4;
+
+__device__ __forceinline__ uint64_t route_key(float s, int e) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, s + 0.f);  // -0 -> +0
+  const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((uint64_t)ord << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
+}
+
+__global__ __launch_bounds__(64 * kRouteWaves) void moe_route_kernel(
+    const float* __restrict__ logits, int64_t T, int E, int top_k, int renormalize, int scoring,
+    const float* __restrict__ bias, float* __restrict__ topk_w, int32_t* __restrict__ topk_ids) {
+  __shared__ uint64_t keys[kRouteWaves][256];
+  __shared__ float sel_w[kRouteWaves][16];
+  __shared__ int sel_e[kRouteWaves][16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t t = (int64_t)blockIdx.x * kRouteWaves + wave;
+  const bool live = t < T;
+  const int64_t tr = live ? t : T - 1;  // idle waves recompute a live row: barriers are per workgroup
   float v[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = lane + 64 * i;
     float l = -INFINITY;
     if (e < E) {
-      l = logits[t * E + e];
+      l = logits[tr * E + e];
       if (bias) l += bias[e];
     }
     v[i] = l;
@@ -62,56 +76,63 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
     for (int i = 0; i < 4; ++i) v[i] = v[i] / sum;
   } else {  // sigmoid
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = (lane + 64 * i) < E ? 1.f / (1.f + expf(-v[i])) : -1.f;
+    for (int i = 0; i < 4; ++i) v[i] = (lane + 64 * i) < E ? 1.f / (1.f + expf(-v[i])) : 0.f;
   }
-  // top-k by repeated arg-max; ties go to the lower expert id
-  float wsum = 0.f;
-  float sel_w[16];
-  int sel_e[16];
-  for (int k = 0; k < top_k; ++k) {
-    float best = -2.f;
-    int be = 0x7fffffff;
+  const int Ep = (E + 1) & ~1;  // keys read in pairs; a padding key is 0, below every real key
+  uint64_t mine[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + 64 * i;
+    if (v[i] != v[i]) v[i] = -1.f;  // NaN scores rank last
+    mine[i] = e < E ? route_key(v[i], e) : 0;
+    if (e < Ep) keys[wave][e] = mine[i];
+  }
+  __syncthreads();
+  int rank[4] = {0, 0, 0, 0};
+  for (int j = 0; j < Ep; j += 2) {
+    const uint64_t k0 = keys[wave][j], k1 = keys[wave][j + 1];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int e = lane + 64 * i;
-      if (e < E && (v[i] > best || (v[i] == best && e < be))) { best = v[i]; be = e; }
+      if (64 * i < E) {  // uniform
+        rank[i] += k0 > mine[i] ? 1 : 0;
+        rank[i] += k1 > mine[i] ? 1 : 0;
+      }
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ob = __shfl_xor(best, off, 64);
-      const int oe = __shfl_xor(be, off, 64);
-      if (ob > best || (ob == best && oe < be)) { best = ob; be = oe; }
-    }
-    sel_w[k] = best;
-    sel_e[k] = be;
-    wsum += best;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (lane + 64 * i == be) v[i] = -3.f;  // remove from the candidates
   }
-  if (lane == 0) {
-    for (int k = 0; k < top_k; ++k) {
-      topk_w[t * top_k + k] = renormalize ? sel_w[k] / wsum : sel_w[k];
-      topk_ids[t * top_k + k] = sel_e[k];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + 64 * i;
+    if (e < E && rank[i] < top_k) {
+      sel_w[wave][rank[i]] = v[i];
+      sel_e[wave][rank[i]] = e;
     }
+  }
+  __syncthreads();
+  if (live && lane < top_k) {
+    float wsum = 0.f;
+    for (int k = 0; k < top_k; ++k) wsum += sel_w[wave][k];  // selection order
+    const float w = sel_w[wave][lane];
+    topk_w[t * top_k + lane] = renormalize ? w / wsum : w;
+    topk_ids[t * top_k + lane] = sel_e[wave][lane];
   }
 }
 
 // ---------------------------------------------------------------------------
-// bucket pairs by expert (single workgroup)
+// moe_prep: workgroups 0..fwht_wgs-1 transform x (one 128-block per 16-lane
+// group) into pair f16; workgroup fwht_wgs buckets the pairs by expert.
 // ---------------------------------------------------------------------------
-constexpr int kAlignThreads = 1024;
+constexpr int kPrepThreads = 256;
 
-__global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
-    const int32_t* __restrict__ topk_ids, int64_t P, int top_k, int E,
-    int32_t* __restrict__ offsets /* [E+1] */, int32_t* __restrict__ sorted_token /* [P] */,
-    int32_t* __restrict__ pair_pos /* [P] */) {
+__device__ void moe_align_block(const int32_t* __restrict__ topk_ids, int64_t P, int top_k, int E,
+                                int32_t* __restrict__ offsets /* [E+1] */,
+                                int32_t* __restrict__ sorted_token /* [P] */,
+                                int32_t* __restrict__ pair_pos /* [P] */) {
   __shared__ int cnt[256];
   __shared__ int base[257];
   const int tid = threadIdx.x;
-  for (int e = tid; e < E; e += kAlignThreads) cnt[e] = 0;
+  for (int e = tid; e < E; e += kPrepThreads) cnt[e] = 0;
   __syncthreads();
-  for (int64_t p = tid; p < P; p += kAlignThreads) {
+  for (int64_t p = tid; p < P; p += kPrepThreads) {
     const int e = topk_ids[p];
     if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
   }
@@ -125,10 +146,10 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
     base[E] = acc;
   }
   __syncthreads();
-  for (int e = tid; e <= E; e += kAlignThreads) offsets[e] = base[e];
-  for (int e = tid; e < E; e += kAlignThreads) cnt[e] = 0;
+  for (int e = tid; e <= E; e += kPrepThreads) offsets[e] = base[e];
+  for (int e = tid; e < E; e += kPrepThreads) cnt[e] = 0;
   __syncthreads();
-  for (int64_t p = tid; p < P; p += kAlignThreads) {
+  for (int64_t p = tid; p < P; p += kPrepThreads) {
     const int e = topk_ids[p];
     int pos = -1;
     if (e >= 0 && e < E) {
@@ -139,33 +160,65 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
   }
 }
 
-// out[t, h] = sum_k w[t, k] * y2[pos(t, k), h], k in order; 8 columns per lane
+__global__ __launch_bounds__(kPrepThreads) void moe_prep_kernel(
+    const uint16_t* __restrict__ x, int64_t T, int nbc, uint32_t* __restrict__ xtf, int fwht_wgs,
+    const int32_t* __restrict__ topk_ids, int64_t P, int top_k, int E, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ sorted_token, int32_t* __restrict__ pair_pos) {
+  if ((int)blockIdx.x == fwht_wgs) {  // whole workgroup
+    moe_align_block(topk_ids, P, top_k, E, offsets, sorted_token, pair_pos);
+    return;
+  }
+  const int64_t total = T * (int64_t)nbc;
+  int64_t bid = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int q = threadIdx.x & 15;
+  const bool live = bid < total;
+  if (!live) bid = total - 1;  // the group stays converged; its store is masked
+  const int64_t r = bid / nbc;
+  const int cb = (int)(bid - r * nbc);
+  float v[8];
+  load8<PE_DTYPE_F16>(x + (r * nbc + cb) * kBlock + q * 8, v);
+  fwht128_group16(v, q);
+  store_pair_block(v, q, xtf + bid * 64, live);
+}
+
+// out[t, c..c+3] = sum_k w[t, k] * y2[pos(t, k), c..c+3], k in order; 4
+// columns per lane, the loads of four slots issued before their sums
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ y2,
                                                           const float* __restrict__ topk_w,
                                                           const int32_t* __restrict__ pair_pos,
                                                           int64_t T, int top_k, int H,
                                                           uint16_t* __restrict__ out) {
-  const int per_row = H / 8;
+  const int per_row = H / 4;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= T * per_row) return;
   const int64_t t = i / per_row;
-  const int c = (int)(i - t * per_row) * 8;
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int k = 0; k < top_k; ++k) {
-    const int pos = pair_pos[t * top_k + k];
-    if (pos < 0) continue;
-    const float w = topk_w[t * top_k + k];
-    const float4* src = reinterpret_cast<const float4*>(y2 + (int64_t)pos * H + c);
-    const float4 a = src[0], b = src[1];
-    acc[0] += w * a.x; acc[1] += w * a.y; acc[2] += w * a.z; acc[3] += w * a.w;
-    acc[4] += w * b.x; acc[5] += w * b.y; acc[6] += w * b.z; acc[7] += w * b.w;
+  const int c = (int)(i - t * per_row) * 4;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int k0 = 0; k0 < top_k; k0 += 4) {
+    int pos[4];
+    float w[4];
+    float4 yv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int k = k0 + u;
+      pos[u] = k < top_k ? pair_pos[t * top_k + k] : -1;
+      w[u] = pos[u] >= 0 ? topk_w[t * top_k + k] : 0.f;
+      yv[u] = pos[u] >= 0 ? *reinterpret_cast<const float4*>(y2 + (int64_t)pos[u] * H + c)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (pos[u] < 0) continue;
+      acc[0] += w[u] * yv[u].x;
+      acc[1] += w[u] * yv[u].y;
+      acc[2] += w[u] * yv[u].z;
+      acc[3] += w[u] * yv[u].w;
+    }
   }
-  uint4 o;
+  uint2 o;
   o.x = pack_h2(acc[0], acc[1]);
   o.y = pack_h2(acc[2], acc[3]);
-  o.z = pack_h2(acc[4], acc[5]);
-  o.w = pack_h2(acc[6], acc[7]);
-  *reinterpret_cast<uint4*>(out + t * H + c) = o;
+  *reinterpret_cast<uint2*>(out + t * H + c) = o;
 }
 
 struct MoeWs {
@@ -203,8 +256,9 @@ extern "C" int pe_moe_route(const float* logits, int64_t T, int E, int top_k, in
   if (T < 0 || E <= 0 || E > 256 || top_k <= 0 || top_k > 16 || top_k > E) return PE_ERR_DIMS;
   if (scoring != 0 && scoring != 1) return PE_ERR_DTYPE;
   if (T == 0) return PE_OK;
-  if ((T + 3) / 4 > INT32_MAX) return PE_ERR_DIMS;
-  moe_route_kernel<<<dim3((unsigned)((T + 3) / 4)), dim3(256), 0,
+  const int64_t wgs = (T + kRouteWaves - 1) / kRouteWaves;
+  if (wgs > INT32_MAX) return PE_ERR_DIMS;
+  moe_route_kernel<<<dim3((unsigned)wgs), dim3(64 * kRouteWaves), 0,
                      reinterpret_cast<hipStream_t>(stream)>>>(logits, T, E, top_k, renormalize,
                                                               scoring, correction_bias, topk_w,
                                                               topk_ids);
@@ -258,13 +312,17 @@ extern "C" int pe_moe_forward(const void* x, int64_t T, int H, int I, int E, int
   const int64_t row13 = nib13 ? (int64_t)nb13 * 64 : (int64_t)nb13 * kBlock;
   const int64_t row2 = nib2 ? (int64_t)nb2 * 64 : (int64_t)nb2 * kBlock;
 
-  // 1. bucket pairs by expert
-  moe_align_kernel<<<dim3(1), dim3(kAlignThreads), 0, st>>>(topk_ids, P, top_k, E, offsets,
-                                                             sorted_token, pair_pos);
-  if (int rc = launch_status()) return rc;
-  // 2. x -> pair f16
-  if (int rc = fwht128(x, PE_DTYPE_F16, T, H, H, ws + L.xtf, PE_XTF_PAIR_F16, st)) return rc;
-  // 3. gate/up + SwiGLU, each 128-column block of h transformed in the same
+  // 1. x -> pair f16, and the pairs bucketed by expert (last workgroup)
+  {
+    const int nbc = H / kBlock;
+    const int64_t fwht_wgs = (T * nbc + 15) / 16;
+    if (fwht_wgs + 1 > INT32_MAX) return PE_ERR_DIMS;
+    moe_prep_kernel<<<dim3((unsigned)(fwht_wgs + 1)), dim3(kPrepThreads), 0, st>>>(
+        reinterpret_cast<const uint16_t*>(x), T, nbc, reinterpret_cast<uint32_t*>(ws + L.xtf),
+        (int)fwht_wgs, topk_ids, P, top_k, E, offsets, sorted_token, pair_pos);
+    if (int rc = launch_status()) return rc;
+  }
+  // 2. gate/up + SwiGLU, each 128-column block of h transformed in the same
   // kernel -> htf [P, Ip] pair f16 (columns past I are zero)
   {
     SmallArgs a{reinterpret_cast<const uint8_t*>(w13_codes), w13_norms, ct13, n_levels13,
@@ -273,7 +331,7 @@ extern "C" int pe_moe_forward(const void* x, int64_t T, int H, int I, int E, int
                 nb13, wlayout(nib13, tiled13, nb13)};
     if (int rc = moe_grouped(nib13, SE_SWIGLU_XTF, a, E, st)) return rc;
   }
-  // 5. down -> y2 [P, H] fp32
+  // 3. down -> y2 [P, H] fp32
   {
     SmallArgs a{reinterpret_cast<const uint8_t*>(w2_codes), w2_norms, ct2, n_levels2,
                 reinterpret_cast<const uint32_t*>(ws + L.htf), nullptr, offsets,
@@ -281,8 +339,8 @@ extern "C" int pe_moe_forward(const void* x, int64_t T, int H, int I, int E, int
                 wlayout(nib2, tiled2, nb2)};
     if (int rc = moe_grouped(nib2, SE_F32, a, E, st)) return rc;
   }
-  // 6. weighted combine -> out fp16
-  const int64_t work = T * (H / 8);
+  // 4. weighted combine -> out fp16
+  const int64_t work = T * (H / 4);
   moe_combine_kernel<<<dim3((unsigned)((work + 255) / 256)), dim3(256), 0, st>>>(
       reinterpret_cast<const float*>(ws + L.y2), topk_w, pair_pos, T, top_k, H,
       reinterpret_cast<uint16_t*>(out));

@@ -629,6 +629,25 @@ def test_moe_route_matches_oracle(scoring, renorm, with_bias):
     np.testing.assert_allclose(w.cpu().numpy(), w_ref, rtol=2e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("t,e,k,scoring", [
+    (7, 8, 2, "softmax"),      # fewer experts than one wave
+    (33, 3, 3, "sigmoid"),     # top_k = E, odd E
+    (50, 160, 6, "softmax"),   # 3 experts per lane on some lanes
+    (9, 256, 16, "sigmoid"),   # the largest E and top_k
+    (5, 64, 1, "softmax"),
+])
+def test_moe_route_shapes(t, e, k, scoring):
+    from polarengine_vllm.moe_method import PolarQuantMoEMethod
+    _say(f"moe route t={t} e={e} k={k} {scoring}")
+    logits = O.seeded_normal((t, e), 1.0, 74 + e, np.float32)
+    logits[0, : min(e, 4)] = 0.25  # exact ties: the lower expert id ranks first
+    w_ref, ids_ref = O.moe_route(logits, k, True, scoring)
+    meth = PolarQuantMoEMethod(128, 3, 4)
+    w, ids = meth.select_experts(to_dev(logits), k, True, scoring)
+    assert np.array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_allclose(w.cpu().numpy(), w_ref, rtol=2e-6, atol=1e-7)
+
+
 def _moe_layer(rng, e, hdim, inter, b13, b2, tile=True):
     from polarengine_vllm.moe_method import PolarQuantMoEMethod
     ip = (inter + 127) // 128 * 128
