@@ -309,7 +309,7 @@ template <int NT>
 struct MoeBlk {
   u32x4v lo[NT];
   u32x4v hi[NT];
-  uint32_t nbits[NT];  // 32-bit: 16-bit members next to vectors were kept in memory
+  _Float16 nrm[NT];
 };
 
 // Weight source of one lane: buffer resources over this expert's codes and
@@ -340,7 +340,8 @@ __device__ __forceinline__ void moe_load_w(MoeBlk<NT>& k, const MoeSrc<NT>& src,
     if constexpr (!NIB)
       k.hi[j] = __builtin_bit_cast(
           u32x4v, __builtin_amdgcn_raw_buffer_load_b128(rc, src.voff_codes[j], cb + 64, kMoeBufNT));
-    k.nbits[j] = __builtin_amdgcn_raw_buffer_load_b16(rn, src.voff_norms[j], nbk, kMoeBufNT);
+    k.nrm[j] = __builtin_bit_cast(
+        _Float16, __builtin_amdgcn_raw_buffer_load_b16(rn, src.voff_norms[j], nbk, kMoeBufNT));
   }
 }
 
@@ -427,57 +428,100 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
       if (k < a.nb) sreg[k % D] = lda(k);
     __syncthreads();  // codebook table and stage 0 written
 
-    // A row of this lane in m-tile i: activation row 16 i + l16 of the stage
-    for (int b0 = 0; b0 < a.nb; b0 += D) {
+    // A row of this lane in m-tile i: activation row 16 i + l16 of the stage.
+    // The loop is compiled once per m-tile count, so that no branch on MT
+    // splits a block's lookups and MFMAs into separately scheduled pieces (a
+    // runtime test there left every lookup's latency exposed).
+    auto kloop = [&](auto mt_) {
+      constexpr int MTC = decltype(mt_)::value;
+      for (int b0 = 0; b0 < a.nb; b0 += D) {
 #pragma unroll
-      for (int d = 0; d < D; ++d) {
-        const int b = b0 + d;
-        if (b < a.nb) {  // uniform
-          const uint32_t st = abuf + (uint32_t)(b & 1) * kStage;
-          // each activation fragment is read from LDS once and feeds the
-          // gate and up tiles alike
-          float4v blk[NT][2];
+        for (int d = 0; d < D; ++d) {
+          const int b = b0 + d;
+          if (b < a.nb) {  // uniform
+            const uint32_t st = abuf + (uint32_t)(b & 1) * kStage;
+            // the weights are scaled by their block norm (fp16) before the
+            // MFMA, which accumulates straight into acc; the slot's norms are
+            // then dead once the last slab is dequantized, before the slot's
+            // next loads are issued (a value still live there is copied at the
+            // loop edge, and the copy waits for the load to arrive)
+            half2v nrm2[NT];
 #pragma unroll
-          for (int j = 0; j < NT; ++j)
+            for (int j = 0; j < NT; ++j) nrm2[j] = half2v{ring[d].nrm[j], ring[d].nrm[j]};
+            // each activation fragment is read from LDS once and feeds the
+            // gate and up tiles alike
+            // software pipeline over the four 32-wide slabs: the activation
+            // reads and codebook lookups of slab t + 1 are issued before the
+            // MFMAs of slab t
+            constexpr int TV = NIB ? 4 : 8;  // lookups per (tile, slab)
+            auto issue = [&](auto t_, u32x4v (&af)[2], uint32_t (&tv)[NT][TV]) {
+              constexpr int t = decltype(t_)::value;
 #pragma unroll
-            for (int i = 0; i < 2; ++i) blk[j][i] = float4v{0.f, 0.f, 0.f, 0.f};
+              for (int i = 0; i < MTC; ++i) {
+                const int r = 16 * i + l16;
+                af[i] = lds_ld128(st + (uint32_t)r * 256u + ((uint32_t)((4 * g + t) ^ (r & 15)) << 4));
+              }
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            u32x4v af[2];
+              for (int j = 0; j < NT; ++j) {
+                const uint32_t wl = ring[d].lo[j][t] & code_mask;
+                tv[j][0] = lds_ld32(tbl_addr<0>(wl, lane4));
+                tv[j][1] = lds_ld32(tbl_addr<1>(wl, lane4));
+                tv[j][2] = lds_ld32(tbl_addr<2>(wl, lane4));
+                tv[j][3] = lds_ld32(tbl_addr<3>(wl, lane4));
+                if constexpr (!NIB) {
+                  const uint32_t wh = ring[d].hi[j][t] & code_mask;
+                  tv[j][TV - 4] = lds_ld32(tbl_addr<0>(wh, lane4));
+                  tv[j][TV - 3] = lds_ld32(tbl_addr<1>(wh, lane4));
+                  tv[j][TV - 2] = lds_ld32(tbl_addr<2>(wh, lane4));
+                  tv[j][TV - 1] = lds_ld32(tbl_addr<3>(wh, lane4));
+                }
+              }
+            };
+            auto mma = [&](const u32x4v (&af)[2], const uint32_t (&tv)[NT][TV]) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-              const int r = 16 * i + l16;
-              if (i < MT) af[i] = lds_ld128(st + (uint32_t)r * 256u + ((uint32_t)((4 * g + t) ^ (r & 15)) << 4));
+              for (int j = 0; j < NT; ++j) {
+                u32x4v bw;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                  // int8: (lo16 of the first-position entry, lo16 of the second)
+                  const uint32_t p = NIB ? tv[j][q] : __builtin_amdgcn_perm(tv[j][TV - 4 + q], tv[j][q], 0x05040100u);
+                  bw[q] = __builtin_bit_cast(uint32_t, as_h2(p) * nrm2[j]);
+                }
+                const half8v bf = __builtin_bit_cast(half8v, bw);
+#pragma unroll
+                for (int i = 0; i < MTC; ++i)
+                  acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, af[i]), bf,
+                                                                     acc[i][j], 0, 0, 0);
+              }
+            };
+            u32x4v af0[2], af1[2];
+            uint32_t tv0[NT][TV], tv1[NT][TV];
+            issue(std::integral_constant<int, 0>{}, af0, tv0);
+            issue(std::integral_constant<int, 1>{}, af1, tv1);
+            __builtin_amdgcn_sched_barrier(0);
+            mma(af0, tv0);
+            issue(std::integral_constant<int, 2>{}, af0, tv0);
+            __builtin_amdgcn_sched_barrier(0);
+            mma(af1, tv1);
+            issue(std::integral_constant<int, 3>{}, af1, tv1);
+            __builtin_amdgcn_sched_barrier(0);
+            mma(af0, tv0);
+            mma(af1, tv1);
+            __builtin_amdgcn_sched_barrier(0);
+            moe_load_w<NIB, NT>(ring[d], src, b + D, a.nb, a.lay);
+            // next stage: block b + 1 into the other buffer (its readers, block
+            // b - 1, finished before the previous barrier); load block b + 1 + D
+            if (b + 1 < a.nb) {
+              if (sr < kMoeRows) lds_st128(abuf + (uint32_t)((b + 1) & 1) * kStage + sdst, sreg[(d + 1) % D]);
+              if (b + 1 + D < a.nb) sreg[(d + 1) % D] = lda(b + 1 + D);
             }
-#pragma unroll
-            for (int j = 0; j < NT; ++j) {
-              const uint32_t wl = ring[d].lo[j][t] & code_mask;
-              const uint32_t wh = NIB ? 0u : (ring[d].hi[j][t] & code_mask);
-              const half8v bf = dequant_slab_raw<NIB>(nullptr, wl, wh, lane4);
-#pragma unroll
-              for (int i = 0; i < 2; ++i)
-                if (i < MT)
-                  blk[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, af[i]), bf,
-                                                                     blk[j][i], 0, 0, 0);
-            }
+            __syncthreads();
           }
-#pragma unroll
-          for (int j = 0; j < NT; ++j) {
-            const float nrm = h2f((uint16_t)ring[d].nbits[j]);
-#pragma unroll
-            for (int i = 0; i < 2; ++i) acc[i][j] += blk[j][i] * nrm;
-          }
-          moe_load_w<NIB, NT>(ring[d], src, b + D, a.nb, a.lay);
-          // next stage: block b + 1 into the other buffer (its readers, block
-          // b - 1, finished before the previous barrier); load block b + 1 + D
-          if (b + 1 < a.nb) {
-            if (sr < kMoeRows) lds_st128(abuf + (uint32_t)((b + 1) & 1) * kStage + sdst, sreg[(d + 1) % D]);
-            if (b + 1 + D < a.nb) sreg[(d + 1) % D] = lda(b + 1 + D);
-          }
-          __syncthreads();
         }
       }
-    }
+    };
+    if (MT == 2) kloop(std::integral_constant<int, 2>{});
+    else kloop(std::integral_constant<int, 1>{});
 
     if constexpr (EP == SE_SWIGLU_XTF) {
       // The workgroup's 128 columns are one 128-block of h: silu(gate) * up
