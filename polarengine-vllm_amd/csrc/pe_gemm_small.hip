@@ -388,6 +388,7 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
     fill_codebook<TBL_F16>(0, a.ct, a.n_levels, tbl_entries, kMoeWaves);
 
   // staging role of this thread: row sr, 16-byte chunk sc of the 256-byte block row
+  static_assert(kMoeThreads == 16 * kMoeRows, "one 16-byte chunk of one staged row per thread");
   const int sr = tid >> 4, sc = tid & 15;
   const uint32_t sdst = (uint32_t)sr * 256u + ((uint32_t)(sc ^ (sr & 15)) << 4);
   const int64_t xrow = (int64_t)a.nb * 64;  // uint32 per activation row
@@ -395,16 +396,16 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
   for (int mbase = 0; mbase < M; mbase += kMoeRows) {
     const int mrem = M - mbase;
     const int MT = mrem > 16 ? 2 : 1;
-    const bool salive = sr < kMoeRows && mbase + sr < M;
-    const uint32_t* ssrc = nullptr;
-    if (salive) {
-      int r = row0 + mbase + sr;
-      if (a.a_rows) r = a.a_rows[r];
-      ssrc = a.xp + (int64_t)r * xrow + sc * 4;
-    }
+    // Rows past M re-read row M - 1 and blocks past the end re-read the last
+    // block: every lane issues the same loads on every path, so the
+    // compiler's vmcnt waits stay exact (a conditional load made it wait for
+    // every outstanding load). Rows past M only feed outputs never stored.
+    int srow = row0 + (mbase + sr < M ? mbase + sr : M - 1);
+    if (a.a_rows) srow = a.a_rows[srow];
+    const uint32_t* ssrc = a.xp + (int64_t)srow * xrow + sc * 4;
     auto lda = [&](int b) -> u32x4v {
-      return salive ? *reinterpret_cast<const u32x4v*>(ssrc + (int64_t)b * 64)
-                    : u32x4v{0u, 0u, 0u, 0u};
+      b = b < a.nb ? b : a.nb - 1;
+      return *reinterpret_cast<const u32x4v*>(ssrc + (int64_t)b * 64);
     };
     float4v acc[2][NT];
 #pragma unroll
@@ -422,10 +423,9 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
     // waits in sreg[k % D]
     u32x4v sreg[D];
     sreg[0] = lda(0);
-    if (sr < kMoeRows) lds_st128(abuf + sdst, sreg[0]);
+    lds_st128(abuf + sdst, sreg[0]);
 #pragma unroll
-    for (int k = 1; k <= D; ++k)
-      if (k < a.nb) sreg[k % D] = lda(k);
+    for (int k = 1; k <= D; ++k) sreg[k % D] = lda(k);
     __syncthreads();  // codebook table and stage 0 written
 
     // A row of this lane in m-tile i: activation row 16 i + l16 of the stage.
@@ -511,10 +511,8 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
             moe_load_w<NIB, NT>(ring[d], src, b + D, a.nb, a.lay);
             // next stage: block b + 1 into the other buffer (its readers, block
             // b - 1, finished before the previous barrier); load block b + 1 + D
-            if (b + 1 < a.nb) {
-              if (sr < kMoeRows) lds_st128(abuf + (uint32_t)((b + 1) & 1) * kStage + sdst, sreg[(d + 1) % D]);
-              if (b + 1 + D < a.nb) sreg[(d + 1) % D] = lda(b + 1 + D);
-            }
+            if (b + 1 < a.nb) lds_st128(abuf + (uint32_t)((b + 1) & 1) * kStage + sdst, sreg[(d + 1) % D]);
+            sreg[(d + 1) % D] = lda(b + 1 + D);
             __syncthreads();
           }
         }
