@@ -272,6 +272,23 @@ def summarize_pmc(fetch_csv, write_csv):
     return out
 
 
+def prefill_extra(dev):
+    """Prefill linear at M=2048 (FWHT-128 of x into pair f16, then the MFMA
+    GEMM): Q4 12288x4096 and the Q3 4096x12288 down projection."""
+    out = {}
+    flops = 2.0 * 2048 * 12288 * 4096
+    for name, (nn, kk, bb, seed) in (("prefill_m2048", (12288, 4096, 4, 300)),
+                                     ("prefill_down_q3_m2048", (4096, 12288, 3, 301))):
+        pf = Linear(nn, kk, bb, 2048, dev, seed=seed)
+        t_pf = time_eager(pf, 3, 20, dev)
+        out[name] = {"us_per_call": round(t_pf * 1e6, 1),
+                     "TFLOP/s": round(flops / t_pf / 1e12, 1),
+                     "mfma_frac": round(flops / t_pf / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                     "includes": "FWHT-128 of x (pair f16) + MFMA GEMM"}
+        del pf
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -284,6 +301,9 @@ def main():
     ap.add_argument("--headline-only", action="store_true",
                     help="time only the headline call (for a rocprofv3 kernel trace whose "
                          "average covers exactly the headline dispatches)")
+    ap.add_argument("--only-extra", choices=("moe", "prefill", "kv"),
+                    help="time only one of the extra workloads and print its JSON (for a "
+                         "rocprofv3 kernel trace of that path alone)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print the traffic JSON from the two pmc passes and exit")
     args = ap.parse_args()
@@ -299,6 +319,10 @@ def main():
     _lib.lib()
     if args.profile_traffic:
         profile_traffic(dev)
+        return
+    if args.only_extra:
+        fn = {"moe": moe_extra, "prefill": prefill_extra, "kv": kv_extra}[args.only_extra]
+        print(json.dumps(fn(dev)))
         return
 
     n, k, bits, m = 12288, 4096, 4, 1
@@ -329,20 +353,7 @@ def main():
             extra[f"decode_{name}_m{mm}"] = {"us_per_call": round(t * 1e6, 2), "GB/s": round(gb, 1),
                                              "hbm_frac": round(gb / HBM_PEAK_GBS, 4)}
             del lay
-    pf = Linear(n, k, bits, 2048, dev, seed=300)
-    t_pf = time_eager(pf, 3, 20, dev)
-    flops = 2.0 * 2048 * n * k
-    extra["prefill_m2048"] = {"us_per_call": round(t_pf * 1e6, 1),
-                              "TFLOP/s": round(flops / t_pf / 1e12, 1),
-                              "mfma_frac": round(flops / t_pf / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
-                              "includes": "FWHT-128 of x (pair f16) + MFMA GEMM"}
-    del pf
-    pf = Linear(4096, 12288, 3, 2048, dev, seed=301)
-    t_pf = time_eager(pf, 3, 20, dev)
-    extra["prefill_down_q3_m2048"] = {"us_per_call": round(t_pf * 1e6, 1),
-                                      "TFLOP/s": round(flops / t_pf / 1e12, 1),
-                                      "mfma_frac": round(flops / t_pf / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
-    del pf
+    extra.update(prefill_extra(dev))
     extra["cache_hot_m1"] = {"us_per_call": round(t_hot * 1e6, 2),
                              "GB/s": round(B / t_hot / 1e9, 1),
                              "note": "one weight copy, Infinity-Cache resident"}
