@@ -393,8 +393,19 @@ __global__ __launch_bounds__(256) void dec_split_reduce_kernel(const float* __re
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (int64_t)M * N) return;
   const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
+  const int64_t slab = (int64_t)M * N;
+  const float* p = part + (int64_t)m * N + n;
+  // the loads of four groups are issued together, then added in group order
   float s = 0.f;
-  for (int g = 0; g < G; ++g) s += part[((int64_t)g * M + m) * N + n];
+  int g = 0;
+  for (; g + 4 <= G; g += 4) {
+    const float v0 = p[g * slab], v1 = p[(g + 1) * slab], v2 = p[(g + 2) * slab], v3 = p[(g + 3) * slab];
+    s += v0;
+    s += v1;
+    s += v2;
+    s += v3;
+  }
+  for (; g < G; ++g) s += p[g * slab];
   _Float16 hv = (_Float16)s;
   if (bias) hv = (_Float16)((float)hv + h2f(bias[n]));
   y[(int64_t)m * ldy + n] = hv;
