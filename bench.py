@@ -187,7 +187,7 @@ def moe_extra(dev, t=128, e=64, h=2048, inter=1408, k=8, b13=3, b2=4):
                                   "GB/s": round(wbytes * active / e / tm / 1e9, 1),
                                   "hbm_frac": round(wbytes * active / e / tm / 1e9 / HBM_PEAK_GBS, 4),
                                   "expert_bytes": wbytes, "active_experts": active,
-                                  "includes": "routing + align + w13 SwiGLU + w2 + combine"}}
+                                  "includes": "routing + x FWHT with expert bucketing + w13 SwiGLU (FWHT of h fused) + w2 + combine"}}
 
 
 def cpu_baseline(budget_s=15.0):
