@@ -345,11 +345,24 @@ __device__ __forceinline__ void moe_load_w(MoeBlk<NT>& k, const MoeSrc<NT>& src,
   }
 }
 
+// first weight row (within the expert) of tile j of `wave`: SwiGLU tiles are
+// the gate tile's row 16 (8 x + wave) (the up tile adds I at the use); the
+// two-tile SE_F32 workgroup x covers rows 256 x .. 256 x + 255, tile j at
+// 128 j + 16 wave
+template <bool SWI, int NT>
+__device__ __forceinline__ int moe_tile_row(int x, int wave, int j) {
+  if constexpr (SWI || NT == 1) return (x * kMoeWaves + wave) * 16;
+  else return x * (NT * 16 * kMoeWaves) + j * (16 * kMoeWaves) + wave * 16;
+}
+
 template <bool NIB, int EP, int D>
 __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint32_t code_mask,
                                                                int tbl_entries, uint32_t abuf) {
   constexpr bool SWI = EP == SE_SWIGLU || EP == SE_SWIGLU_XTF;
-  constexpr int NT = SWI ? 2 : 1;
+  // tiles per wave: gate and up (SwiGLU); SE_F32 with nibble codes: two
+  // 16-row tiles 128 rows apart, so the workgroup's table fill, staging and
+  // prologue serve 256 weight rows
+  constexpr int NT = SWI ? 2 : (NIB ? 2 : 1);
   constexpr uint32_t kStage = kMoeRows * 256;  // bytes per LDS stage
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -374,7 +387,7 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
   src.norms_none = __builtin_amdgcn_make_buffer_rsrc((void*)norms, (short)0, 0, kMoeBufFlags);
 #pragma unroll
   for (int j = 0; j < NT; ++j) {
-    int n = nt * 16 + l16;
+    int n = moe_tile_row<SWI, NT>(blockIdx.x, wave, j) + l16;
     if (n >= a.N) n = a.N - 1;
     if (SWI && j == 1) n += a.N;
     if (n >= wrows) n = wrows - 1;
@@ -558,24 +571,27 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
       store_pair_block(v, q, reinterpret_cast<uint32_t*>(a.y) + prow * (a.ldy / 2) + (int64_t)blockIdx.x * 64, live);
     } else {
     // epilogue from registers: D element (lane, e) of m-tile i is row
-    // 16 i + 4 (lane / 16) + e, column 16 nt + lane % 16
-    const int n = nt * 16 + l16;
-    if (n < a.N) {
+    // 16 i + 4 (lane / 16) + e, column moe_tile_row + lane % 16
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        if (i >= MT) continue;
+    for (int j = 0; j < (SWI ? 1 : NT); ++j) {
+      const int n = moe_tile_row<SWI, NT>(blockIdx.x, wave, j) + l16;
+      if (n < a.N) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int m = mbase + 16 * i + 4 * g + e;
-          if (m >= M) continue;
-          const int64_t row = row0 + m;
-          const float s = acc[i][0][e];
-          if constexpr (EP == SE_F32) {
-            reinterpret_cast<float*>(a.y)[row * a.ldy + n] = s;
-          } else {
-            const float u = acc[i][NT - 1][e];
-            const float act = s / (1.f + __expf(-s)) * u;
-            reinterpret_cast<_Float16*>(a.y)[row * a.ldy + n] = (_Float16)act;
+        for (int i = 0; i < 2; ++i) {
+          if (i >= MT) continue;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int m = mbase + 16 * i + 4 * g + e;
+            if (m >= M) continue;
+            const int64_t row = row0 + m;
+            const float s = acc[i][j][e];
+            if constexpr (EP == SE_F32) {
+              reinterpret_cast<float*>(a.y)[row * a.ldy + n] = s;
+            } else {
+              const float u = acc[i][NT - 1][e];
+              const float act = s / (1.f + __expf(-s)) * u;
+              reinterpret_cast<_Float16*>(a.y)[row * a.ldy + n] = (_Float16)act;
+            }
           }
         }
       }
@@ -598,7 +614,9 @@ static int launch_moe_t(const SmallArgs& a, int groups, hipStream_t st) {
                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
   }();
   (void)attr_ok;
-  const int wgs = (a.N + 16 * kMoeWaves - 1) / (16 * kMoeWaves);
+  constexpr bool SWI = EP == SE_SWIGLU || EP == SE_SWIGLU_XTF;
+  const int rows_per_wg = 16 * kMoeWaves * (SWI ? 1 : (NIB ? 2 : 1));
+  const int wgs = (a.N + rows_per_wg - 1) / rows_per_wg;
   const uint8_t mb = NIB ? (uint8_t)((a.n_levels - 1) * 0x11) : (uint8_t)(a.n_levels - 1);
   kern<<<dim3(wgs, groups), dim3(kMoeThreads), lds, st>>>(a, 0x01010101u * mb, entries, abuf);
   return launch_status();
