@@ -304,6 +304,9 @@ static int launch_small_ep(const SmallArgs& a, int groups, hipStream_t st) {
 constexpr int kMoeWaves = 8;
 constexpr int kMoeThreads = 64 * kMoeWaves;
 constexpr int kMoeRows = 32;  // activation rows per pass (two 16-row m-tiles)
+// 16-row tiles per wave of the SE_F32 (w2) kernel with nibble codes; 2 keeps
+// two workgroups per CU (4 tiles: one, and slower)
+constexpr int kMoeF32Tiles = 2;
 
 template <int NT>
 struct MoeBlk {
@@ -362,7 +365,7 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
   // tiles per wave: gate and up (SwiGLU); SE_F32 with nibble codes: two
   // 16-row tiles 128 rows apart, so the workgroup's table fill, staging and
   // prologue serve 256 weight rows
-  constexpr int NT = SWI ? 2 : (NIB ? 2 : 1);
+  constexpr int NT = SWI ? 2 : (NIB ? kMoeF32Tiles : 1);
   constexpr uint32_t kStage = kMoeRows * 256;  // bytes per LDS stage
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -615,7 +618,7 @@ static int launch_moe_t(const SmallArgs& a, int groups, hipStream_t st) {
   }();
   (void)attr_ok;
   constexpr bool SWI = EP == SE_SWIGLU || EP == SE_SWIGLU_XTF;
-  const int rows_per_wg = 16 * kMoeWaves * (SWI ? 1 : (NIB ? 2 : 1));
+  const int rows_per_wg = 16 * kMoeWaves * (SWI ? 1 : (NIB ? kMoeF32Tiles : 1));
   const int wgs = (a.N + rows_per_wg - 1) / rows_per_wg;
   const uint8_t mb = NIB ? (uint8_t)((a.n_levels - 1) * 0x11) : (uint8_t)(a.n_levels - 1);
   kern<<<dim3(wgs, groups), dim3(kMoeThreads), lds, st>>>(a, 0x01010101u * mb, entries, abuf);
