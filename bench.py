@@ -338,7 +338,7 @@ def main():
     t_hot, _ = time_graph(layers[:1], 128, args.warmup, args.steps, dev)
 
     extra = {}
-    for mm in (4, 8, 16):
+    for mm in (4, 8, 16, 32, 64):
         lay = [Linear(n, k, bits, mm, dev, seed=200 + i) for i in range(N_COPIES)]
         t, _ = time_graph(lay, 4, 64, 512, dev)
         extra[f"decode_m{mm}"] = {"us_per_call": round(t * 1e6, 2),

@@ -177,7 +177,8 @@ __device__ __forceinline__ void dec_table_write(const DecTable<NIB>& t, int n_le
 // registers per lane. SPLIT: the K blocks are divided into gridDim.y groups,
 // blockIdx.y's group only (its activations alone in LDS); y then receives
 // fp32 partial sums [gridDim.y][M][N], added by dec_split_reduce_kernel.
-template <bool NIB, int TN, int KS, bool XRAW, bool MASK, int XC, int D, bool CTV, bool SPLIT>
+template <bool NIB, int TN, int KS, bool XRAW, bool MASK, int XC, int D, bool CTV, bool SPLIT,
+          int MTD = 1>
 __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
     const float* __restrict__ ct, int n_levels, uint32_t code_mask,
@@ -322,17 +323,26 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
   // ---- 3. K loop, D blocks in flight: A (row m = l16) from
   // LDS, B dequantized from the code registers; a block's lookups are issued
   // before its MFMAs.
-  float4v acc = float4v{0.f, 0.f, 0.f, 0.f};
-  // A row of this lane: rows past M repeat row M-1; they only feed D rows
-  // >= M, which are never stored
+  // MTD m-tiles of 16 rows share every weight lookup
+  float4v acc[MTD];
+#pragma unroll
+  for (int i = 0; i < MTD; ++i) acc[i] = float4v{0.f, 0.f, 0.f, 0.f};
+  // A row of this lane in m-tile i: row 16 i + l16; rows past M repeat row
+  // M-1; they only feed D rows >= M, which are never stored
   // (item (m, b) of the group sits at m * xrow_b + (b - kb0) * 256: the base
   // wraps below zero and comes back with b >= kb0)
-  const uint32_t arow = xs_addr + (uint32_t)(l16 < M ? l16 : M - 1) * xrow_b -
-                        (uint32_t)kb0 * 256u + 64u * g;
-  auto do_block = [&](const DecBlk<NIB, 1>& k, int b) {
-    u32x4v af[4];
+  uint32_t arow[MTD];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) af[t] = lds_ld128(arow + (uint32_t)b * 256u + 16u * t);
+  for (int i = 0; i < MTD; ++i) {
+    const int r = 16 * i + l16;
+    arow[i] = xs_addr + (uint32_t)(r < M ? r : M - 1) * xrow_b - (uint32_t)kb0 * 256u + 64u * g;
+  }
+  auto do_block = [&](const DecBlk<NIB, 1>& k, int b) {
+    u32x4v af[MTD][4];
+#pragma unroll
+    for (int i = 0; i < MTD; ++i)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) af[i][t] = lds_ld128(arow[i] + (uint32_t)b * 256u + 16u * t);
     half8v bf[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -343,12 +353,18 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
       }
       bf[t] = dec_dequant<NIB>(wl, wh, lane4);
     }
-    float4v blk = float4v{0.f, 0.f, 0.f, 0.f};
+    float4v blk[MTD];
+#pragma unroll
+    for (int i = 0; i < MTD; ++i) blk[i] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < 4; ++t)
-      blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, af[t]), bf[t], blk,
-                                                   0, 0, 0);
-    acc += blk * h2f(k.nb[0]);
+#pragma unroll
+      for (int i = 0; i < MTD; ++i)
+        blk[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8v, af[i][t]), bf[t],
+                                                        blk[i], 0, 0, 0);
+    const float nrm = h2f(k.nb[0]);
+#pragma unroll
+    for (int i = 0; i < MTD; ++i) acc[i] += blk[i] * nrm;
   };
   for (int i = 0; i < nbw; i += D) {
 #pragma unroll
@@ -359,20 +375,25 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
     }
   }
 
-  // ---- 4. combine the KS K-slices of each tile through LDS: red[ks][jt][lane][4]
+  // ---- 4. combine the KS K-slices of each tile through LDS:
+  // red[ks][jt][i][lane][4]
   __syncthreads();
-  lds_st128((uint32_t)(((ks * TN + jt) * 64 + lane) * 16), __builtin_bit_cast(u32x4v, acc));
+#pragma unroll
+  for (int i = 0; i < MTD; ++i)
+    lds_st128((uint32_t)((((ks * TN + jt) * MTD + i) * 64 + lane) * 16), __builtin_bit_cast(u32x4v, acc[i]));
   __syncthreads();
-  // outputs: rows m < M (D element e of lane l: row 4*(l/16) + e), 16*TN columns
-  for (int o = tid; o < TN * 256; o += NW * 64) {
-    const int j = o >> 8, le = o & 255, ln = le >> 2, e = le & 3;
-    const int m = 4 * (ln >> 4) + e;
+  // outputs: rows m < M (D element e of lane l in m-tile i: row 16 i +
+  // 4 (l / 16) + e), 16 TN columns
+  for (int o = tid; o < TN * MTD * 256; o += NW * 64) {
+    const int ji = o >> 8, le = o & 255, ln = le >> 2, e = le & 3;  // ji = j * MTD + i
+    const int j = ji / MTD, i = ji - j * MTD;
+    const int m = 16 * i + 4 * (ln >> 4) + e;
     const int n = (blockIdx.x * TN + j) * 16 + (ln & 15);
     if (m >= M || n >= N) continue;
     float s = 0.f;
 #pragma unroll
     for (int w = 0; w < KS; ++w)
-      s += __builtin_bit_cast(float, lds_ld32((uint32_t)((((w * TN + j) * 64) * 4 + le) * 4)));
+      s += __builtin_bit_cast(float, lds_ld32((uint32_t)(((((w * TN + j) * MTD + i) * 64) * 4 + le) * 4)));
     if constexpr (SPLIT) {
       reinterpret_cast<float*>(y)[((int64_t)blockIdx.y * M + m) * N + n] = s;
     } else {
@@ -426,19 +447,23 @@ constexpr int dec_ks() { return kDecW / TN; }
 // 16-lane groups of the workgroup
 static int dec_xc(int M, int nb, int nw) { return (M * nb + 4 * nw - 1) / (4 * nw); }
 
+// 16-row m-tiles per MFMA pass: 1 (M <= 16), 2 (M <= 32) or 4 (M <= 64)
+static int dec_mtd(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : 4; }
+
 static size_t dec_lds(bool nibble, int M, int nb, int n_levels, int nw) {
   size_t lds = (size_t)table_entries(nibble, n_levels) * 256 + (size_t)M * (nb * 256 + 16);
-  const size_t red = (size_t)nw * 64 * 16;
+  const size_t red = (size_t)nw * dec_mtd(M) * 64 * 16;
   return lds < red ? red : lds;
 }
 
-template <bool NIB, int TN, bool XRAW, bool MASK, int XC, bool CTV, bool SPLIT = false>
+template <bool NIB, int TN, bool XRAW, bool MASK, int XC, bool CTV, bool SPLIT = false, int MTD = 1>
 static int launch_dec(const DecArgs& a, hipStream_t st, int groups = 1) {
   constexpr int KS = dec_ks<TN>(), NW = TN * KS;
   // blocks in flight per wave (nibble 1 KB, int8 2 KB each); deeper rings
   // measured slower (3 -> 8: 7.6 -> 8.8 us on Q4 12288 x 4096)
   constexpr int D = NIB ? 3 : 2;
-  auto kern = gemv_mfma_kernel<NIB, TN, KS, XRAW, MASK, XC, D, CTV, SPLIT>;
+  auto kern = gemv_mfma_kernel<NIB, TN, KS, XRAW, MASK, XC, D, CTV, SPLIT, MTD>;
+  if (dec_mtd(a.M) != MTD) return PE_ERR_DIMS;
   const int nbg = (a.nb + groups - 1) / groups;  // most blocks of one group
   const size_t lds = dec_lds(NIB, a.M, nbg, a.n_levels, NW);
   if (lds > 160 * 1024 || dec_xc(a.M, nbg, NW) > XC) return PE_ERR_DIMS;
@@ -520,7 +545,8 @@ static int launch_dec_tn(const DecArgs& a, hipStream_t st) {
 // K split over workgroups: 12 row tiles per workgroup (one K range per wave),
 // gridDim.y groups sized for at most one workgroup per CU. Returns the group
 // count, or 0 when the split does not apply (fewer than 2 groups, or one
-// group's activations still do not fit).
+// group's activations still do not fit). M > 16 (two or four m-tiles) takes
+// more groups, and rounds, until one group's activations fit.
 constexpr int kSplitTN = 12;
 static int dec_split_groups(bool nibble, int M, int N, int nb, int n_levels) {
   const int wgn = ((N + 15) / 16 + kSplitTN - 1) / kSplitTN;
@@ -528,6 +554,12 @@ static int dec_split_groups(bool nibble, int M, int N, int nb, int n_levels) {
   // workgroup would run as a second round of its own
   int G = num_cus() / wgn;
   if (G > nb) G = nb;
+  if (M > 16) {
+    if (G < 2) G = nb < 2 ? nb : 2;
+    while (G < nb && (dec_xc(M, (nb + G - 1) / G, kDecW) > 8 ||
+                      dec_lds(nibble, M, (nb + G - 1) / G, n_levels, kDecW) > 160 * 1024))
+      ++G;
+  }
   if (G < 2) return 0;
   const int nbg = (nb + G - 1) / G;
   if (dec_xc(M, nbg, kDecW) > 8 || dec_lds(nibble, M, nbg, n_levels, kDecW) > 160 * 1024) return 0;
@@ -537,10 +569,11 @@ static int dec_split_groups(bool nibble, int M, int N, int nb, int n_levels) {
 // the split path where the whole activation set does not fit in LDS (each
 // workgroup then transforms and holds only its K range of the activations;
 // where it fits, one launch without the partial-sum pass measured faster),
-// for M >= 2 (M = 1 takes no workspace: it keeps its own paths)
+// for M >= 2 (M = 1 takes no workspace: it keeps its own paths); M > 16 runs
+// only here
 static bool dec_use_split(bool nibble, int M, int N, int nb, int n_levels) {
   const bool whole = dec_xc(M, nb, kDecW) <= 8 && dec_lds(nibble, M, nb, n_levels, kDecW) <= 160 * 1024;
-  return M >= 2 && !whole && dec_split_groups(nibble, M, N, nb, n_levels) > 0;
+  return M >= 2 && (M > 16 || !whole) && dec_split_groups(nibble, M, N, nb, n_levels) > 0;
 }
 
 template <bool NIB, bool XRAW, bool MASK>
@@ -548,6 +581,19 @@ static int launch_dec_split(const DecArgs& a, hipStream_t st) {
   const int G = dec_split_groups(NIB, a.M, a.N, a.nb, a.n_levels);
   if (!a.ws || a.ws_bytes < (size_t)G * a.M * a.N * 4) return PE_ERR_WORKSPACE;
   const int xc = dec_xc(a.M, (a.nb + G - 1) / G, kDecW);
+  const int mtd = dec_mtd(a.M);
+  if (mtd > 1) {  // two or four m-tiles: activation registers 4 or 8
+    if (a.ct_host) {
+      if (mtd == 2) return xc <= 4 ? launch_dec<NIB, kSplitTN, XRAW, MASK, 4, true, true, 2>(a, st, G)
+                                   : launch_dec<NIB, kSplitTN, XRAW, MASK, 8, true, true, 2>(a, st, G);
+      return xc <= 4 ? launch_dec<NIB, kSplitTN, XRAW, MASK, 4, true, true, 4>(a, st, G)
+                     : launch_dec<NIB, kSplitTN, XRAW, MASK, 8, true, true, 4>(a, st, G);
+    }
+    if (mtd == 2) return xc <= 4 ? launch_dec<NIB, kSplitTN, XRAW, MASK, 4, false, true, 2>(a, st, G)
+                                 : launch_dec<NIB, kSplitTN, XRAW, MASK, 8, false, true, 2>(a, st, G);
+    return xc <= 4 ? launch_dec<NIB, kSplitTN, XRAW, MASK, 4, false, true, 4>(a, st, G)
+                   : launch_dec<NIB, kSplitTN, XRAW, MASK, 8, false, true, 4>(a, st, G);
+  }
   if (a.ct_host) {
     if (xc <= 2) return launch_dec<NIB, kSplitTN, XRAW, MASK, 2, true, true>(a, st, G);
     if (xc <= 4) return launch_dec<NIB, kSplitTN, XRAW, MASK, 4, true, true>(a, st, G);
@@ -567,16 +613,17 @@ static int launch_dec_m(const DecArgs& a, hipStream_t st) {
 }
 
 size_t gemv_mfma_workspace(bool nibble, int M, int N, int nb, int n_levels) {
-  if (M < 1 || M > 16 || !dec_use_split(nibble, M, N, nb, n_levels)) return 0;
+  if (M < 1 || M > kDecMaxRows || !dec_use_split(nibble, M, N, nb, n_levels)) return 0;
   return (size_t)dec_split_groups(nibble, M, N, nb, n_levels) * M * N * 4;
 }
 
 bool gemv_mfma_fits(bool nibble, int M, int N, int nb, int n_levels) {
-  if (M < 1 || M > 16) return false;
+  if (M < 1 || M > kDecMaxRows) return false;
   // buffer resources address codes and norms with 31-bit offsets (tiled
   // layouts round N up to 16 rows)
   if ((int64_t)(N + 15) * nb * (nibble ? 64 : kBlock) >= (int64_t)1 << 31) return false;
   if (dec_use_split(nibble, M, N, nb, n_levels)) return true;
+  if (M > 16) return false;  // two or four m-tiles: the split path only
   // the workgroup's 4 * kDecW lane groups hold the activations in <= 8 registers
   return dec_xc(M, nb, kDecW) <= 8 && dec_lds(nibble, M, nb, n_levels, kDecW) <= 160 * 1024;
 }

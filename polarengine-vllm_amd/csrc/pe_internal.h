@@ -96,7 +96,9 @@ int gemm_small(bool nibble, int epilogue, const SmallArgs& a, int groups, hipStr
 // SE_SWIGLU_XTF)
 int moe_grouped(bool nibble, int epilogue, const SmallArgs& a, int groups, hipStream_t st);
 
-// pe_gemv_mfma.hip: decode GEMV, 1 <= M <= 16, fp16 out (+ fp16 bias)
+// pe_gemv_mfma.hip: decode GEMV, 1 <= M <= kDecMaxRows (M > 16 through the K
+// split with two or four m-tiles), fp16 out (+ fp16 bias)
+constexpr int kDecMaxRows = 64;
 struct DecArgs {
   const uint8_t* codes;
   const uint16_t* norms;

@@ -3,13 +3,14 @@
 // (polar_matmul, kernels/polar_gemm.py:425-534).
 //
 // Routing by M (rows of the activation):
-//   M <= 16 (when x, or for M >= 8 one K group of it, fits in LDS beside the
-//   codebook table)
+//   M <= 16 (when x, or one K group of it, fits in LDS beside the codebook
+//   table), or 17 <= M <= 64 when one K group fits
 //                     -> gemv_mfma: decode GEMV on 16x16x32 MFMA, FWHT fused
 //                        into its prologue (one launch per linear; with the K
-//                        split over workgroups, plus a partial-sum reduction);
+//                        split over workgroups, plus a partial-sum reduction;
+//                        M > 16 with two or four m-tiles per weight lookup);
 //   M == 1 otherwise  -> gemv1 (register-resident dot2 GEMV, LDS activations);
-//   2 <= M <= 64      -> FWHT-128 to pair-f16 x_tf, then the small-M MFMA
+//   2 <= M <= 64 else -> FWHT-128 to pair-f16 x_tf, then the small-M MFMA
 //                        kernel (16x16x32 f16, K split across waves);
 //   M >  kSmallM      -> FWHT-128 to pair-f16 x_tf, then the prefill GEMM
 //                        (32x32x16 f16 MFMA, LDS A tiles, dequantized B).
@@ -36,9 +37,9 @@ static int check_format(int bits, int packed, int n_levels, bool* nibble, bool* 
 
 using namespace pe;
 
-// fp32 partial sums of the K-split decode path (M <= 16), 0 otherwise
+// fp32 partial sums of the K-split decode path (M <= 64), 0 otherwise
 static size_t decode_workspace(int64_t M, int kp, int out_f, int bits, int packed) {
-  if (M < 1 || M > 16 || bits < 2 || bits > 8) return 0;
+  if (M < 1 || M > kDecMaxRows || bits < 2 || bits > 8) return 0;
   const bool nib = (packed & PE_PACK_NIBBLE) != 0 && bits <= 4;
   return round_up(gemv_mfma_workspace(nib, (int)M, out_f, kp / kBlock, 1 << bits), 256);
 }
@@ -77,7 +78,7 @@ extern "C" int pe_linear_forward_xtf(const void* x_tf_pair, int64_t M, int in_f_
   if (!aligned16(x_tf_pair) || !aligned16(codes)) return PE_ERR_ALIGN;
   if (M == 0) return PE_OK;
   const int nb = in_f_padded / kBlock;
-  if (M <= 16 && gemv_mfma_fits(nib, (int)M, out_f, nb, n_levels)) {
+  if (M <= kDecMaxRows && gemv_mfma_fits(nib, (int)M, out_f, nb, n_levels)) {
     if (workspace && !aligned16(workspace)) return PE_ERR_ALIGN;
     DecArgs a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels,
               x_tf_pair, (int64_t)in_f_padded, y, out_f, reinterpret_cast<const uint16_t*>(bias),
@@ -107,7 +108,7 @@ extern "C" int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f
   if (!aligned16(x) || !aligned16(codes) || (ldx * 2) % 16) return PE_ERR_ALIGN;
   if (M == 0) return PE_OK;
   const int nb = in_f / kBlock;
-  if (M <= 16 && gemv_mfma_fits(nib, (int)M, out_f, nb, n_levels)) {
+  if (M <= kDecMaxRows && gemv_mfma_fits(nib, (int)M, out_f, nb, n_levels)) {
     if (workspace && !aligned16(workspace)) return PE_ERR_ALIGN;
     DecArgs a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels, x, ldx, y,
               out_f, reinterpret_cast<const uint16_t*>(bias), (int)M, out_f, nb,
