@@ -226,7 +226,7 @@ DECODE_CASES = [(1, 12288, 4096, 4), (1, 4096, 4096, 5), (2, 1000, 1408, 3),
                 # 17 <= M <= 64: two or four m-tiles per weight lookup, K split
                 (17, 12288, 4096, 4), (24, 4096, 12288, 3), (32, 12288, 4096, 4),
                 (48, 1000, 2048, 5), (64, 12288, 4096, 4), (64, 4096, 12288, 4),
-                (33, 700, 4096, 2), (40, 96, 640, 8)]
+                (33, 700, 4096, 2), (40, 96, 640, 8), (64, 50, 256, 4), (17, 16, 384, 3)]
 
 
 @pytest.mark.parametrize("m,n,k,bits", DECODE_CASES)
