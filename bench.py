@@ -274,7 +274,8 @@ def summarize_pmc(fetch_csv, write_csv):
 
 def prefill_extra(dev):
     """Prefill linear at M=2048 (FWHT-128 of x into pair f16, then the MFMA
-    GEMM): Q4 12288x4096 and the Q3 4096x12288 down projection."""
+    GEMM): Q4 12288x4096 and the Q3 4096x12288 down projection; and the Q4
+    down projection at M=128 / 512 (K split over workgroups)."""
     out = {}
     flops = 2.0 * 2048 * 12288 * 4096
     for name, (nn, kk, bb, seed) in (("prefill_m2048", (12288, 4096, 4, 300)),
@@ -286,6 +287,15 @@ def prefill_extra(dev):
                      "mfma_frac": round(flops / t_pf / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
                      "includes": "FWHT-128 of x (pair f16) + MFMA GEMM"}
         del pf
+    # chunked-prefill sizes on the down projection (few output tiles: K split)
+    for mm in (128, 512):
+        lay = [Linear(4096, 12288, 4, mm, dev, seed=310 + i) for i in range(4)]
+        t, _ = time_graph(lay, 4, 32, 256, dev)
+        fl = 2.0 * mm * 4096 * 12288
+        out[f"prefill_down_q4_m{mm}"] = {"us_per_call": round(t * 1e6, 1),
+                                         "TFLOP/s": round(fl / t / 1e12, 1),
+                                         "GB/s": round(algo_bytes(mm, 4096, 12288, 4) / t / 1e9, 1)}
+        del lay
     return out
 
 

@@ -179,6 +179,13 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
   if constexpr (NIB) fill_codebook<TBL_NIB_H2>(0, ct, n_levels, tbl_entries, NT / 64);
   else fill_codebook<TBL_F16>(0, ct, n_levels, tbl_entries, NT / 64);
 
+  // K range of this workgroup: gridDim.z groups split the 128-blocks; with
+  // more than one, each writes fp32 partial sums to its slab [M][ldy] of y
+  // (one group: the whole K range, y itself)
+  const int kb0 = (int)((int64_t)nb * blockIdx.z / gridDim.z);
+  const int nbz = (int)((int64_t)nb * (blockIdx.z + 1) / gridDim.z) - kb0;
+  y = reinterpret_cast<char*>(y) + (int64_t)blockIdx.z * M * ldy * (OM == 0 ? 4 : 2);
+
   // A loader: thread t moves uint4 q = t + NT i (row q >> 3, 16-byte col q & 7)
   const int64_t xrow_u32 = (int64_t)nb * 64;
   const uint32_t* a_src[KA];
@@ -189,7 +196,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
     const int r = q >> 3, c = q & 7;
     int m = m0 + r;
     if (m >= M) m = M - 1;  // clamped rows feed discarded outputs only
-    a_src[i] = xp + (int64_t)m * xrow_u32 + c * 4;
+    a_src[i] = xp + (int64_t)m * xrow_u32 + (int64_t)kb0 * 64 + c * 4;
     a_dst[i] = r * kAStride + c * 16;
   }
   // B rows of this wave
@@ -199,8 +206,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
   for (int j = 0; j < TNW; ++j) {
     int n = n0 + wn * TNW * 32 + j * 32 + l32;
     if (n >= N) n = N - 1;
-    b_row[j] = codes + lay.codes_off(n) + 16 * h;
-    n_row[j] = norms + lay.norms_off(n);
+    b_row[j] = codes + lay.codes_off(n) + 16 * h + (int64_t)kb0 * lay.c_blk;
+    n_row[j] = norms + lay.norms_off(n) + (int64_t)kb0 * lay.n_blk;
   }
 
   float16v acc[TMW][TNW];
@@ -211,7 +218,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  const int nkt = 2 * nb;  // half-block K-tiles (always even)
+  const int nkt = 2 * nbz;  // half-block K-tiles of this K range (always even)
   const int a_off = (wm * TMW * 32 + l32) * kAStride + 64 * h;
   u32x4v ar[KA];
   BTile<NIB, TNW> b0, b1;
@@ -453,6 +460,13 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
   else fill_codebook<TBL_F16>(0, ct, n_levels, tbl_entries, NT / 64);
   const uint32_t abuf = (uint32_t)tbl_entries * 256u;
 
+  // K range of this workgroup, in pairs of 128-blocks (the loop takes four
+  // half-blocks per step): gridDim.z groups; with more than one, fp32 partial
+  // sums go to slab blockIdx.z [M][ldy] of y
+  const int kb0 = 2 * (int)((int64_t)(nb / 2) * blockIdx.z / gridDim.z);
+  const int nbz = 2 * (int)((int64_t)(nb / 2) * (blockIdx.z + 1) / gridDim.z) - kb0;
+  y = reinterpret_cast<char*>(y) + (int64_t)blockIdx.z * M * ldy * (OM == OM_F16 ? 2 : 4);
+
   const int64_t xrow_u32 = (int64_t)nb * 64;
   const uint32_t* a_src[KA];
   uint32_t a_dst[KA];
@@ -462,7 +476,7 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
     const int r = q >> 3, c = q & 7;
     int m = m0 + r;
     if (m >= M) m = M - 1;  // clamped rows feed discarded outputs only
-    a_src[i] = xp + (int64_t)m * xrow_u32 + c * 4;
+    a_src[i] = xp + (int64_t)m * xrow_u32 + (int64_t)kb0 * 64 + c * 4;
     a_dst[i] = (uint32_t)(r * kARow4 + (((uint32_t)c ^ a4_swz(r)) << 4));
   }
   const uint8_t* b_row[2];
@@ -471,14 +485,14 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
   for (int j = 0; j < 2; ++j) {
     int n = n0 + wave * 64 + j * 32 + l32;
     if (n >= N) n = N - 1;
-    b_row[j] = codes + lay.codes_off(n) + 16 * h;
-    n_row[j] = norms + lay.norms_off(n);
+    b_row[j] = codes + lay.codes_off(n) + 16 * h + (int64_t)kb0 * lay.c_blk;
+    n_row[j] = norms + lay.norms_off(n) + (int64_t)kb0 * lay.n_blk;
   }
   uint32_t a_off[4];  // lane's row l32, chunk 4h + t, swizzled
 #pragma unroll
   for (int t = 0; t < 4; ++t) a_off[t] = (uint32_t)(l32 * kARow4 + (((uint32_t)(4 * h + t) ^ a4_swz(l32)) << 4));
 
-  const int nkt = 2 * nb;  // half-blocks, a multiple of 4
+  const int nkt = 2 * nbz;  // half-blocks of this K range, a multiple of 4
   // loads past the last half-block re-read it (in bounds, never used)
   auto ldb = [&](BSlot4<NIB>& sl, int kt) {
     kt = kt < nkt ? kt : nkt - 1;
@@ -560,7 +574,7 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
 }
 
 template <bool NIB, int TMW, bool MASK, int OM>
-static int launch_gemm4_t(const GemmArgs& a, hipStream_t st) {
+static int launch_gemm4_t(const GemmArgs& a, hipStream_t st, int ksplit = 1) {
   constexpr int BM = TMW * 32, BN = 256;
   auto kern = gemm4_kernel<NIB, TMW, MASK, OM>;
   const int entries = table_entries(NIB, a.n_levels);
@@ -579,8 +593,10 @@ static int launch_gemm4_t(const GemmArgs& a, hipStream_t st) {
   const int64_t total = (int64_t)tiles_m * tiles_n;
   if (total > INT32_MAX) return PE_ERR_DIMS;
   const uint8_t mb = NIB ? (uint8_t)((a.n_levels - 1) * 0x11) : (uint8_t)(a.n_levels - 1);
-  const int vec_ok = ((uintptr_t)a.y % 16 == 0) && ((a.ldy * (int64_t)ES) % 16 == 0);
-  kern<<<dim3((unsigned)total), dim3(256), lds, st>>>(
+  // 16-byte stores need aligned rows; with a K split, aligned slab starts too
+  const int vec_ok = ((uintptr_t)a.y % 16 == 0) && ((a.ldy * (int64_t)ES) % 16 == 0) &&
+                     (ksplit == 1 || ((int64_t)a.M * a.ldy * (int64_t)ES) % 16 == 0);
+  kern<<<dim3((unsigned)total, 1, (unsigned)ksplit), dim3(256), lds, st>>>(
       a.codes, a.norms, a.ct, a.n_levels, 0x01010101u * mb, entries,
       reinterpret_cast<const uint32_t*>(a.xp), a.y, a.bias, a.M, a.N, a.nb, a.ldy, tiles_m,
       (int)total, a.lay, vec_ok);
@@ -588,7 +604,7 @@ static int launch_gemm4_t(const GemmArgs& a, hipStream_t st) {
 }
 
 template <bool NIB, int TMW, int TNW, int WM, int WN, int OM>
-static int launch_gemm_t(const GemmArgs& a, hipStream_t st) {
+static int launch_gemm_t(const GemmArgs& a, hipStream_t st, int ksplit = 1) {
   constexpr int BM = WM * TMW * 32, BN = WN * TNW * 32;
   auto kern = gemm_kernel<NIB, TMW, TNW, WM, WN, OM>;
   const int entries = table_entries(NIB, a.n_levels);
@@ -604,7 +620,7 @@ static int launch_gemm_t(const GemmArgs& a, hipStream_t st) {
   const int64_t total = (int64_t)tiles_m * tiles_n;
   if (total > INT32_MAX) return PE_ERR_DIMS;
   const uint8_t mb = NIB ? (uint8_t)((a.n_levels - 1) * 0x11) : (uint8_t)(a.n_levels - 1);
-  kern<<<dim3((unsigned)total), dim3(WM * WN * 64), lds, st>>>(
+  kern<<<dim3((unsigned)total, 1, (unsigned)ksplit), dim3(WM * WN * 64), lds, st>>>(
       a.codes, a.norms, a.ct, a.n_levels, 0x01010101u * mb, entries,
       reinterpret_cast<const uint32_t*>(a.xp), a.y, a.bias, a.M, a.N, a.nb, a.ldy, tiles_m,
       (int)total, a.lay);
@@ -641,44 +657,107 @@ static GemmShape pick_gemm_tile(int M, int N) {
   return best;
 }
 
+static bool use_gemm4(int M, int N, int nb) {
+  const int64_t tiles4 = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
+  return (nb & 1) == 0 && tiles4 >= num_cus() && tiles4 <= 4 * (int64_t)num_cus();
+}
+
+// K split of the four-wave kernel for M >= 256 whose 128 x 256 tiles are too
+// few for one round (M = 256..512 on the 4096 x 12288 down projection: 32-64
+// tiles): groups of at least four 128-blocks (an even count each), about one
+// workgroup per CU in all. 1 = no split.
+static int gemm4_ksplit(int M, int N, int nb) {
+  if (M < 256 || (nb & 1) || use_gemm4(M, N, nb)) return 1;
+  const int64_t tiles4 = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
+  int z = (int)(num_cus() / tiles4);
+  if (z > nb / 4) z = nb / 4;
+  return z < 2 ? 1 : z;
+}
+
+// K split of the eight-wave kernel when its tiles would leave more than half
+// the CUs idle (few output tiles over a long K: M = 128 on the 4096 x 12288
+// down projection has 32): gemm_ksplit groups of at least two 128-blocks,
+// fp32 partial sums in the workspace, then the ordered reduction shared with
+// the decode path. 1 = no split (the four-wave kernel never splits).
+static int gemm_ksplit(int M, int N, int nb) {
+  if (use_gemm4(M, N, nb) || gemm4_ksplit(M, N, nb) > 1) return 1;
+  const GemmShape g = pick_gemm_tile(M, N);
+  const int bm = 32 * g.tmw, bn = 32 * g.wn;
+  const int64_t tiles = (int64_t)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+  const int cus = num_cus();
+  if (tiles * 2 > cus) return 1;
+  int z = (int)(cus / tiles);
+  if (z > nb / 2) z = nb / 2;
+  return z < 2 ? 1 : z;
+}
+
 // The four-wave kernel (128 x 256 tiles) is the faster one when its tiles fill
 // the CUs for one to four rounds (measured on M = 2048 prefill shapes: 6-18%
 // ahead); with fewer tiles the eight-wave kernel's narrower tiles spread
 // wider, and with many rounds its two waves per SIMD hide more latency.
 template <bool NIB, int OM>
-static int launch_gemm_shape(const GemmArgs& a, hipStream_t st) {
-  const int cus = num_cus();
-  const int64_t tiles4 = (int64_t)((a.M + 127) / 128) * ((a.N + 255) / 256);
-  if ((a.nb & 1) == 0 && tiles4 >= cus && tiles4 <= 4 * (int64_t)cus) {
+static int launch_gemm_eight(const GemmArgs& a, hipStream_t st, int ksplit) {
+  const GemmShape g = pick_gemm_tile(a.M, a.N);
+  switch (g.tmw * 16 + g.wn) {
+    case 8 * 16 + 8: return launch_gemm_t<NIB, 8, 1, 1, 8, OM>(a, st, ksplit);
+    case 4 * 16 + 8: return launch_gemm_t<NIB, 4, 1, 1, 8, OM>(a, st, ksplit);
+    case 2 * 16 + 8: return launch_gemm_t<NIB, 2, 1, 1, 8, OM>(a, st, ksplit);
+    case 8 * 16 + 4: return launch_gemm_t<NIB, 8, 1, 1, 4, OM>(a, st, ksplit);
+    case 4 * 16 + 4: return launch_gemm_t<NIB, 4, 1, 1, 4, OM>(a, st, ksplit);
+    default: return launch_gemm_t<NIB, 2, 1, 1, 4, OM>(a, st, ksplit);
+  }
+}
+
+template <bool NIB, int OM>
+static int launch_gemm_shape(const GemmArgs& a, hipStream_t st, void* ws, size_t ws_bytes) {
+  if (use_gemm4(a.M, a.N, a.nb)) {
     const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
     return mask ? launch_gemm4_t<NIB, 4, true, OM>(a, st) : launch_gemm4_t<NIB, 4, false, OM>(a, st);
   }
-  const GemmShape g = pick_gemm_tile(a.M, a.N);
-  switch (g.tmw * 16 + g.wn) {
-    case 8 * 16 + 8: return launch_gemm_t<NIB, 8, 1, 1, 8, OM>(a, st);
-    case 4 * 16 + 8: return launch_gemm_t<NIB, 4, 1, 1, 8, OM>(a, st);
-    case 2 * 16 + 8: return launch_gemm_t<NIB, 2, 1, 1, 8, OM>(a, st);
-    case 8 * 16 + 4: return launch_gemm_t<NIB, 8, 1, 1, 4, OM>(a, st);
-    case 4 * 16 + 4: return launch_gemm_t<NIB, 4, 1, 1, 4, OM>(a, st);
-    default: return launch_gemm_t<NIB, 2, 1, 1, 4, OM>(a, st);
+  // fp16 out (the linear entry points): split K when the tiles are few and
+  // the workspace holds the partial sums; otherwise one launch
+  const int z4 = OM == OM_F16 ? gemm4_ksplit(a.M, a.N, a.nb) : 1;
+  if (z4 > 1 && ws && aligned16(ws) && ws_bytes >= (size_t)z4 * a.M * a.N * 4) {
+    GemmArgs p = a;
+    p.y = ws;
+    p.ldy = a.N;
+    p.bias = nullptr;
+    const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
+    const int rc = mask ? launch_gemm4_t<NIB, 4, true, OM_F32>(p, st, z4)
+                        : launch_gemm4_t<NIB, 4, false, OM_F32>(p, st, z4);
+    if (rc) return rc;
+    return split_reduce(reinterpret_cast<const float*>(ws), z4, a.M, a.N, a.bias, a.y, a.ldy, st);
   }
+  const int z = OM == OM_F16 ? gemm_ksplit(a.M, a.N, a.nb) : 1;
+  if (z > 1 && ws && aligned16(ws) && ws_bytes >= (size_t)z * a.M * a.N * 4) {
+    GemmArgs p = a;
+    p.y = ws;
+    p.ldy = a.N;
+    p.bias = nullptr;
+    if (int rc = launch_gemm_eight<NIB, OM_F32>(p, st, z)) return rc;
+    return split_reduce(reinterpret_cast<const float*>(ws), z, a.M, a.N, a.bias, a.y, a.ldy, st);
+  }
+  return launch_gemm_eight<NIB, OM>(a, st, 1);
 }
 
-int gemm(bool nibble, int omode, const GemmArgs& a, hipStream_t st) {
-  if (nibble) return omode == 0 ? launch_gemm_shape<true, 0>(a, st) : launch_gemm_shape<true, 1>(a, st);
-  return omode == 0 ? launch_gemm_shape<false, 0>(a, st) : launch_gemm_shape<false, 1>(a, st);
+int gemm(bool nibble, int omode, const GemmArgs& a, hipStream_t st, void* ws, size_t ws_bytes) {
+  if (nibble) return omode == 0 ? launch_gemm_shape<true, 0>(a, st, ws, ws_bytes) : launch_gemm_shape<true, 1>(a, st, ws, ws_bytes);
+  return omode == 0 ? launch_gemm_shape<false, 0>(a, st, ws, ws_bytes) : launch_gemm_shape<false, 1>(a, st, ws, ws_bytes);
 }
 
-// Matmul on a pair-f16 x_tf, used by the linear entry points for M > 1.
+// Matmul on a pair-f16 x_tf, used by the linear entry points for M > 1: the
+// fp32 partial sums of the K split, if it applies.
 size_t mm_xtf_workspace(bool nibble, int64_t M, int N, int nb) {
-  (void)nibble; (void)M; (void)N; (void)nb;
-  return 0;
+  (void)nibble;
+  if (M <= kSmallMaxRows || M > INT32_MAX) return 0;
+  const int z4 = gemm4_ksplit((int)M, N, nb);
+  const int z = z4 > 1 ? z4 : gemm_ksplit((int)M, N, nb);
+  return z > 1 ? (size_t)z * (size_t)M * (size_t)N * 4 : 0;
 }
 
 int mm_xtf(bool nibble, bool tiled, const void* codes, const uint16_t* norms, const float* ct,
            int n_levels, const void* x_pair, int64_t M, int N, int nb, void* y, int out_mode,
            int64_t ldy, const uint16_t* bias, void* ws, size_t ws_bytes, hipStream_t st) {
-  (void)ws; (void)ws_bytes;
   if (M > INT32_MAX) return PE_ERR_DIMS;
   const WLayout lay = wlayout(nibble, tiled, nb);
   if (M <= kSmallMaxRows) {
@@ -689,7 +768,7 @@ int mm_xtf(bool nibble, bool tiled, const void* codes, const uint16_t* norms, co
   }
   GemmArgs a{reinterpret_cast<const uint8_t*>(codes), norms, ct, n_levels, x_pair, y, bias,
              (int)M, N, nb, ldy, lay};
-  return gemm(nibble, out_mode, a, st);
+  return gemm(nibble, out_mode, a, st, ws, ws_bytes);
 }
 
 }  // namespace pe

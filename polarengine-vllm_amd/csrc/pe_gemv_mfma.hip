@@ -436,6 +436,15 @@ __global__ __launch_bounds__(256) void dec_split_reduce_kernel(const float* __re
 // host launch
 // ---------------------------------------------------------------------------
 
+int split_reduce(const float* part, int G, int M, int N, const uint16_t* bias, void* y, int64_t ldy,
+                 hipStream_t st) {
+  const int64_t total = (int64_t)M * N;
+  if (total <= 0 || (total + 255) / 256 > INT32_MAX) return PE_ERR_DIMS;
+  dec_split_reduce_kernel<<<dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st>>>(
+      part, G, M, N, bias, reinterpret_cast<_Float16*>(y), ldy);
+  return launch_status();
+}
+
 // waves per workgroup: TN tiles x KS K-slices = 12 (one workgroup per CU;
 // measured better than 15-16 waves: fewer competing streams per CU); at least
 // 8 so that the table fill covers 256 entries with two per wave

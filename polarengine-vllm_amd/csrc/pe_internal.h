@@ -116,11 +116,15 @@ struct DecArgs {
   size_t ws_bytes;
 };
 bool gemv_mfma_fits(bool nibble, int M, int N, int nb, int n_levels);
+// y[m, n] = fp16(sum over g = 0.. G-1 in order of part[g][m][n]) (+ fp16 bias)
+int split_reduce(const float* part, int G, int M, int N, const uint16_t* bias, void* y, int64_t ldy,
+                 hipStream_t st);
 size_t gemv_mfma_workspace(bool nibble, int M, int N, int nb, int n_levels);
 int gemv_mfma(bool nibble, bool xraw, const DecArgs& a, hipStream_t st);
 
-// pe_gemm.hip
-int gemm(bool nibble, int omode, const GemmArgs& a, hipStream_t st);
+// pe_gemm.hip (ws: fp32 partial sums of the K split for fp16 output; may be null)
+int gemm(bool nibble, int omode, const GemmArgs& a, hipStream_t st, void* ws = nullptr,
+         size_t ws_bytes = 0);
 size_t mm_xtf_workspace(bool nibble, int64_t M, int N, int nb);
 int mm_xtf(bool nibble, bool tiled, const void* codes, const uint16_t* norms, const float* ct,
            int n_levels, const void* x_pair, int64_t M, int N, int nb, void* y, int out_mode,

@@ -444,6 +444,45 @@ def test_prefill_gemm_full_size_row_sample(m, n, k, bits):
     assert torch.isfinite(y).all()
 
 
+# Mid-size M with few output tiles: the eight-wave (M < 256) or four-wave
+# kernel splits K over workgroups (fp32 partial sums, ordered reduction with
+# the bias); odd M and N tails exercise the unaligned partial slabs
+@pytest.mark.parametrize("m,n,k,bits", [(128, 4096, 12288, 4), (96, 12288, 4096, 3),
+                                        (256, 4096, 12288, 5), (200, 700, 2048, 4),
+                                        (512, 4096, 12288, 4), (65, 64, 4096, 2),
+                                        # four-wave kernel with the K split (M >= 256)
+                                        (256, 12288, 4096, 3), (300, 4100, 8192, 4),
+                                        (257, 2050, 12288, 6)])
+def test_prefill_ksplit_row_sample(m, n, k, bits):
+    from polarengine_vllm import _lib
+    _say(f"prefill k-split m={m} n={n} k={k} bits={bits}")
+    rng = np.random.default_rng(bits + m + n)
+    codes, norms, ct = rand_layer(rng, n, k, bits)
+    x = O.seeded_normal((m, k), 1.0, 23)
+    bias = O.seeded_normal((n,), 0.1, 24)
+    dcodes, nib = dev_codes(codes, bits)
+    L = _lib.lib()
+    wsb = L.pe_linear_workspace_size(m, k, n, bits, int(nib))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+    xd, nd, cd, bd = to_dev(x), to_dev(norms), to_dev(ct), to_dev(bias)
+    outs = []
+    for _ in range(2):
+        y = torch.empty(m, n, dtype=torch.float16, device=DEV)
+        rc = L.pe_linear_forward(xd.data_ptr(), 0, m, k, k, dcodes.data_ptr(), bits, int(nib),
+                                 nd.data_ptr(), cd.data_ptr(), None, 1 << bits, bd.data_ptr(),
+                                 y.data_ptr(), n, ws.data_ptr(), wsb,
+                                 _lib.stream_ptr(torch.device(DEV)))
+        torch.cuda.synchronize()
+        _lib.check(rc, "pe_linear_forward")
+        outs.append(y)
+    assert torch.equal(outs[0], outs[1]), "k-split prefill not deterministic"
+    rows = np.sort(rng.choice(m, 24, replace=False))
+    rows[0], rows[-1] = 0, m - 1
+    want = O.linear_apply(x[rows], codes, norms, ct, k, bias)
+    got = outs[0][torch.from_numpy(rows).to(DEV)].float().cpu().numpy()
+    check_close(got, want.astype(np.float32), f"k-split prefill {m}x{n}x{k}")
+
+
 # Shapes whose 128 x 256 tile count fills the CUs for one to four rounds take
 # the four-wave prefill kernel: f16 and f32 outputs, nibble and int8 codes,
 # masked small codebooks, bias, M and N tails, both weight layouts.
