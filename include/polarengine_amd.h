@@ -129,7 +129,9 @@ int pe_polar_matmul(const void* codes, int packed, const float* x_tf, int64_t M,
  *   bias   : NULL or [out_f] in x_dtype
  *   y      : [M, out_f] in x_dtype, row stride out_f
  * Needs pe_linear_workspace_size(...) bytes of workspace (0 is valid when the
- * query returns 0).
+ * query returns 0): for M > 1 the pair-f16 x_tf, and the fp32 partial sums of
+ * a K split over workgroups (decode at M <= 64 when the activations do not fit
+ * one workgroup; prefill when the output tiles are too few for the CUs).
  */
 size_t pe_linear_workspace_size(int64_t M, int in_f, int out_f, int bits, int packed);
 int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f, int64_t ldx,
