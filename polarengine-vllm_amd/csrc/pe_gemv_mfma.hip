@@ -591,17 +591,13 @@ static int launch_dec_split(const DecArgs& a, hipStream_t st) {
   if (!a.ws || a.ws_bytes < (size_t)G * a.M * a.N * 4) return PE_ERR_WORKSPACE;
   const int xc = dec_xc(a.M, (a.nb + G - 1) / G, kDecW);
   const int mtd = dec_mtd(a.M);
-  if (mtd > 1) {  // two or four m-tiles: activation registers 4 or 8
-    if (a.ct_host) {
-      if (mtd == 2) return xc <= 4 ? launch_dec<NIB, kSplitTN, XRAW, MASK, 4, true, true, 2>(a, st, G)
-                                   : launch_dec<NIB, kSplitTN, XRAW, MASK, 8, true, true, 2>(a, st, G);
-      return xc <= 4 ? launch_dec<NIB, kSplitTN, XRAW, MASK, 4, true, true, 4>(a, st, G)
-                     : launch_dec<NIB, kSplitTN, XRAW, MASK, 8, true, true, 4>(a, st, G);
-    }
-    if (mtd == 2) return xc <= 4 ? launch_dec<NIB, kSplitTN, XRAW, MASK, 4, false, true, 2>(a, st, G)
-                                 : launch_dec<NIB, kSplitTN, XRAW, MASK, 8, false, true, 2>(a, st, G);
-    return xc <= 4 ? launch_dec<NIB, kSplitTN, XRAW, MASK, 4, false, true, 4>(a, st, G)
-                   : launch_dec<NIB, kSplitTN, XRAW, MASK, 8, false, true, 4>(a, st, G);
+  if (mtd > 1) {  // two m-tiles (kDecMaxRows = 32): activation registers 4 or 8
+    if (mtd != 2) return PE_ERR_DIMS;
+    if (a.ct_host)
+      return xc <= 4 ? launch_dec<NIB, kSplitTN, XRAW, MASK, 4, true, true, 2>(a, st, G)
+                     : launch_dec<NIB, kSplitTN, XRAW, MASK, 8, true, true, 2>(a, st, G);
+    return xc <= 4 ? launch_dec<NIB, kSplitTN, XRAW, MASK, 4, false, true, 2>(a, st, G)
+                   : launch_dec<NIB, kSplitTN, XRAW, MASK, 8, false, true, 2>(a, st, G);
   }
   if (a.ct_host) {
     if (xc <= 2) return launch_dec<NIB, kSplitTN, XRAW, MASK, 2, true, true>(a, st, G);

@@ -4,16 +4,19 @@
 //
 // Routing by M (rows of the activation):
 //   M <= 16 (when x, or one K group of it, fits in LDS beside the codebook
-//   table), or 17 <= M <= 64 when one K group fits
+//   table), or 17 <= M <= 32 when one K group fits
 //                     -> gemv_mfma: decode GEMV on 16x16x32 MFMA, FWHT fused
 //                        into its prologue (one launch per linear; with the K
 //                        split over workgroups, plus a partial-sum reduction;
-//                        M > 16 with two or four m-tiles per weight lookup);
+//                        M > 16 with two m-tiles per weight lookup);
 //   M == 1 otherwise  -> gemv1 (register-resident dot2 GEMV, LDS activations);
 //   2 <= M <= 64 else -> FWHT-128 to pair-f16 x_tf, then the small-M MFMA
-//                        kernel (16x16x32 f16, K split across waves);
-//   M >  kSmallM      -> FWHT-128 to pair-f16 x_tf, then the prefill GEMM
-//                        (32x32x16 f16 MFMA, LDS A tiles, dequantized B).
+//                        kernel (16x16x32 f16, K split across waves); at
+//                        M = 33..64 with fp16 out, the prefill GEMM instead
+//                        when its K split over workgroups applies;
+//   M > 64            -> FWHT-128 to pair-f16 x_tf, then the prefill GEMM
+//                        (32x32x16 f16 MFMA, dequantized B; K split over
+//                        workgroups when the output tiles are few).
 // The reference routes M = 1 to split-K GEMV and every M > 1 to its Triton
 // GEMM; results are the same function either way.
 

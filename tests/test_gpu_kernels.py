@@ -223,7 +223,8 @@ DECODE_CASES = [(1, 12288, 4096, 4), (1, 4096, 4096, 5), (2, 1000, 1408, 3),
                 # LDS): fp32 partials reduced by a second kernel
                 (16, 12288, 4096, 4), (16, 4096, 12288, 3), (6, 2048, 24576, 4),
                 (2, 700, 40960, 2), (10, 50, 640, 6),
-                # 17 <= M <= 64: two or four m-tiles per weight lookup, K split
+                # 17 <= M <= 32: two m-tiles per weight lookup, K split; M = 33..64:
+                # the prefill GEMM's K split or the small-M kernel
                 (17, 12288, 4096, 4), (24, 4096, 12288, 3), (32, 12288, 4096, 4),
                 (48, 1000, 2048, 5), (64, 12288, 4096, 4), (64, 4096, 12288, 4),
                 (33, 700, 4096, 2), (40, 96, 640, 8), (64, 50, 256, 4), (17, 16, 384, 3)]
