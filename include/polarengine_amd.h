@@ -120,18 +120,25 @@ int pe_polar_matmul(const void* codes, int packed, const float* x_tf, int64_t M,
  * The quantized linear forward of PolarQuantLinearMethod.apply
  * (polarengine_vllm/linear_method.py:157-222): pad -> FWHT -> quantized
  * GEMV/GEMM (fp32 accumulate) -> cast -> + bias.
- *   x      : [M, in_f] in x_dtype (PE_DTYPE_F16), row stride ldx
+ *   x      : [M, in_f] in x_dtype (PE_DTYPE_F16 or PE_DTYPE_BF16), row stride
+ *            ldx; the transformed activation enters the matrix cores as fp16
  *   codes  : runtime layout for (bits, packed); packed = PE_PACK_NIBBLE for
  *            nibble codes, | PE_LAYOUT_TILE16 for the tiled-16 layout
  *   ct_host: NULL, or a host copy of ct_scaled (n_levels floats, equal to the
  *            device values); the decode kernel then takes the codebook by
  *            value in its kernel arguments instead of reading ct_scaled
  *   bias   : NULL or [out_f] in x_dtype
- *   y      : [M, out_f] in x_dtype, row stride out_f
- * Needs pe_linear_workspace_size(...) bytes of workspace (0 is valid when the
- * query returns 0): for M > 1 the pair-f16 x_tf, and the fp32 partial sums of
- * a K split over workgroups (decode at M <= 64 when the activations do not fit
- * one workgroup; prefill when the output tiles are too few for the CUs).
+ *   y      : [M, out_f] in x_dtype, row stride out_f. The reference always
+ *            returns fp16 (linear_method.py:219); here a bf16 activation gets
+ *            a bf16 result (rounded once, then + bias, rounded again).
+ * Needs at least pe_linear_workspace_size(...) bytes of workspace (NULL is
+ * valid when the query returns 0): the pair-f16 x_tf wherever the transform
+ * is not fused into the decode kernel (M > 32, and any M whose shape exceeds
+ * the decode kernel's LDS or addressing limits, M = 1 included), and the
+ * fp32 partial sums of a K split over workgroups (decode at 2 <= M <= 32
+ * when the activations do not fit one workgroup; prefill when the output
+ * tiles are too few for the CUs). The query and the call choose the path by
+ * the same rule from the same arguments.
  */
 size_t pe_linear_workspace_size(int64_t M, int in_f, int out_f, int bits, int packed);
 int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f, int64_t ldx,
@@ -143,7 +150,8 @@ int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f, int64_t l
 /*
  * Same, starting from an already-transformed activation in the pair-f16
  * layout (the FWHTCache hit of linear_method.py:190-197, shared by Q/K/V).
- * in_f_padded = 128 * nb of x_tf; ct_host as for pe_linear_forward.
+ * in_f_padded = 128 * nb of x_tf; ct_host as for pe_linear_forward;
+ * out_dtype PE_DTYPE_F16 or PE_DTYPE_BF16 for y and bias.
  */
 size_t pe_linear_xtf_workspace_size(int64_t M, int in_f_padded, int out_f, int bits, int packed);
 int pe_linear_forward_xtf(const void* x_tf_pair, int64_t M, int in_f_padded,
@@ -234,11 +242,27 @@ int pe_moe_route(const float* logits, int64_t T, int E, int top_k, int renormali
                  int32_t* topk_ids, void* stream);
 
 /*
+ * Grouped top-k routing (vLLM's grouped_topk, which the reference reaches by
+ * passing use_grouped_topk / num_expert_group / topk_group through
+ * PolarPassthroughMoEMethod.apply, moe_method.py:74-89): scores = softmax or
+ * sigmoid of the logits; the E experts form num_expert_group contiguous groups
+ * (E % num_expert_group == 0, at most 64 groups); a group's score is its best
+ * expert score, or, with correction_bias, the sum of its two best scores +
+ * bias; the topk_group best groups (ties: lower group) are kept, top_k of
+ * their experts are taken by (biased) score (ties: lower id), and the
+ * weights are the unbiased scores, optionally renormalised. top_k must not
+ * exceed the kept experts; E, top_k limits as pe_moe_route.
+ */
+int pe_moe_route_grouped(const float* logits, int64_t T, int E, int top_k, int renormalize,
+                         int scoring, const float* correction_bias, int num_expert_group,
+                         int topk_group, float* topk_w, int32_t* topk_ids, void* stream);
+
+/*
  * Quantized SwiGLU MoE forward over resident experts (the grouped-expert
  * path). The reference forwards MoE layers to vLLM's bf16 fused MoE
  * (moe_method.py:74-92); the per-expert math is that of
  * nemotron_offload.py:203-226.
- *   x       : float16 [T, H], H % 128 == 0
+ *   x       : [T, H] in x_dtype (PE_DTYPE_F16 or PE_DTYPE_BF16), H % 128 == 0
  *   topk_w / topk_ids : routing (pe_moe_route or the caller's own)
  *   w13     : codes [E, 2I, ...] in the runtime layout for (bits13, packed13),
  *             norms float16 [E, 2I, H/128], ct13 float32 [2**bits13];
@@ -249,11 +273,11 @@ int pe_moe_route(const float* logits, int64_t T, int E, int top_k, int renormali
  *             must then be multiples of 16)
  *   w2      : codes [E, H, ...] over in_f = I padded to Ip = ceil(I/128)*128,
  *             norms float16 [E, H, Ip/128], ct2 float32 [2**bits2]
- *   out     : float16 [T, H] = sum_k topk_w[t,k] * expert_{ids[t,k]}(x_t)
+ *   out     : [T, H] in x_dtype = sum_k topk_w[t,k] * expert_{ids[t,k]}(x_t)
  * Workspace: pe_moe_workspace_size(T, top_k, E, H, I) bytes.
  */
 size_t pe_moe_workspace_size(int64_t T, int top_k, int E, int H, int I);
-int pe_moe_forward(const void* x, int64_t T, int H, int I, int E, int top_k,
+int pe_moe_forward(const void* x, int x_dtype, int64_t T, int H, int I, int E, int top_k,
                    const float* topk_w, const int32_t* topk_ids,
                    const void* w13_codes, int bits13, int packed13,
                    const uint16_t* w13_norms, const float* ct13, int n_levels13,

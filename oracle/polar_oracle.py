@@ -35,6 +35,8 @@ hadamard_domain_matmul      equals x @ dequant_weight(...).T (two routes,
                             different algebra); one-hot probe returns
                             ct_scaled[code]*norm
 linear_apply                equals the dense route; bias/half cast semantics
+dequant_matmul              equals linear_apply (a different algebra: H folded
+                            into W instead of applied to x)
 kv_centroids                golden vectors from the reference's
                             kv_cache/cache.py get_centroids (tests/golden/
                             golden_kv.npz); symmetry, monotone levels
@@ -45,6 +47,15 @@ kv_quantize / kv_dequantize golden packed codes, bf16 norms and bf16 outputs
                             fp32 near-ties of the rotation, outputs to 1 bf16
                             ulp: numpy's and torch's fp32 matmuls round
                             differently)
+moe_route_grouped           equals moe_route when every group is kept (no
+                            bias) and with one group; a plain-Python brute
+                            force (explicit loops, sorted() on tuple keys) on
+                            small cases with exact ties; vLLM itself (the
+                            reference's dependency) is absent: its published
+                            grouped_topk algorithm is restated, not run
+linear_apply bf16 output    bf16 rounding pinned by hand-computed bit patterns
+                            of f32_to_bf16_bits (RNE ties, NaN) and the fp32
+                            route rounded once (bias: twice)
 moe_forward                 parity unpinned against vLLM (the reference's MoE
                             compute lives in an absent dependency); pinned
                             against a per-token brute-force loop and the
@@ -382,28 +393,56 @@ def hadamard_domain_matmul(codes: np.ndarray, norms: np.ndarray, ct_sc: np.ndarr
     nb = kp // block_size
     x2 = np.asarray(x_tf, dtype=np.float32).reshape(-1, kp)
     vals = np.asarray(ct_sc, dtype=np.float32)[c].reshape(n, nb, block_size)
-    part = np.einsum("nbk,mbk->mnb", vals, x2.reshape(-1, nb, block_size),
-                     optimize=True)
-    return (part * np.asarray(norms, dtype=np.float32)[None, :, :]).sum(-1).astype(np.float32)
+    nrm = np.asarray(norms, dtype=np.float32)[None, :, :]
+    out = np.empty((x2.shape[0], n), dtype=np.float32)
+    # rows in chunks: the per-block partials [rows, n, nb] stay below ~128 MB
+    step = max(1, (32 << 20) // max(1, n * nb))
+    for r0 in range(0, x2.shape[0], step):
+        xr = x2[r0:r0 + step].reshape(-1, nb, block_size)
+        part = np.einsum("nbk,mbk->mnb", vals, xr, optimize=True)
+        out[r0:r0 + step] = (part * nrm).sum(-1)
+    return out
+
+
+def dequant_matmul(x: np.ndarray, w: np.ndarray, bias: Optional[np.ndarray] = None
+                   ) -> np.ndarray:
+    """The reference's dense check path: y = x @ W.T in fp32 with W from
+    :func:`dequant_weight` materialised once, then .half() and + bias
+    (polar_gemv.py:354-363 and polar_gemm.py:607-615 build W this way; the
+    fp16 cast and bias follow linear_method.py:219-221). x [M, Kp]."""
+    y = (np.asarray(x, dtype=np.float32) @ np.asarray(w, dtype=np.float32).T).astype(np.float16)
+    if bias is not None:
+        y = (y + np.asarray(bias).astype(np.float16)).astype(np.float16)
+    return y
 
 
 def linear_apply(x: np.ndarray, codes: np.ndarray, norms: np.ndarray,
                  ct_sc: np.ndarray, in_f: int, bias: Optional[np.ndarray] = None,
-                 block_size: int = BLOCK_SIZE) -> np.ndarray:
-    """Full linear forward, fp32 compute, fp16 result.
+                 block_size: int = BLOCK_SIZE, out_dtype: str = "float16") -> np.ndarray:
+    """Full linear forward, fp32 compute, 16-bit result.
 
     Reference: polarengine_vllm/linear_method.py:184-221: x.float() -> pad to
     Kp -> blockwise FWHT -> Hadamard-domain GEMV/GEMM -> .half() -> + bias.
+    out_dtype "bfloat16" casts to bf16 instead of .half() (x may then be given
+    as float32 values of bf16 activations) and adds a bf16 bias the same way;
+    the result is returned as bf16 bit patterns (uint16).
     """
     x2 = np.asarray(x, dtype=np.float32).reshape(-1, in_f)
     kp = np.asarray(codes).shape[1]
     if kp != in_f:
         x2 = np.pad(x2, ((0, 0), (0, kp - in_f)))
     y = hadamard_domain_matmul(codes, norms, ct_sc, fwht_blocks(x2, block_size), block_size)
+    shape = (*np.asarray(x).shape[:-1], -1)
+    if out_dtype == "bfloat16":
+        yb = f32_to_bf16_bits(y)
+        if bias is not None:
+            bb = bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(bias, dtype=np.float32)))
+            yb = f32_to_bf16_bits(bf16_bits_to_f32(yb) + bb)
+        return yb.reshape(shape)
     y = y.astype(np.float16)
     if bias is not None:
         y = (y + np.asarray(bias).astype(np.float16)).astype(np.float16)
-    return y.reshape(*np.asarray(x).shape[:-1], -1)
+    return y.reshape(shape)
 
 
 # ---------------------------------------------------------------------------
@@ -433,6 +472,55 @@ def moe_route(router_logits: np.ndarray, top_k: int, renormalize: bool = True,
     else:
         raise ValueError(f"unsupported scoring_func {scoring_func}")
     idx = np.argsort(-p, axis=-1, kind="stable")[:, :top_k]
+    w = np.take_along_axis(p, idx, axis=-1)
+    if renormalize:
+        w = w / w.sum(axis=-1, keepdims=True)
+    return w.astype(np.float32), idx.astype(np.int32)
+
+
+def moe_route_grouped(router_logits: np.ndarray, top_k: int, renormalize: bool,
+                      num_expert_group: int, topk_group: int, scoring_func: str = "softmax",
+                      e_score_correction_bias: Optional[np.ndarray] = None
+                      ) -> Tuple[np.ndarray, np.ndarray]:
+    """Grouped top-k routing.
+
+    The reference passes use_grouped_topk / num_expert_group / topk_group
+    straight to vLLM's fused MoE (moe_method.py:74-89); the algorithm is that
+    of vLLM's ``grouped_topk`` (fused_moe, vllm>=0.8.0 per setup.py:26; vLLM
+    is not vendored): scores = softmax|sigmoid(logits); with a correction
+    bias the ranking score is scores + bias and a group's score is the sum of
+    its two best ranking scores, else a group's score is its best score; the
+    topk_group best groups are kept; top_k experts of the kept groups by
+    ranking score; weights = the unbiased scores of those experts,
+    optionally renormalised. Ties resolve to the lower group / expert index;
+    the result is sorted by descending ranking score.
+    """
+    lg = np.asarray(router_logits, dtype=np.float32)
+    if scoring_func == "softmax":
+        z = lg - lg.max(axis=-1, keepdims=True)
+        p = np.exp(z)
+        p = p / p.sum(axis=-1, keepdims=True)
+    elif scoring_func == "sigmoid":
+        p = 1.0 / (1.0 + np.exp(-lg))
+    else:
+        raise ValueError(f"unsupported scoring_func {scoring_func}")
+    p = p.astype(np.float32)
+    t, e = p.shape
+    g = num_expert_group
+    rank_s = p if e_score_correction_bias is None else (
+        p + np.asarray(e_score_correction_bias, dtype=np.float32)).astype(np.float32)
+    grouped = rank_s.reshape(t, g, e // g)
+    if e_score_correction_bias is None:
+        gscore = grouped.max(axis=-1)
+    else:
+        top2 = np.sort(grouped, axis=-1)[..., -2:]
+        gscore = (top2[..., 1] + top2[..., 0]).astype(np.float32)
+    keep_g = np.argsort(-gscore, axis=-1, kind="stable")[:, :topk_group]
+    gmask = np.zeros((t, g), dtype=bool)
+    np.put_along_axis(gmask, keep_g, True, axis=-1)
+    emask = np.repeat(gmask, e // g, axis=-1)
+    masked = np.where(emask, rank_s, -np.inf)
+    idx = np.argsort(-masked, axis=-1, kind="stable")[:, :top_k]
     w = np.take_along_axis(p, idx, axis=-1)
     if renormalize:
         w = w / w.sum(axis=-1, keepdims=True)

@@ -41,4 +41,4 @@ extern "C" const char* pe_status_string(int status) {
   }
 }
 
-extern "C" int pe_abi_version(void) { return 1; }
+extern "C" int pe_abi_version(void) { return 2; }

@@ -68,6 +68,28 @@ __device__ __forceinline__ uint16_t f2bf_bits(float f) {
   return (uint16_t)(u >> 16);
 }
 
+// fp32 -> bf16 bits, round to nearest even in hardware (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint16_t f2bf_rne(float f) {
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+// 16-bit activation / output element: bf16 when `bf`, else fp16
+__device__ __forceinline__ float f16or_bf(uint16_t bits, bool bf) {
+  return bf ? bf2f(bits) : h2f(bits);
+}
+__device__ __forceinline__ uint16_t to16(float f, bool bf) { return bf ? f2bf_rne(f) : f2h_bits(f); }
+__device__ __forceinline__ uint32_t pack16x2(float lo, float hi, bool bf) {
+  return (uint32_t)to16(lo, bf) | ((uint32_t)to16(hi, bf) << 16);
+}
+// One output element of a linear epilogue: the fp32 result rounded to the
+// 16-bit output type, then the bias (same type) added in fp32 and rounded
+// again -- the reference's `output.half()` then `+ bias.half()`
+// (linear_method.py:219-221), in the output type of the activation.
+__device__ __forceinline__ uint16_t out16(float v, const uint16_t* bias, int64_t n, bool bf) {
+  uint16_t r = to16(v, bf);
+  if (bias) r = to16(f16or_bf(r, bf) + f16or_bf(bias[n], bf), bf);
+  return r;
+}
+
 // Raw LDS access by byte address. The kernels of this library declare no
 // static LDS, so their dynamic LDS block starts at address 0 and a table
 // address built by v_perm is used as is (no base add per lookup).
@@ -299,6 +321,10 @@ namespace pe {
 int num_cus();                         // CUs of the current device (cached)
 int launch_status();                   // PE_OK or PE_ERR_LAUNCH
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+// 16-bit activation dtype code -> bf16 flag; -1 for anything else
+inline int bf16_flag(int dtype) {
+  return dtype == PE_DTYPE_F16 ? 0 : dtype == PE_DTYPE_BF16 ? 1 : -1;
+}
 inline int table_entries(bool nibble, int n_levels) {
   // nibble: entries 0..mask where mask = (n_levels-1) * 0x11; int8: n_levels.
   return nibble ? (n_levels - 1) * 0x11 + 1 : n_levels;

@@ -31,15 +31,14 @@ namespace pe {
 
 constexpr int kAStride = 144;  // bytes per A-tile row in LDS (128 + 16 pad)
 
+// OM_F16: 16-bit output, bfloat16 when ybf (bias of the same type)
 template <int OM>
 __device__ __forceinline__ void store_out(void* y, int64_t ldy, int m, int n, float v,
-                                          const uint16_t* bias) {
+                                          const uint16_t* bias, bool ybf) {
   if constexpr (OM == 0) {
     reinterpret_cast<float*>(y)[(int64_t)m * ldy + n] = v;
   } else {
-    _Float16 h = (_Float16)v;
-    if (bias) h = (_Float16)((float)h + h2f(bias[n]));
-    reinterpret_cast<_Float16*>(y)[(int64_t)m * ldy + n] = h;
+    reinterpret_cast<uint16_t*>(y)[(int64_t)m * ldy + n] = out16(v, bias, n, ybf);
   }
 }
 
@@ -151,7 +150,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
     const float* __restrict__ ct, int n_levels, uint32_t code_mask, int tbl_entries,
     const uint32_t* __restrict__ xp, void* __restrict__ y, const uint16_t* __restrict__ bias,
-    int M, int N, int nb, int64_t ldy, int tiles_m, int tiles_total, WLayout lay) {
+    int M, int N, int nb, int64_t ldy, int tiles_m, int tiles_total, WLayout lay, int ybf) {
   constexpr int NT = WM * WN * 64;
   constexpr int BM = WM * TMW * 32;
   constexpr int BN = WN * TNW * 32;
@@ -264,7 +263,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int m = m0 + wm * TMW * 32 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-        if (m < M) store_out<OM>(y, ldy, m, n, acc[i][j][e], bias);
+        if (m < M) store_out<OM>(y, ldy, m, n, acc[i][j][e], bias, ybf != 0);
       }
     }
   }
@@ -369,7 +368,7 @@ __device__ __forceinline__ void mma_frag4(float16v (&acc)[TMW][2], const Frag4<N
 template <int TMW, int OM>
 __device__ __forceinline__ void store_tile4(const float16v (&acc)[TMW][2], void* __restrict__ y,
                                             int64_t ldy, const uint16_t* __restrict__ bias, int M,
-                                            int N, int m0, int n0, int vec_ok) {
+                                            int N, int m0, int n0, int vec_ok, bool ybf) {
   constexpr int BM = TMW * 32, BN = 256;
   constexpr int ES = OM == OM_F16 ? 2 : 4;
   constexpr uint32_t OSTR = BN * ES + 16;
@@ -389,7 +388,7 @@ __device__ __forceinline__ void store_tile4(const float16v (&acc)[TMW][2], void*
         const float v0 = acc[i][j][4 * g], v1 = acc[i][j][4 * g + 1];
         const float v2 = acc[i][j][4 * g + 2], v3 = acc[i][j][4 * g + 3];
         if constexpr (OM == OM_F16) {
-          lds_st64(addr, u32x2v{pack_h2(v0, v1), pack_h2(v2, v3)});
+          lds_st64(addr, u32x2v{pack16x2(v0, v1, ybf), pack16x2(v2, v3, ybf)});
         } else {
           lds_st128(addr, u32x4v{__builtin_bit_cast(uint32_t, v0), __builtin_bit_cast(uint32_t, v1),
                                  __builtin_bit_cast(uint32_t, v2), __builtin_bit_cast(uint32_t, v3)});
@@ -407,11 +406,12 @@ __device__ __forceinline__ void store_tile4(const float16v (&acc)[TMW][2], void*
       if (bias) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const half2v x = as_h2(v[e]);
+          const float x0 = f16or_bf((uint16_t)(v[e] & 0xffff), ybf);
+          const float x1 = f16or_bf((uint16_t)(v[e] >> 16), ybf);
           const int nn = n + 2 * e;
-          const float b0 = nn < N ? h2f(bias[nn]) : 0.f;
-          const float b1 = nn + 1 < N ? h2f(bias[nn + 1]) : 0.f;
-          v[e] = pack_h2((float)x[0] + b0, (float)x[1] + b1);
+          const float b0 = nn < N ? f16or_bf(bias[nn], ybf) : 0.f;
+          const float b1 = nn + 1 < N ? f16or_bf(bias[nn + 1], ybf) : 0.f;
+          v[e] = pack16x2(x0 + b0, x1 + b1, ybf);
         }
       }
     }
@@ -435,7 +435,8 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
     const float* __restrict__ ct, int n_levels, uint32_t code_mask, int tbl_entries,
     const uint32_t* __restrict__ xp, void* __restrict__ y, const uint16_t* __restrict__ bias,
-    int M, int N, int nb, int64_t ldy, int tiles_m, int tiles_total, WLayout lay, int vec_ok) {
+    int M, int N, int nb, int64_t ldy, int tiles_m, int tiles_total, WLayout lay, int vec_ok,
+    int ybf) {
   constexpr int NT = 256;
   constexpr int BM = TMW * 32;
   constexpr int BN = 256;
@@ -570,7 +571,7 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
     half_step(std::integral_constant<int, 3>{}, kt + 3);
   }
 
-  store_tile4<TMW, OM>(acc, y, ldy, bias, M, N, m0, n0, vec_ok);
+  store_tile4<TMW, OM>(acc, y, ldy, bias, M, N, m0, n0, vec_ok, ybf != 0);
 }
 
 template <bool NIB, int TMW, bool MASK, int OM>
@@ -599,7 +600,7 @@ static int launch_gemm4_t(const GemmArgs& a, hipStream_t st, int ksplit = 1) {
   kern<<<dim3((unsigned)total, 1, (unsigned)ksplit), dim3(256), lds, st>>>(
       a.codes, a.norms, a.ct, a.n_levels, 0x01010101u * mb, entries,
       reinterpret_cast<const uint32_t*>(a.xp), a.y, a.bias, a.M, a.N, a.nb, a.ldy, tiles_m,
-      (int)total, a.lay, vec_ok);
+      (int)total, a.lay, vec_ok, a.ybf);
   return launch_status();
 }
 
@@ -623,7 +624,7 @@ static int launch_gemm_t(const GemmArgs& a, hipStream_t st, int ksplit = 1) {
   kern<<<dim3((unsigned)total, 1, (unsigned)ksplit), dim3(WM * WN * 64), lds, st>>>(
       a.codes, a.norms, a.ct, a.n_levels, 0x01010101u * mb, entries,
       reinterpret_cast<const uint32_t*>(a.xp), a.y, a.bias, a.M, a.N, a.nb, a.ldy, tiles_m,
-      (int)total, a.lay);
+      (int)total, a.lay, a.ybf);
   return launch_status();
 }
 
@@ -726,7 +727,8 @@ static int launch_gemm_shape(const GemmArgs& a, hipStream_t st, void* ws, size_t
     const int rc = mask ? launch_gemm4_t<NIB, 4, true, OM_F32>(p, st, z4)
                         : launch_gemm4_t<NIB, 4, false, OM_F32>(p, st, z4);
     if (rc) return rc;
-    return split_reduce(reinterpret_cast<const float*>(ws), z4, a.M, a.N, a.bias, a.y, a.ldy, st);
+    return split_reduce(reinterpret_cast<const float*>(ws), z4, a.M, a.N, a.bias, a.y, a.ldy, st,
+                        a.ybf != 0);
   }
   const int z = OM == OM_F16 ? gemm_ksplit(a.M, a.N, a.nb) : 1;
   if (z > 1 && ws && aligned16(ws) && ws_bytes >= (size_t)z * a.M * a.N * 4) {
@@ -735,7 +737,8 @@ static int launch_gemm_shape(const GemmArgs& a, hipStream_t st, void* ws, size_t
     p.ldy = a.N;
     p.bias = nullptr;
     if (int rc = launch_gemm_eight<NIB, OM_F32>(p, st, z)) return rc;
-    return split_reduce(reinterpret_cast<const float*>(ws), z, a.M, a.N, a.bias, a.y, a.ldy, st);
+    return split_reduce(reinterpret_cast<const float*>(ws), z, a.M, a.N, a.bias, a.y, a.ldy, st,
+                        a.ybf != 0);
   }
   return launch_gemm_eight<NIB, OM>(a, st, 1);
 }
@@ -765,17 +768,18 @@ size_t mm_xtf_workspace(bool nibble, int64_t M, int N, int nb) {
 
 int mm_xtf(bool nibble, bool tiled, const void* codes, const uint16_t* norms, const float* ct,
            int n_levels, const void* x_pair, int64_t M, int N, int nb, void* y, int out_mode,
-           int64_t ldy, const uint16_t* bias, void* ws, size_t ws_bytes, hipStream_t st) {
+           int64_t ldy, const uint16_t* bias, void* ws, size_t ws_bytes, hipStream_t st,
+           bool ybf) {
   if (M > INT32_MAX) return PE_ERR_DIMS;
   const WLayout lay = wlayout(nibble, tiled, nb);
   if (mm_small(M, N, nb, out_mode)) {
     SmallArgs s{reinterpret_cast<const uint8_t*>(codes), norms, ct, n_levels,
                 reinterpret_cast<const uint32_t*>(x_pair), nullptr, nullptr, 0, 0, y, ldy, bias,
-                (int)M, N, nb, lay};
+                (int)M, N, nb, lay, ybf ? 1 : 0};
     return gemm_small(nibble, out_mode == OM_F32 ? SE_F32 : SE_F16, s, 1, st);
   }
   GemmArgs a{reinterpret_cast<const uint8_t*>(codes), norms, ct, n_levels, x_pair, y, bias,
-             (int)M, N, nb, ldy, lay};
+             (int)M, N, nb, ldy, lay, ybf ? 1 : 0};
   return gemm(nibble, out_mode, a, st, ws, ws_bytes);
 }
 

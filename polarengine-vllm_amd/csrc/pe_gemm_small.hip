@@ -244,9 +244,7 @@ __global__ __launch_bounds__(kSmallThreads) void gemm_small_kernel(
       if constexpr (EP == SE_F32) {
         reinterpret_cast<float*>(a.y)[row * a.ldy + n] = s;
       } else if constexpr (EP == SE_F16) {
-        _Float16 hv = (_Float16)s;
-        if (a.bias) hv = (_Float16)((float)hv + h2f(a.bias[n]));
-        reinterpret_cast<_Float16*>(a.y)[row * a.ldy + n] = hv;
+        reinterpret_cast<uint16_t*>(a.y)[row * a.ldy + n] = out16(s, a.bias, n, a.ybf != 0);
       } else {
         const float act = s / (1.f + __expf(-s)) * u;
         reinterpret_cast<_Float16*>(a.y)[row * a.ldy + n] = (_Float16)act;

@@ -120,7 +120,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv1_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
     const float* __restrict__ ct, int n_levels, uint32_t code_mask, int tbl_entries,
     const void* __restrict__ x, void* __restrict__ y, const uint16_t* __restrict__ bias,
-    int N, int nb) {
+    int N, int nb, int io) {
+  const bool xbf = (io & 1) != 0, ybf = (io & 2) != 0;  // raw x / y and bias are bfloat16
   extern __shared__ uint4 smem4[];
   char* smem = reinterpret_cast<char*>(smem4);
   char* xs = smem + tbl_entries * 256;  // the table occupies [0, tbl_entries * 256)
@@ -173,8 +174,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv1_kernel(
         if constexpr (XM == XM_RAW_F16) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            v[2 * i] = h2f((uint16_t)(xraw[0][i] & 0xffff));
-            v[2 * i + 1] = h2f((uint16_t)(xraw[0][i] >> 16));
+            v[2 * i] = f16or_bf((uint16_t)(xraw[0][i] & 0xffff), xbf);
+            v[2 * i + 1] = f16or_bf((uint16_t)(xraw[0][i] >> 16), xbf);
           }
         } else {
 #pragma unroll
@@ -184,7 +185,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv1_kernel(
           }
         }
       } else if constexpr (XM == XM_RAW_F16) {
-        load8<PE_DTYPE_F16>(reinterpret_cast<const uint16_t*>(x) + b * kBlock + q * 8, v);
+        if (xbf) load8<PE_DTYPE_BF16>(reinterpret_cast<const uint16_t*>(x) + b * kBlock + q * 8, v);
+        else load8<PE_DTYPE_F16>(reinterpret_cast<const uint16_t*>(x) + b * kBlock + q * 8, v);
       } else {
         load8<PE_DTYPE_F32>(reinterpret_cast<const float*>(x) + b * kBlock + q * 8, v);
       }
@@ -280,10 +282,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv1_kernel(
         if constexpr (OM == OM_F32) {
           reinterpret_cast<float*>(y)[n] = r;
         } else {
-          // reference order: fp32 result -> .half() -> + bias.half() (fp16 add)
-          _Float16 h = (_Float16)r;
-          if (bias) h = (_Float16)((float)h + h2f(bias[n]));
-          reinterpret_cast<_Float16*>(y)[n] = h;
+          // reference order: fp32 result -> .half() -> + bias.half() (16-bit add)
+          reinterpret_cast<uint16_t*>(y)[n] = out16(r, bias, n, ybf);
         }
       }
     }
@@ -315,7 +315,8 @@ static int launch_gemv1_s(const Gemv1Args& a, hipStream_t st) {
   const uint8_t mb = NIB ? (uint8_t)((a.n_levels - 1) * 0x11) : (uint8_t)(a.n_levels - 1);
   const uint32_t mask = 0x01010101u * mb;
   kern<<<dim3(grid), dim3(kGemvThreads), lds, st>>>(a.codes, a.norms, a.ct, a.n_levels, mask,
-                                                   entries, a.x, a.y, a.bias, a.N, a.nb);
+                                                   entries, a.x, a.y, a.bias, a.N, a.nb,
+                                                   (a.xbf ? 1 : 0) | (a.ybf ? 2 : 0));
   return launch_status();
 }
 

@@ -184,8 +184,9 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
     const float* __restrict__ ct, int n_levels, uint32_t code_mask,
     const void* __restrict__ x, int64_t ldx, void* __restrict__ y, int64_t ldy,
     const uint16_t* __restrict__ bias, int M, int N, int nb, uint32_t xs_addr, WLayout lay,
-    DecCtArg<NIB> ctv) {
+    DecCtArg<NIB> ctv, int io) {
   constexpr int NW = TN * KS;
+  const bool xbf = (io & 1) != 0, ybf = (io & 2) != 0;  // raw x / y and bias are bfloat16
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar loads, branches
@@ -285,10 +286,18 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
         if constexpr (XRAW) {
           const int q = l16;
           float v[8];
+          if (xbf) {  // uniform
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            v[2 * k] = h2f((uint16_t)(xr[i][k] & 0xffff));
-            v[2 * k + 1] = h2f((uint16_t)(xr[i][k] >> 16));
+            for (int k = 0; k < 4; ++k) {
+              v[2 * k] = bf2f((uint16_t)(xr[i][k] & 0xffff));
+              v[2 * k + 1] = bf2f((uint16_t)(xr[i][k] >> 16));
+            }
+          } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              v[2 * k] = h2f((uint16_t)(xr[i][k] & 0xffff));
+              v[2 * k + 1] = h2f((uint16_t)(xr[i][k] >> 16));
+            }
           }
           fwht128_group16(v, q);
           float o[8];
@@ -397,9 +406,7 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
     if constexpr (SPLIT) {
       reinterpret_cast<float*>(y)[((int64_t)blockIdx.y * M + m) * N + n] = s;
     } else {
-      _Float16 hv = (_Float16)s;
-      if (bias) hv = (_Float16)((float)hv + h2f(bias[n]));
-      reinterpret_cast<_Float16*>(y)[(int64_t)m * ldy + n] = hv;
+      reinterpret_cast<uint16_t*>(y)[(int64_t)m * ldy + n] = out16(s, bias, n, ybf);
     }
   }
 }
@@ -409,8 +416,8 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
 __global__ __launch_bounds__(256) void dec_split_reduce_kernel(const float* __restrict__ part,
                                                                int G, int M, int N,
                                                                const uint16_t* __restrict__ bias,
-                                                               _Float16* __restrict__ y,
-                                                               int64_t ldy) {
+                                                               uint16_t* __restrict__ y,
+                                                               int64_t ldy, int ybf) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (int64_t)M * N) return;
   const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
@@ -427,9 +434,7 @@ __global__ __launch_bounds__(256) void dec_split_reduce_kernel(const float* __re
     s += v3;
   }
   for (; g < G; ++g) s += p[g * slab];
-  _Float16 hv = (_Float16)s;
-  if (bias) hv = (_Float16)((float)hv + h2f(bias[n]));
-  y[(int64_t)m * ldy + n] = hv;
+  y[(int64_t)m * ldy + n] = out16(s, bias, n, ybf != 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -437,11 +442,11 @@ __global__ __launch_bounds__(256) void dec_split_reduce_kernel(const float* __re
 // ---------------------------------------------------------------------------
 
 int split_reduce(const float* part, int G, int M, int N, const uint16_t* bias, void* y, int64_t ldy,
-                 hipStream_t st) {
+                 hipStream_t st, bool ybf) {
   const int64_t total = (int64_t)M * N;
   if (total <= 0 || (total + 255) / 256 > INT32_MAX) return PE_ERR_DIMS;
   dec_split_reduce_kernel<<<dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st>>>(
-      part, G, M, N, bias, reinterpret_cast<_Float16*>(y), ldy);
+      part, G, M, N, bias, reinterpret_cast<uint16_t*>(y), ldy, (int)ybf);
   return launch_status();
 }
 
@@ -497,13 +502,13 @@ static int launch_dec(const DecArgs& a, hipStream_t st, int groups = 1) {
   }
   kern<<<dim3(tiles, groups), dim3(NW * 64), lds, st>>>(
       a.codes, a.norms, a.ct, a.n_levels, 0x01010101u * mb, a.x, a.ldx, SPLIT ? a.ws : a.y, a.ldy,
-      a.bias, a.M, a.N, a.nb, xs_addr, a.lay, ctv);
+      a.bias, a.M, a.N, a.nb, xs_addr, a.lay, ctv, (a.xbf ? 1 : 0) | (a.ybf ? 2 : 0));
   if constexpr (SPLIT) {
     if (int rc = launch_status()) return rc;
     const int64_t total = (int64_t)a.M * a.N;
     dec_split_reduce_kernel<<<dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st>>>(
         reinterpret_cast<const float*>(a.ws), groups, a.M, a.N, a.bias,
-        reinterpret_cast<_Float16*>(a.y), a.ldy);
+        reinterpret_cast<uint16_t*>(a.y), a.ldy, a.ybf);
   }
   return launch_status();
 }

@@ -45,6 +45,8 @@ struct Gemv1Args {
   const uint16_t* bias;
   int N;
   int nb;
+  int xbf = 0;  // XM_RAW_F16 input is bfloat16
+  int ybf = 0;  // OM_F16 output (and bias) is bfloat16
 };
 
 struct GemmArgs {
@@ -58,6 +60,7 @@ struct GemmArgs {
   int M, N, nb;
   int64_t ldy;
   WLayout lay;
+  int ybf = 0;  // 16-bit output (and bias) is bfloat16
 };
 
 // pe_gemv.hip
@@ -87,6 +90,7 @@ struct SmallArgs {
   int N;                     // output columns (SwiGLU: I; the weights hold 2I rows)
   int nb;
   WLayout lay;               // per-expert layout (row-major for the MoE path)
+  int ybf = 0;               // SE_F16 output (and bias) is bfloat16
 };
 
 // pe_gemm_small.hip: M <= kSmallMaxRows per pass is cheapest (larger M loops)
@@ -115,11 +119,13 @@ struct DecArgs {
   const float* ct_host;  // nullable host copy of ct (n_levels floats): codebook by value
   void* ws;              // fp32 partial sums of the K-split path (gemv_mfma_workspace bytes)
   size_t ws_bytes;
+  int xbf = 0;           // raw x is bfloat16 (else fp16)
+  int ybf = 0;           // y and bias are bfloat16 (else fp16)
 };
 bool gemv_mfma_fits(bool nibble, int M, int N, int nb, int n_levels);
 // y[m, n] = fp16(sum over g = 0.. G-1 in order of part[g][m][n]) (+ fp16 bias)
 int split_reduce(const float* part, int G, int M, int N, const uint16_t* bias, void* y, int64_t ldy,
-                 hipStream_t st);
+                 hipStream_t st, bool ybf = false);
 size_t gemv_mfma_workspace(bool nibble, int M, int N, int nb, int n_levels);
 int gemv_mfma(bool nibble, bool xraw, const DecArgs& a, hipStream_t st);
 
@@ -129,7 +135,8 @@ int gemm(bool nibble, int omode, const GemmArgs& a, hipStream_t st, void* ws = n
 size_t mm_xtf_workspace(bool nibble, int64_t M, int N, int nb);
 int mm_xtf(bool nibble, bool tiled, const void* codes, const uint16_t* norms, const float* ct,
            int n_levels, const void* x_pair, int64_t M, int N, int nb, void* y, int out_mode,
-           int64_t ldy, const uint16_t* bias, void* ws, size_t ws_bytes, hipStream_t st);
+           int64_t ldy, const uint16_t* bias, void* ws, size_t ws_bytes, hipStream_t st,
+           bool ybf = false);
 
 // pe_fwht.hip
 int fwht128(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t ldx, void* y,

@@ -36,34 +36,51 @@ static int check_format(int bits, int packed, int n_levels, bool* nibble, bool* 
 }
 
 
+// The path one call of the linear forward takes, and the workspace it needs.
+// Both the size queries and the entry points use this, so a query can never
+// disagree with the path the call runs.
+enum LinearRoute {
+  LR_DECODE = 0,  // gemv_mfma: FWHT fused (raw x) or pair-f16 x_tf; partial sums when K-split
+  LR_GEMV1 = 1,   // M = 1, row-major weights, K within the gemv1 LDS budget (raw x only)
+  LR_MM = 2       // [FWHT-128 into the workspace], then the small-M / prefill matmul
+};
+struct LinearPlan {
+  int route;
+  size_t xtf_bytes;  // pair-f16 x_tf at the workspace start (raw-x MM route only)
+  size_t ws_bytes;   // total workspace
+};
+
+static LinearPlan plan_linear(bool raw_x, int64_t M, int kp, int out_f, int bits, int packed) {
+  const bool nib = (packed & PE_PACK_NIBBLE) != 0 && bits <= 4;
+  const bool tiled = (packed & PE_LAYOUT_TILE16) != 0;
+  const int nb = kp / kBlock, n_levels = 1 << bits;
+  if (M >= 1 && M <= kDecMaxRows && gemv_mfma_fits(nib, (int)M, out_f, nb, n_levels))
+    return LinearPlan{LR_DECODE, 0,
+                      round_up(gemv_mfma_workspace(nib, (int)M, out_f, nb, n_levels), 256)};
+  if (raw_x && M == 1 && !tiled && kp <= gemv1_max_kp(nib)) return LinearPlan{LR_GEMV1, 0, 0};
+  const size_t xtf = raw_x ? round_up((size_t)M * kp * 2, 256) : 0;
+  return LinearPlan{LR_MM, xtf, xtf + round_up(mm_xtf_workspace(nib, M, out_f, nb), 256)};
+}
+
+static bool plan_args_ok(int64_t M, int kp, int out_f, int bits) {
+  return M >= 1 && kp > 0 && kp % kBlock == 0 && out_f > 0 && bits >= 2 && bits <= 8;
+}
+
 }  // namespace pe
 
 using namespace pe;
 
-// fp32 partial sums of the K-split decode path (M <= 64), 0 otherwise
-static size_t decode_workspace(int64_t M, int kp, int out_f, int bits, int packed) {
-  if (M < 1 || M > kDecMaxRows || bits < 2 || bits > 8) return 0;
-  const bool nib = (packed & PE_PACK_NIBBLE) != 0 && bits <= 4;
-  return round_up(gemv_mfma_workspace(nib, (int)M, out_f, kp / kBlock, 1 << bits), 256);
-}
-
 extern "C" size_t pe_linear_xtf_workspace_size(int64_t M, int in_f_padded, int out_f, int bits,
                                                int packed) {
-  if (M <= 1 || in_f_padded <= 0 || out_f <= 0) return 0;
-  const size_t mm = mm_xtf_workspace((packed & PE_PACK_NIBBLE) != 0 && bits <= 4, M, out_f,
-                                     in_f_padded / kBlock);
-  const size_t dec = decode_workspace(M, in_f_padded, out_f, bits, packed);
-  return mm > dec ? mm : dec;
+  if (!plan_args_ok(M, in_f_padded, out_f, bits)) return 0;
+  return plan_linear(false, M, in_f_padded, out_f, bits, packed).ws_bytes;
 }
 
 extern "C" size_t pe_linear_workspace_size(int64_t M, int in_f, int out_f, int bits, int packed) {
-  if (M <= 1 || in_f <= 0 || out_f <= 0) return 0;
+  if (in_f <= 0) return 0;
   const int kp = (in_f + kBlock - 1) / kBlock * kBlock;
-  // pair-f16 x_tf, then whatever the matmul needs; or the decode path's partials
-  const size_t mm = round_up((size_t)M * kp * 2, 256) +
-                    pe_linear_xtf_workspace_size(M, kp, out_f, bits, packed);
-  const size_t dec = decode_workspace(M, kp, out_f, bits, packed);
-  return mm > dec ? mm : dec;
+  if (!plan_args_ok(M, kp, out_f, bits)) return 0;
+  return plan_linear(true, M, kp, out_f, bits, packed).ws_bytes;
 }
 
 extern "C" int pe_linear_forward_xtf(const void* x_tf_pair, int64_t M, int in_f_padded,
@@ -75,22 +92,26 @@ extern "C" int pe_linear_forward_xtf(const void* x_tf_pair, int64_t M, int in_f_
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (!x_tf_pair || !codes || !norms_f16 || !ct_scaled || !y) return PE_ERR_NULL;
   if (M < 0 || out_f <= 0 || in_f_padded <= 0 || in_f_padded % kBlock) return PE_ERR_DIMS;
-  if (out_dtype != PE_DTYPE_F16) return PE_ERR_DTYPE;
+  const int ybf = bf16_flag(out_dtype);
+  if (ybf < 0) return PE_ERR_DTYPE;
   bool nib = false, tiled = false;
   if (int rc = check_format(bits, packed, n_levels, &nib, &tiled)) return rc;
   if (!aligned16(x_tf_pair) || !aligned16(codes)) return PE_ERR_ALIGN;
   if (M == 0) return PE_OK;
   const int nb = in_f_padded / kBlock;
-  if (M <= kDecMaxRows && gemv_mfma_fits(nib, (int)M, out_f, nb, n_levels)) {
-    if (workspace && !aligned16(workspace)) return PE_ERR_ALIGN;
+  const LinearPlan plan = plan_linear(false, M, in_f_padded, out_f, bits, packed);
+  if (plan.ws_bytes && (!workspace || workspace_bytes < plan.ws_bytes)) return PE_ERR_WORKSPACE;
+  if (workspace && !aligned16(workspace)) return PE_ERR_ALIGN;
+  if (plan.route == LR_DECODE) {
     DecArgs a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels,
               x_tf_pair, (int64_t)in_f_padded, y, out_f, reinterpret_cast<const uint16_t*>(bias),
-              (int)M, out_f, nb, wlayout(nib, tiled, nb), ct_host, workspace, workspace_bytes};
+              (int)M, out_f, nb, wlayout(nib, tiled, nb), ct_host, workspace, workspace_bytes,
+              0, ybf};
     return gemv_mfma(nib, false, a, st);
   }
   return mm_xtf(nib, tiled, codes, norms_f16, ct_scaled, n_levels, x_tf_pair, M, out_f, nb, y,
                 OM_F16, out_f, reinterpret_cast<const uint16_t*>(bias), workspace,
-                workspace_bytes, st);
+                workspace_bytes, st, ybf != 0);
 }
 
 extern "C" int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f, int64_t ldx,
@@ -102,7 +123,9 @@ extern "C" int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (!x || !codes || !norms_f16 || !ct_scaled || !y) return PE_ERR_NULL;
   if (M < 0 || in_f <= 0 || out_f <= 0 || ldx < in_f) return PE_ERR_DIMS;
-  if (x_dtype != PE_DTYPE_F16) return PE_ERR_DTYPE;
+  // x, bias and y share one 16-bit dtype (fp16 or bf16)
+  const int xbf = bf16_flag(x_dtype);
+  if (xbf < 0) return PE_ERR_DTYPE;
   // The kernels read 128-wide blocks of x: in_f must already be a multiple of
   // 128 (the Python layer pads otherwise, as linear_method.py:194-195 does).
   if (in_f % kBlock) return PE_ERR_DIMS;
@@ -111,32 +134,33 @@ extern "C" int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f
   if (!aligned16(x) || !aligned16(codes) || (ldx * 2) % 16) return PE_ERR_ALIGN;
   if (M == 0) return PE_OK;
   const int nb = in_f / kBlock;
-  if (M <= kDecMaxRows && gemv_mfma_fits(nib, (int)M, out_f, nb, n_levels)) {
-    if (workspace && !aligned16(workspace)) return PE_ERR_ALIGN;
+  const LinearPlan plan = plan_linear(true, M, in_f, out_f, bits, packed);
+  if (plan.ws_bytes && (!workspace || workspace_bytes < plan.ws_bytes)) return PE_ERR_WORKSPACE;
+  if (workspace && !aligned16(workspace)) return PE_ERR_ALIGN;
+  const uint16_t* b16 = reinterpret_cast<const uint16_t*>(bias);
+  if (plan.route == LR_DECODE) {
     DecArgs a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels, x, ldx, y,
-              out_f, reinterpret_cast<const uint16_t*>(bias), (int)M, out_f, nb,
-              wlayout(nib, tiled, nb), ct_host, workspace, workspace_bytes};
+              out_f, b16, (int)M, out_f, nb, wlayout(nib, tiled, nb), ct_host, workspace,
+              workspace_bytes, xbf, xbf};
     return gemv_mfma(nib, true, a, st);
   }
-  if (M == 1 && !tiled && in_f <= gemv1_max_kp(nib)) {
+  if (plan.route == LR_GEMV1) {
     Gemv1Args a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels, x, y,
-                reinterpret_cast<const uint16_t*>(bias), out_f, nb};
+                b16, out_f, nb, xbf, xbf};
     return gemv1(nib, XM_RAW_F16, OM_F16, a, st);
   }
-  const size_t need = pe_linear_workspace_size(M, in_f, out_f, bits, packed);
-  if (!workspace || workspace_bytes < need) return PE_ERR_WORKSPACE;
-  if (!aligned16(workspace)) return PE_ERR_ALIGN;
   char* ws = reinterpret_cast<char*>(workspace);
-  const size_t xtf_bytes = round_up((size_t)M * in_f * 2, 256);
   if (int rc = fwht128(x, x_dtype, M, in_f, ldx, ws, PE_XTF_PAIR_F16, st)) return rc;
   return mm_xtf(nib, tiled, codes, norms_f16, ct_scaled, n_levels, ws, M, out_f, nb, y, OM_F16,
-                out_f, reinterpret_cast<const uint16_t*>(bias), ws + xtf_bytes,
-                workspace_bytes - xtf_bytes, st);
+                out_f, b16, ws + plan.xtf_bytes, workspace_bytes - plan.xtf_bytes, st, xbf != 0);
 }
 
+// Workspace of pe_polar_matmul: the fp32 x_tf repacked to pair f16, except at
+// M = 1 when the GEMV takes x_tf directly (K within its LDS budget for either
+// code format: int8 is the smaller bound).
 extern "C" size_t pe_polar_matmul_workspace_size(int64_t M, int in_f_padded) {
-  if (M <= 1 || in_f_padded <= 0) return 0;
-  // the already-transformed fp32 x_tf repacked to pair f16
+  if (M <= 0 || in_f_padded <= 0) return 0;
+  if (M == 1 && in_f_padded <= gemv1_max_kp(false)) return 0;
   return round_up((size_t)M * in_f_padded * 2, 256);
 }
 

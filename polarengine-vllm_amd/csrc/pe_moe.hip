@@ -31,8 +31,17 @@ namespace pe {
 // equal scores rank the lower id first. The keys go to LDS; each lane counts
 // the keys above its own (its rank), and ranks 0..top_k-1 are the selection
 // in descending order, the order of the reference's repeated arg-max / topk.
+//
+// Grouped top-k (n_group > 0; the use_grouped_topk / num_expert_group /
+// topk_group arguments moe_method.py:74-78 passes on to vLLM's fused MoE,
+// whose grouped_topk is restated here): the E experts form n_group
+// contiguous groups; a group's score is its best expert score, or with a
+// correction bias the sum of its two best biased scores; the topk_group best
+// groups (ties: lower group) stay, every other expert is masked, and top_k is
+// taken over the rest by biased score. The weights are the unbiased scores.
 // ---------------------------------------------------------------------------
 constexpr int kRouteWaves = 4;
+constexpr int kRouteMaxGroups = 64;
 
 __device__ __forceinline__ uint64_t route_key(float s, int e) {
   const uint32_t b = __builtin_bit_cast(uint32_t, s + 0.f);  // -0 -> +0
@@ -42,10 +51,14 @@ __device__ __forceinline__ uint64_t route_key(float s, int e) {
 
 __global__ __launch_bounds__(64 * kRouteWaves) void moe_route_kernel(
     const float* __restrict__ logits, int64_t T, int E, int top_k, int renormalize, int scoring,
-    const float* __restrict__ bias, float* __restrict__ topk_w, int32_t* __restrict__ topk_ids) {
+    const float* __restrict__ bias, float* __restrict__ topk_w, int32_t* __restrict__ topk_ids,
+    int n_group, int topk_group) {
   __shared__ uint64_t keys[kRouteWaves][256];
   __shared__ float sel_w[kRouteWaves][16];
   __shared__ int sel_e[kRouteWaves][16];
+  __shared__ float gsc[kRouteWaves][256];            // grouped: biased expert scores
+  __shared__ float grp[kRouteWaves][kRouteMaxGroups];  // grouped: group scores
+  __shared__ int gkeep[kRouteWaves][kRouteMaxGroups];  // grouped: group selected
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t t = (int64_t)blockIdx.x * kRouteWaves + wave;
   const bool live = t < T;
@@ -57,7 +70,7 @@ __global__ __launch_bounds__(64 * kRouteWaves) void moe_route_kernel(
     float l = -INFINITY;
     if (e < E) {
       l = logits[tr * E + e];
-      if (bias) l += bias[e];
+      if (bias && n_group == 0) l += bias[e];  // ungrouped: bias on the logits
     }
     v[i] = l;
   }
@@ -79,12 +92,63 @@ __global__ __launch_bounds__(64 * kRouteWaves) void moe_route_kernel(
     for (int i = 0; i < 4; ++i) v[i] = (lane + 64 * i) < E ? 1.f / (1.f + expf(-v[i])) : 0.f;
   }
   const int Ep = (E + 1) & ~1;  // keys read in pairs; a padding key is 0, below every real key
-  uint64_t mine[4];
+  // ranking score of each expert: the score, or (grouped, with a bias) the
+  // biased score; masked experts (grouped: outside the kept groups) get the
+  // padding key 0 and rank below every live one
+  float rs[4];
+  bool live_e[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = lane + 64 * i;
     if (v[i] != v[i]) v[i] = -1.f;  // NaN scores rank last
-    mine[i] = e < E ? route_key(v[i], e) : 0;
+    rs[i] = v[i];
+    if (n_group > 0 && bias && e < E) rs[i] = v[i] + bias[e];
+    if (rs[i] != rs[i]) rs[i] = -1.f;
+    live_e[i] = e < E;
+  }
+  if (n_group > 0) {  // uniform
+    const int epg = E / n_group;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E) gsc[wave][e] = rs[i];
+    }
+    __syncthreads();
+    if (lane < n_group) {
+      float m1 = -INFINITY, m2 = -INFINITY;  // two best of the group, duplicates kept
+      for (int j = 0; j < epg; ++j) {
+        const float s = gsc[wave][lane * epg + j];
+        if (s > m1) {
+          m2 = m1;
+          m1 = s;
+        } else if (s > m2) {
+          m2 = s;
+        }
+      }
+      grp[wave][lane] = bias ? m1 + m2 : m1;
+    }
+    __syncthreads();
+    if (lane < n_group) {
+      const float mine_g = grp[wave][lane];
+      int r = 0;
+      for (int h = 0; h < n_group; ++h) {
+        const float o = grp[wave][h];
+        r += (o > mine_g || (o == mine_g && h < lane)) ? 1 : 0;
+      }
+      gkeep[wave][lane] = r < topk_group;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E) live_e[i] = gkeep[wave][e / epg] != 0;
+    }
+  }
+  uint64_t mine[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + 64 * i;
+    mine[i] = live_e[i] ? route_key(rs[i], e) : 0;
     if (e < Ep) keys[wave][e] = mine[i];
   }
   __syncthreads();
@@ -102,8 +166,8 @@ __global__ __launch_bounds__(64 * kRouteWaves) void moe_route_kernel(
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = lane + 64 * i;
-    if (e < E && rank[i] < top_k) {
-      sel_w[wave][rank[i]] = v[i];
+    if (live_e[i] && rank[i] < top_k) {
+      sel_w[wave][rank[i]] = v[i];  // the unbiased score (grouped) or the score
       sel_e[wave][rank[i]] = e;
     }
   }
@@ -163,7 +227,7 @@ __device__ void moe_align_block(const int32_t* __restrict__ topk_ids, int64_t P,
 __global__ __launch_bounds__(kPrepThreads) void moe_prep_kernel(
     const uint16_t* __restrict__ x, int64_t T, int nbc, uint32_t* __restrict__ xtf, int fwht_wgs,
     const int32_t* __restrict__ topk_ids, int64_t P, int top_k, int E, int32_t* __restrict__ offsets,
-    int32_t* __restrict__ sorted_token, int32_t* __restrict__ pair_pos) {
+    int32_t* __restrict__ sorted_token, int32_t* __restrict__ pair_pos, int xbf) {
   if ((int)blockIdx.x == fwht_wgs) {  // whole workgroup
     moe_align_block(topk_ids, P, top_k, E, offsets, sorted_token, pair_pos);
     return;
@@ -176,7 +240,8 @@ __global__ __launch_bounds__(kPrepThreads) void moe_prep_kernel(
   const int64_t r = bid / nbc;
   const int cb = (int)(bid - r * nbc);
   float v[8];
-  load8<PE_DTYPE_F16>(x + (r * nbc + cb) * kBlock + q * 8, v);
+  if (xbf) load8<PE_DTYPE_BF16>(x + (r * nbc + cb) * kBlock + q * 8, v);
+  else load8<PE_DTYPE_F16>(x + (r * nbc + cb) * kBlock + q * 8, v);
   fwht128_group16(v, q);
   store_pair_block(v, q, xtf + bid * 64, live);
 }
@@ -187,7 +252,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
                                                           const float* __restrict__ topk_w,
                                                           const int32_t* __restrict__ pair_pos,
                                                           int64_t T, int top_k, int H,
-                                                          uint16_t* __restrict__ out) {
+                                                          uint16_t* __restrict__ out, int ybf) {
   const int per_row = H / 4;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= T * per_row) return;
@@ -216,8 +281,8 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
     }
   }
   uint2 o;
-  o.x = pack_h2(acc[0], acc[1]);
-  o.y = pack_h2(acc[2], acc[3]);
+  o.x = pack16x2(acc[0], acc[1], ybf != 0);
+  o.y = pack16x2(acc[2], acc[3], ybf != 0);
   *reinterpret_cast<uint2*>(out + t * H + c) = o;
 }
 
@@ -249,20 +314,41 @@ static MoeWs moe_ws_layout(int64_t T, int top_k, int E, int H, int I) {
 
 using namespace pe;
 
-extern "C" int pe_moe_route(const float* logits, int64_t T, int E, int top_k, int renormalize,
-                            int scoring, const float* correction_bias, float* topk_w,
-                            int32_t* topk_ids, void* stream) {
+static int route(const float* logits, int64_t T, int E, int top_k, int renormalize, int scoring,
+                 const float* correction_bias, int n_group, int topk_group, float* topk_w,
+                 int32_t* topk_ids, hipStream_t st) {
   if (!logits || !topk_w || !topk_ids) return PE_ERR_NULL;
   if (T < 0 || E <= 0 || E > 256 || top_k <= 0 || top_k > 16 || top_k > E) return PE_ERR_DIMS;
   if (scoring != 0 && scoring != 1) return PE_ERR_DTYPE;
   if (T == 0) return PE_OK;
   const int64_t wgs = (T + kRouteWaves - 1) / kRouteWaves;
   if (wgs > INT32_MAX) return PE_ERR_DIMS;
-  moe_route_kernel<<<dim3((unsigned)wgs), dim3(64 * kRouteWaves), 0,
-                     reinterpret_cast<hipStream_t>(stream)>>>(logits, T, E, top_k, renormalize,
-                                                              scoring, correction_bias, topk_w,
-                                                              topk_ids);
+  moe_route_kernel<<<dim3((unsigned)wgs), dim3(64 * kRouteWaves), 0, st>>>(
+      logits, T, E, top_k, renormalize, scoring, correction_bias, topk_w, topk_ids, n_group,
+      topk_group);
   return launch_status();
+}
+
+extern "C" int pe_moe_route(const float* logits, int64_t T, int E, int top_k, int renormalize,
+                            int scoring, const float* correction_bias, float* topk_w,
+                            int32_t* topk_ids, void* stream) {
+  return route(logits, T, E, top_k, renormalize, scoring, correction_bias, 0, 0, topk_w, topk_ids,
+               reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int pe_moe_route_grouped(const float* logits, int64_t T, int E, int top_k,
+                                    int renormalize, int scoring, const float* correction_bias,
+                                    int num_expert_group, int topk_group, float* topk_w,
+                                    int32_t* topk_ids, void* stream) {
+  // whole groups, at most 64 of them; the kept groups must hold top_k experts;
+  // a bias ranks groups by their two best experts
+  if (num_expert_group <= 0 || num_expert_group > kRouteMaxGroups || E % num_expert_group ||
+      topk_group <= 0 || topk_group > num_expert_group ||
+      top_k > topk_group * (E / num_expert_group) ||
+      (correction_bias && E / num_expert_group < 2))
+    return PE_ERR_DIMS;
+  return route(logits, T, E, top_k, renormalize, scoring, correction_bias, num_expert_group,
+               topk_group, topk_w, topk_ids, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t pe_moe_workspace_size(int64_t T, int top_k, int E, int H, int I) {
@@ -270,7 +356,7 @@ extern "C" size_t pe_moe_workspace_size(int64_t T, int top_k, int E, int H, int 
   return moe_ws_layout(T, top_k, E, H, I).total;
 }
 
-extern "C" int pe_moe_forward(const void* x, int64_t T, int H, int I, int E, int top_k,
+extern "C" int pe_moe_forward(const void* x, int x_dtype, int64_t T, int H, int I, int E, int top_k,
                               const float* topk_w, const int32_t* topk_ids,
                               const void* w13_codes, int bits13, int packed13,
                               const uint16_t* w13_norms, const float* ct13, int n_levels13,
@@ -283,6 +369,8 @@ extern "C" int pe_moe_forward(const void* x, int64_t T, int H, int I, int E, int
     return PE_ERR_NULL;
   if (T < 0 || H <= 0 || I <= 0 || E <= 0 || E > 256 || top_k <= 0 || top_k > E) return PE_ERR_DIMS;
   if (H % kBlock) return PE_ERR_DIMS;
+  const int xbf = bf16_flag(x_dtype);  // x and out: fp16 or bf16
+  if (xbf < 0) return PE_ERR_DTYPE;
   for (int which = 0; which < 2; ++which) {
     const int bits = which ? bits2 : bits13, packed = which ? packed2 : packed13;
     const int nl = which ? n_levels2 : n_levels13;
@@ -319,7 +407,7 @@ extern "C" int pe_moe_forward(const void* x, int64_t T, int H, int I, int E, int
     if (fwht_wgs + 1 > INT32_MAX) return PE_ERR_DIMS;
     moe_prep_kernel<<<dim3((unsigned)(fwht_wgs + 1)), dim3(kPrepThreads), 0, st>>>(
         reinterpret_cast<const uint16_t*>(x), T, nbc, reinterpret_cast<uint32_t*>(ws + L.xtf),
-        (int)fwht_wgs, topk_ids, P, top_k, E, offsets, sorted_token, pair_pos);
+        (int)fwht_wgs, topk_ids, P, top_k, E, offsets, sorted_token, pair_pos, xbf);
     if (int rc = launch_status()) return rc;
   }
   // 2. gate/up + SwiGLU, each 128-column block of h transformed in the same
@@ -339,10 +427,10 @@ extern "C" int pe_moe_forward(const void* x, int64_t T, int H, int I, int E, int
                 wlayout(nib2, tiled2, nb2)};
     if (int rc = moe_grouped(nib2, SE_F32, a, E, st)) return rc;
   }
-  // 4. weighted combine -> out fp16
+  // 4. weighted combine -> out (x's dtype)
   const int64_t work = T * (H / 4);
   moe_combine_kernel<<<dim3((unsigned)((work + 255) / 256)), dim3(256), 0, st>>>(
       reinterpret_cast<const float*>(ws + L.y2), topk_w, pair_pos, T, top_k, H,
-      reinterpret_cast<uint16_t*>(out));
+      reinterpret_cast<uint16_t*>(out), xbf);
   return launch_status();
 }

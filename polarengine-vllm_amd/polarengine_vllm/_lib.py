@@ -54,8 +54,10 @@ _SIGNATURES = {
                              _vp]),
     "pe_tile_weights": (_c_int, [_vp, _vp, _c_i64, _c_int, _c_int, _vp, _vp, _vp]),
     "pe_moe_route": (_c_int, [_vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp]),
+    "pe_moe_route_grouped": (_c_int, [_vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp, _c_int,
+                                      _c_int, _vp, _vp, _vp]),
     "pe_moe_workspace_size": (_c_sz, [_c_i64, _c_int, _c_int, _c_int, _c_int]),
-    "pe_moe_forward": (_c_int, [_vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
+    "pe_moe_forward": (_c_int, [_vp, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
                                 _vp, _c_int, _c_int, _vp, _vp, _c_int,
                                 _vp, _c_int, _c_int, _vp, _vp, _c_int,
                                 _vp, _vp, _c_sz, _vp]),
@@ -117,6 +119,14 @@ def require_device(*tensors: torch.Tensor) -> torch.device:
 
 def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
+
+
+def act_dtype(t: torch.Tensor) -> int:
+    """PE_DTYPE_* code of a 16-bit activation tensor (fp16 or bf16)."""
+    code = {torch.float16: PE_DTYPE_F16, torch.bfloat16: PE_DTYPE_BF16}.get(t.dtype)
+    if code is None:
+        raise TypeError(f"PolarEngine kernels take float16 or bfloat16 activations, got {t.dtype}")
+    return code
 
 
 _WS_CACHE: dict = {}

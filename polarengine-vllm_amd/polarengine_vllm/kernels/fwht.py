@@ -12,6 +12,7 @@ import math
 from typing import Optional
 
 import torch
+from torch.autograd.graph import increment_version
 
 from polarengine_vllm import _lib
 
@@ -53,6 +54,7 @@ def fwht_matmul(x: torch.Tensor, block_size: int = 128, out: Optional[torch.Tens
         raise TypeError(f"unsupported dtype {x.dtype}")
     xc = x.contiguous()
     rows = xc.numel() // in_features if in_features else 0
+    caller_out = out is not None
     if out is None:
         out = torch.empty_like(xc)
     layout = {torch.float32: _lib.PE_XTF_F32, torch.float16: _lib.PE_XTF_F16,
@@ -63,6 +65,10 @@ def fwht_matmul(x: torch.Tensor, block_size: int = 128, out: Optional[torch.Tens
           torch.float32: _lib.PE_DTYPE_F32}[xc.dtype]
     _lib.check(_lib.lib().pe_fwht128(xc.data_ptr(), dt, rows, in_features, in_features,
                                      out.data_ptr(), layout, _lib.stream_ptr(dev)), "pe_fwht128")
+    if caller_out:
+        # the kernel wrote the caller's tensor through a raw pointer: record
+        # the write so that version-keyed caches (FWHTCache) see it
+        increment_version(out)
     return out.view(x.shape)
 
 
@@ -89,8 +95,15 @@ class FWHTCache:
     returns the cached transform when ``x`` is the tensor that was ``put``,
     ``clear`` empties it. The entry keeps a reference to ``x`` and records
     its version counter and geometry, so a different tensor that later
-    reuses the same storage address, or an in-place update of ``x``, misses
-    instead of returning a stale transform.
+    reuses the same storage address, or an in-place update of ``x`` through
+    torch, misses instead of returning a stale transform.
+
+    A write that bypasses torch (a kernel handed ``x.data_ptr()``) does not
+    bump the version. This package's own wrappers record such writes into
+    caller tensors (``increment_version``); for anything else the cache must
+    be scoped: ``install_fwht_cache_hooks`` (linear_method) clears it at the
+    start of every forward of a module that owns PolarQuant linears, so an
+    entry only ever serves sibling projections inside one parent forward.
     """
 
     def __init__(self):

@@ -24,6 +24,7 @@ import math
 from typing import Dict, Optional, Tuple
 
 import torch
+from torch.autograd.graph import increment_version
 
 from .config import PolarKVConfig
 
@@ -150,6 +151,7 @@ class PolarKVQuantizer:
         from polarengine_vllm import _lib
         dev = _lib.require_device(packed)
         n = packed.shape[0]
+        caller_out = out is not None
         if out is None:
             out = torch.empty(n, self.head_dim, dtype=torch.bfloat16, device=dev)
         nb = norms.contiguous().to(torch.bfloat16)
@@ -157,6 +159,8 @@ class PolarKVQuantizer:
                                                self.head_dim, self.centroids.data_ptr(), self.nbits,
                                                out.data_ptr(), out.stride(0), _lib.stream_ptr(dev)),
                    "pe_kv_dequantize")
+        if caller_out:
+            increment_version(out)  # written through a raw pointer
         return out.reshape(shape)
 
 
@@ -166,11 +170,19 @@ class PolarKVLayer:
 
     ``update(new)`` appends ``new`` [B, H, S_new, D]; tokens beyond
     ``residual_length`` are compressed; the return value is the whole history
-    [B, H, S, D] in bf16 (expanded history followed by the residual)."""
+    [B, H, S, D] in bf16 (expanded history followed by the residual).
 
-    def __init__(self, quantizer: PolarKVQuantizer, residual_length: int = 128) -> None:
+    By default only the codes, norms and residual persist and the history is
+    expanded per call, as the reference does. ``keep_expanded=True`` keeps a
+    bf16 copy of the expanded history as a read cache (each token expanded
+    once), at the cost of more memory than an uncompressed cache;
+    ``memory_bytes`` then counts it."""
+
+    def __init__(self, quantizer: PolarKVQuantizer, residual_length: int = 128,
+                 keep_expanded: bool = False) -> None:
         self.quantizer = quantizer
         self.residual_length = residual_length
+        self.keep_expanded = keep_expanded
         self.reset()
 
     def reset(self) -> None:
@@ -192,11 +204,14 @@ class PolarKVLayer:
         rb = BitPacker.packed_size(d, self.quantizer.nbits)
         packed = torch.empty(bh, new_cap, rb, dtype=torch.uint8, device=dev)
         norms = torch.empty(bh, new_cap, dtype=torch.bfloat16, device=dev)
-        expanded = torch.empty(bh, new_cap, d, dtype=torch.bfloat16, device=dev)
+        expanded = None
+        if self.keep_expanded:
+            expanded = torch.empty(bh, new_cap, d, dtype=torch.bfloat16, device=dev)
         if cap:
             packed[:, :self._q_count] = self._packed[:, :self._q_count]
             norms[:, :self._q_count] = self._norms[:, :self._q_count]
-            expanded[:, :self._q_count] = self._expanded[:, :self._q_count]
+            if expanded is not None:
+                expanded[:, :self._q_count] = self._expanded[:, :self._q_count]
         self._packed, self._norms, self._expanded = packed, norms, expanded
 
     def update(self, new_tensor: torch.Tensor) -> torch.Tensor:
@@ -215,15 +230,25 @@ class PolarKVLayer:
             s0, s1 = self._q_count, self._q_count + n_q
             self._packed[:, s0:s1] = packed.view(bh, n_q, -1)
             self._norms[:, s0:s1] = norms.view(bh, n_q)
-            # expand only the newly compressed tokens, straight into the history
-            dst = self._expanded[:, s0:s1]
-            if dst.is_contiguous():
-                self.quantizer.dequantize(packed, norms, (bh * n_q, self._D), out=dst.view(bh * n_q, self._D))
-            else:
-                dst.copy_(self.quantizer.dequantize(packed, norms, (bh, n_q, self._D)))
+            if self._expanded is not None:
+                # read cache: expand only the newly compressed tokens into it
+                dst = self._expanded[:, s0:s1]
+                if dst.is_contiguous():
+                    self.quantizer.dequantize(packed, norms, (bh * n_q, self._D),
+                                              out=dst.view(bh * n_q, self._D))
+                else:
+                    dst.copy_(self.quantizer.dequantize(packed, norms, (bh, n_q, self._D)))
             self._q_count = s1
         if self._q_count:
-            hist = self._expanded[:, :self._q_count].reshape(self._B, self._H, self._q_count, self._D)
+            q = self._q_count
+            if self._expanded is not None:
+                hist = self._expanded[:, :q]
+            else:  # transient expansion of the whole compressed history
+                bh = self._B * self._H
+                hist = self.quantizer.dequantize(self._packed[:, :q].reshape(bh * q, -1),
+                                                 self._norms[:, :q].reshape(bh * q),
+                                                 (bh * q, self._D))
+            hist = hist.reshape(self._B, self._H, q, self._D)
             return torch.cat([hist, self.residual], dim=2)
         return self.residual
 
@@ -240,20 +265,24 @@ class PolarKVLayer:
 
     def memory_bytes(self) -> int:
         """Bytes of the compressed history (codes + norms) and the residual,
-        as the reference counts them (the bf16 expansion is a read cache)."""
+        as the reference counts them, plus the expanded read cache's
+        allocation when ``keep_expanded`` holds one."""
         total = 0
         if self._q_count:
             bh = self._B * self._H
             total += bh * self._q_count * self._packed.shape[2] + bh * self._q_count * 2
         if self.residual is not None:
             total += self.residual.numel() * 2
+        if self._expanded is not None:
+            total += self._expanded.numel() * 2
         return total
 
 
 class PolarKVCache:
     """K and V caches of all layers (reference: cache.py:357-462)."""
 
-    def __init__(self, config: PolarKVConfig, device: Optional[str] = None) -> None:
+    def __init__(self, config: PolarKVConfig, device: Optional[str] = None,
+                 keep_expanded: bool = False) -> None:
         self.config = config
         device = device or ("cuda" if torch.cuda.is_available() else "cpu")
         self.quantizer = PolarKVQuantizer(config.head_dim, config.nbits, device)
@@ -261,8 +290,9 @@ class PolarKVCache:
         self.v_layers = []
         for i in range(config.num_layers):
             skip = i in config.skip_layers
-            self.k_layers.append(None if skip else PolarKVLayer(self.quantizer, config.residual_length))
-            self.v_layers.append(None if skip else PolarKVLayer(self.quantizer, config.residual_length))
+            mk = lambda: PolarKVLayer(self.quantizer, config.residual_length, keep_expanded)
+            self.k_layers.append(None if skip else mk())
+            self.v_layers.append(None if skip else mk())
         self._seen_tokens = 0
 
     def update(self, key_states: torch.Tensor, value_states: torch.Tensor,

@@ -15,8 +15,11 @@ Differences from the reference, on purpose:
 * the FWHT cache is process-wide (the reference's lives per method instance,
   linear_method.py:85, so separate q/k/v modules never shared it) and keyed
   safely (see kernels.fwht.FWHTCache);
-* activations must be float16 (the kernels' operand type); the output dtype
-  is float16 as in the reference (linear_method.py:219).
+* a bf16 activation gives a bf16 result (the reference casts every output to
+  fp16, linear_method.py:219, which a bf16 model cannot add to its bf16
+  residual stream without a promotion); fp16 stays fp16, and other float
+  dtypes give fp16 as in the reference. The transformed activation enters the
+  matrix cores as fp16 in every case.
 """
 
 from __future__ import annotations
@@ -118,21 +121,27 @@ class PolarQuantLinearMethod:
     # ------------------------------------------------------------------
     def apply(self, layer: torch.nn.Module, x: torch.Tensor,
               bias: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """Quantized forward: y = x . W^T (+ bias), fp16 [..., out_f]."""
+        """Quantized forward: y = x . W^T (+ bias), [..., out_f].
+
+        fp16 and bf16 activations give a result of the same dtype; any other
+        float dtype is transformed from its own precision and gives fp16, the
+        reference's output dtype (linear_method.py:184-221 casts x.float()
+        and returns .half())."""
         orig_shape = x.shape
         packed = bool(getattr(layer, "packed", False))
         codes = layer.codes_packed if packed else layer.codes
         dev = _lib.require_device(x, codes)
-        if x.dtype != torch.float16:
-            raise TypeError(f"PolarEngine gfx950 kernels take float16 activations, got {x.dtype}")
+        if not x.is_floating_point():
+            raise TypeError(f"PolarEngine linear takes floating-point activations, got {x.dtype}")
+        out_dtype = x.dtype if x.dtype in (torch.float16, torch.bfloat16) else torch.float16
         x2 = x.reshape(-1, layer.in_f)
         m = x2.shape[0]
-        y = torch.empty(m, layer.out_f, dtype=torch.float16, device=dev)
+        y = torch.empty(m, layer.out_f, dtype=out_dtype, device=dev)
         if m == 0:
             return y.view(*orig_shape[:-1], layer.out_f)
         b = None
         if bias is not None:
-            b = bias.to(device=dev, dtype=torch.float16).contiguous()
+            b = bias.to(device=dev, dtype=out_dtype).contiguous()
         L = _lib.lib()
         st = _lib.stream_ptr(dev)
         n_levels = layer.ct_scaled.numel()
@@ -141,8 +150,9 @@ class PolarQuantLinearMethod:
         ct_host = None if ct_host is None else ct_host.ctypes.data
         fmt = (_lib.PE_PACK_NIBBLE if packed else 0) | (
             _lib.PE_LAYOUT_TILE16 if getattr(layer, "tiled", False) else 0)
+        out_code = _lib.act_dtype(y)
 
-        if m >= _SHARE_FWHT_MIN_M:
+        if m >= _SHARE_FWHT_MIN_M or x.dtype != out_dtype:
             x_tf = self._fwht_cache.get(x, layer.in_f)
             if x_tf is None:
                 xp = x2 if kp == layer.in_f else F.pad(x2, (0, kp - layer.in_f))
@@ -153,7 +163,7 @@ class PolarQuantLinearMethod:
             rc = L.pe_linear_forward_xtf(
                 x_tf.data_ptr(), m, kp, codes.data_ptr(), layer.bits, fmt,
                 layer.norms.data_ptr(), layer.ct_scaled.data_ptr(), ct_host, n_levels, _lib.ptr(b),
-                _lib.PE_DTYPE_F16, y.data_ptr(), layer.out_f, _lib.ptr(ws), ws_bytes, st)
+                out_code, y.data_ptr(), layer.out_f, _lib.ptr(ws), ws_bytes, st)
             _lib.check(rc, "pe_linear_forward_xtf")
         else:
             xc = x2 if kp == layer.in_f else F.pad(x2, (0, kp - layer.in_f))
@@ -161,7 +171,7 @@ class PolarQuantLinearMethod:
             ws_bytes = L.pe_linear_workspace_size(m, kp, layer.out_f, layer.bits, fmt)
             ws = _lib.workspace(dev, ws_bytes)
             rc = L.pe_linear_forward(
-                xc.data_ptr(), _lib.PE_DTYPE_F16, m, kp, kp, codes.data_ptr(), layer.bits,
+                xc.data_ptr(), out_code, m, kp, kp, codes.data_ptr(), layer.bits,
                 fmt, layer.norms.data_ptr(), layer.ct_scaled.data_ptr(), ct_host, n_levels,
                 _lib.ptr(b), y.data_ptr(), layer.out_f, _lib.ptr(ws), ws_bytes, st)
             _lib.check(rc, "pe_linear_forward")
@@ -175,3 +185,29 @@ def create_fwht_clear_hook(linear_method: PolarQuantLinearMethod):
         linear_method._fwht_cache.clear()
 
     return hook
+
+
+def install_fwht_cache_hooks(model: torch.nn.Module, cache: Optional[FWHTCache] = None) -> int:
+    """Register the cache-clearing pre-hook on every module that has a
+    PolarQuant linear as a direct child (e.g. a decoder layer's attention and
+    MLP blocks), and return how many were registered.
+
+    Sibling projections called inside one such forward (q/k/v on the same
+    hidden state, gate/up) still share one transform; a new forward of the
+    parent always starts empty, so a hidden-state buffer rewritten outside
+    torch between forwards can never be served a stale transform. The
+    reference defines the hook but registers it nowhere."""
+    cache = GLOBAL_FWHT_CACHE if cache is None else cache
+
+    def hook(module: torch.nn.Module, args):
+        cache.clear()
+
+    n = 0
+    for parent in model.modules():
+        if any(isinstance(getattr(child, "quant_method", None), PolarQuantLinearMethod)
+               for child in parent.children()):
+            if not getattr(parent, "_polar_fwht_hook", False):
+                parent.register_forward_pre_hook(hook)
+                parent._polar_fwht_hook = True
+                n += 1
+    return n

@@ -98,8 +98,13 @@ class PolarQuantMoEMethod:
 
     def select_experts(self, router_logits: torch.Tensor, top_k: int, renormalize: bool,
                        scoring_func: str = "softmax",
-                       e_score_correction_bias: Optional[torch.Tensor] = None):
-        """(topk_weights float32 [T, k], topk_ids int32 [T, k]) via pe_moe_route."""
+                       e_score_correction_bias: Optional[torch.Tensor] = None,
+                       use_grouped_topk: bool = False, num_expert_group: Optional[int] = None,
+                       topk_group: Optional[int] = None):
+        """(topk_weights float32 [T, k], topk_ids int32 [T, k]) via pe_moe_route,
+        or pe_moe_route_grouped for grouped top-k (vLLM's grouped_topk, the
+        routing the reference's apply hands to vLLM with use_grouped_topk,
+        moe_method.py:74-89)."""
         dev = _lib.require_device(router_logits)
         lg = router_logits.to(torch.float32).contiguous()
         t, e = lg.shape
@@ -111,6 +116,14 @@ class PolarQuantMoEMethod:
         scoring = {"softmax": 0, "sigmoid": 1}.get(scoring_func)
         if scoring is None:
             raise ValueError(f"unsupported scoring_func {scoring_func}")
+        if use_grouped_topk:
+            if num_expert_group is None or topk_group is None:
+                raise ValueError("grouped top-k needs num_expert_group and topk_group")
+            _lib.check(_lib.lib().pe_moe_route_grouped(
+                lg.data_ptr(), t, e, top_k, int(bool(renormalize)), scoring, _lib.ptr(bias),
+                int(num_expert_group), int(topk_group), w.data_ptr(), ids.data_ptr(),
+                _lib.stream_ptr(dev)), "pe_moe_route_grouped")
+            return w, ids
         _lib.check(_lib.lib().pe_moe_route(lg.data_ptr(), t, e, top_k, int(bool(renormalize)),
                                            scoring, _lib.ptr(bias), w.data_ptr(), ids.data_ptr(),
                                            _lib.stream_ptr(dev)), "pe_moe_route")
@@ -121,13 +134,9 @@ class PolarQuantMoEMethod:
               topk_group: Optional[int] = None, num_expert_group: Optional[int] = None,
               custom_routing_function=None, scoring_func: str = "softmax",
               e_score_correction_bias: Optional[torch.Tensor] = None, **kwargs) -> torch.Tensor:
-        """Routed quantized SwiGLU experts: [T, H] fp16 -> [T, H] fp16."""
-        if use_grouped_topk:
-            raise NotImplementedError("grouped top-k routing is not implemented by the "
-                                      "PolarEngine gfx950 MoE path")
+        """Routed quantized SwiGLU experts: [T, H] fp16 or bf16 -> [T, H] of the same dtype."""
         dev = _lib.require_device(x, layer.w13_codes)
-        if x.dtype != torch.float16:
-            raise TypeError(f"PolarEngine gfx950 kernels take float16 activations, got {x.dtype}")
+        x_code = _lib.act_dtype(x)
         xs = x.reshape(-1, layer.hidden_size).contiguous()
         t = xs.shape[0]
         if custom_routing_function is not None:
@@ -137,7 +146,8 @@ class PolarQuantMoEMethod:
             ids = ids.to(torch.int32).contiguous()
         else:
             w, ids = self.select_experts(router_logits.reshape(t, -1), top_k, renormalize,
-                                         scoring_func, e_score_correction_bias)
+                                         scoring_func, e_score_correction_bias, use_grouped_topk,
+                                         num_expert_group, topk_group)
         out = torch.empty_like(xs)
         if t == 0:
             return out.view(x.shape)
@@ -146,7 +156,7 @@ class PolarQuantMoEMethod:
         wsb = L.pe_moe_workspace_size(t, top_k, e, h, i)
         ws = _lib.workspace(dev, wsb)
         rc = L.pe_moe_forward(
-            xs.data_ptr(), t, h, i, e, top_k, w.data_ptr(), ids.data_ptr(),
+            xs.data_ptr(), x_code, t, h, i, e, top_k, w.data_ptr(), ids.data_ptr(),
             layer.w13_codes.data_ptr(), self.bits13, _layout(layer.w13_packed, layer.w13_tiled),
             layer.w13_norms.data_ptr(), layer.w13_ct_scaled.data_ptr(), 1 << self.bits13,
             layer.w2_codes.data_ptr(), self.bits2, _layout(layer.w2_packed, layer.w2_tiled),

@@ -72,3 +72,56 @@ def test_no_cpu_fallback():
     from polarengine_vllm.kernels.fwht import fwht_matmul
     with pytest.raises(RuntimeError, match="GPU only"):
         fwht_matmul(torch.randn(2, 128))
+
+
+def _ru(v, a=256):
+    return (v + a - 1) // a * a
+
+
+def test_workspace_queries_cover_every_path():
+    """Size queries (host code; 256 CUs assumed without a device) follow the
+    path the call takes, M = 1 included: the fused decode kernel needs
+    nothing; an M = 1 call past the decode kernel's limits on the tiled
+    layout, or past the M = 1 GEMV's LDS budget on the row-major one, needs
+    the pair-f16 transform; the reference-API matmul at M = 1 with int8 codes
+    past 24576 needs its repacked activation."""
+    from polarengine_vllm import _lib
+    L = _lib.lib()
+    NIB, T16 = _lib.PE_PACK_NIBBLE, _lib.PE_LAYOUT_TILE16
+    # the headline decode shape: fused, no workspace
+    assert L.pe_linear_workspace_size(1, 4096, 12288, 4, NIB | T16) == 0
+    assert L.pe_linear_workspace_size(1, 12288, 4096, 3, NIB | T16) == 0
+    # K = 53248 (416 blocks): too many activation registers for the decode
+    # kernel at M = 1; tiled -> FWHT + matmul; row-major nibbles past 49152
+    # too -> the same
+    for fmt in (NIB | T16, NIB):
+        assert L.pe_linear_workspace_size(1, 53248, 4096, 4, fmt) >= _ru(53248 * 2)
+    # row-major int8, 128 blocks: the decode kernel holds x in LDS beside the
+    # 256-entry table (64 KB + 32 KB): fused, no workspace
+    assert L.pe_linear_workspace_size(1, 16384, 1000, 6, 0) == 0
+    # reference-API matmul
+    assert L.pe_polar_matmul_workspace_size(1, 4096) == 0
+    assert L.pe_polar_matmul_workspace_size(1, 28672) >= 28672 * 2
+    assert L.pe_polar_matmul_workspace_size(8, 4096) >= 8 * 4096 * 2
+    # prefill: the pair-f16 transform at least
+    assert L.pe_linear_workspace_size(2048, 4096, 12288, 4, NIB | T16) >= 2048 * 4096 * 2
+    # invalid arguments: zero
+    assert L.pe_linear_workspace_size(0, 4096, 4096, 4, NIB) == 0
+    assert L.pe_linear_workspace_size(1, 4096, 4096, 9, 0) == 0
+
+
+def test_workspace_checked_before_launch():
+    """A call whose path needs workspace fails with PE_ERR_WORKSPACE (6)
+    before launching anything when it gets none or too little."""
+    from polarengine_vllm import _lib
+    L = _lib.lib()
+    NIB, T16 = _lib.PE_PACK_NIBBLE, _lib.PE_LAYOUT_TILE16
+    need = L.pe_linear_workspace_size(1, 53248, 4096, 4, NIB | T16)
+    assert need > 0
+    assert L.pe_linear_forward(16, 0, 1, 53248, 53248, 16, 4, NIB | T16, 16, 16, None, 16, None,
+                               16, 4096, None, 0, None) == 6
+    assert L.pe_linear_forward(16, 0, 1, 53248, 53248, 16, 4, NIB | T16, 16, 16, None, 16, None,
+                               16, 4096, 256, need - 256, None) == 6
+    # unsupported activation dtype
+    assert L.pe_linear_forward(16, 2, 1, 128, 128, 16, 4, NIB, 16, 16, None, 16, None, 16, 8,
+                               None, 0, None) == 5

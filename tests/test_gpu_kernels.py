@@ -14,6 +14,7 @@ import pytest
 import torch
 
 import polar_oracle as O
+from gpu_helpers import stratified_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -359,9 +360,12 @@ def test_tile_weights_bit_exact(n, k, bits):
     assert np.array_equal(nt.cpu().numpy().view(np.uint16), want_n.view(np.uint16))
 
 
+# includes the two-m-tile decode kernel (M = 17..32) and the M = 33..64
+# prefill K split on the MLP shapes
 TILED_CASES = [(1, 12288, 4096, 4), (1, 4096, 12288, 3), (1, 1000, 1408, 5), (4, 257, 384, 2),
                (16, 4096, 2048, 4), (16, 4096, 4096, 4), (33, 1000, 1408, 6), (256, 1536, 1024, 4),
-               (300, 200, 640, 8), (1, 48, 256, 6)]
+               (300, 200, 640, 8), (1, 48, 256, 6), (24, 4096, 12288, 3), (32, 12288, 4096, 4),
+               (64, 12288, 4096, 4), (20, 1000, 1408, 5)]
 
 
 @pytest.mark.parametrize("m,n,k,bits", TILED_CASES)
@@ -419,7 +423,9 @@ def test_polar_matmul_reference_api(m, n, k, bits):
 @pytest.mark.parametrize("m,n,k,bits", [(2048, 12288, 4096, 4), (2048, 4096, 12288, 3),
                                         (8192, 12288, 4096, 4)])
 def test_prefill_gemm_full_size_row_sample(m, n, k, bits):
-    """BASELINE prefill shapes: the oracle checks a seeded sample of rows."""
+    """BASELINE prefill shapes on the reference row-major layout: the oracle
+    checks at least one row of every 128-row m-tile (the tiled layout's
+    whole outputs are in test_gpu_layer.py)."""
     from polarengine_vllm import _lib
     _say(f"prefill m={m} n={n} k={k} bits={bits}")
     rng = np.random.default_rng(bits + m)
@@ -437,8 +443,7 @@ def test_prefill_gemm_full_size_row_sample(m, n, k, bits):
                              _lib.stream_ptr(torch.device(DEV)))
     torch.cuda.synchronize()
     _lib.check(rc, "pe_linear_forward")
-    rows = np.sort(rng.choice(m, 24, replace=False))
-    rows[0], rows[-1] = 0, m - 1
+    rows = stratified_rows(m, seed=bits + m)  # every 128-row m-tile, all columns
     want = O.linear_apply(x[rows], codes, norms, ct, k)
     got = y[torch.from_numpy(rows).to(DEV)].float().cpu().numpy()
     check_close(got, want.astype(np.float32), f"prefill {m}x{n}x{k}")
@@ -477,8 +482,7 @@ def test_prefill_ksplit_row_sample(m, n, k, bits):
         _lib.check(rc, "pe_linear_forward")
         outs.append(y)
     assert torch.equal(outs[0], outs[1]), "k-split prefill not deterministic"
-    rows = np.sort(rng.choice(m, 24, replace=False))
-    rows[0], rows[-1] = 0, m - 1
+    rows = stratified_rows(m, seed=bits + m + n, tile=32, per_tile=2)
     want = O.linear_apply(x[rows], codes, norms, ct, k, bias)
     got = outs[0][torch.from_numpy(rows).to(DEV)].float().cpu().numpy()
     check_close(got, want.astype(np.float32), f"k-split prefill {m}x{n}x{k}")
@@ -509,8 +513,7 @@ def test_four_wave_prefill_row_sample(m, n, k, bits, out, with_bias, tiled):
         fmt = _lib.PE_PACK_NIBBLE if nib else 0
     L = _lib.lib()
     cd = to_dev(ct)
-    rows = np.sort(rng.choice(m, 24, replace=False))
-    rows[0], rows[-1] = 0, m - 1
+    rows = stratified_rows(m, seed=m + n + bits, per_tile=2)
     if out == "f16":
         y = torch.empty(m, n, dtype=torch.float16, device=DEV)
         wsb = L.pe_linear_workspace_size(m, k, n, bits, fmt)

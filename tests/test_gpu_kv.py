@@ -184,21 +184,24 @@ def _expected_history(tokens: np.ndarray, residual: int, bits: int) -> tuple:
     return O.kv_quantize(tokens[:, :, :sq].reshape(-1, d), bits)
 
 
+@pytest.mark.parametrize("keep", [False, True])
 @pytest.mark.parametrize("b,h,d,bits,chunks", [(2, 3, 128, 3, [40, 1, 1, 1, 20, 1]),
                                                (1, 1, 64, 2, [10, 10, 10]),
                                                (1, 4, 256, 4, [5, 300, 1, 2])])
-def test_kv_layer_update(b, h, d, bits, chunks):
+def test_kv_layer_update(b, h, d, bits, chunks, keep):
     """The history returned after every update: the residual tokens exactly,
     the compressed ones as the expansion of the oracle's codes; compressed()
     holds the oracle's codes and norms for every token so far, in token order
-    per head (the order the reference's buffer has while it holds one chunk)."""
+    per head (the order the reference's buffer has while it holds one chunk).
+    keep: with the expanded read cache (counted by memory_bytes) or without
+    (the history expanded per call)."""
     from polarengine_vllm.kv_cache import PolarKVLayer, PolarKVQuantizer
     R = 16
     qz = PolarKVQuantizer(d, bits, DEV)
-    layer = PolarKVLayer(qz, residual_length=R)
+    layer = PolarKVLayer(qz, residual_length=R, keep_expanded=keep)
     seen = np.zeros((b, h, 0, d), np.float32)
     for step, s_new in enumerate(chunks):
-        _say(f"kv layer b={b} h={h} d={d} bits={bits} step={step} s_new={s_new}")
+        _say(f"kv layer b={b} h={h} d={d} bits={bits} keep={keep} step={step} s_new={s_new}")
         new = torch.from_numpy(O.seeded_normal((b, h, s_new, d), 1.0, 100 * step + d)).to(torch.bfloat16)
         seen = np.concatenate([seen, new.float().numpy()], axis=2)
         full = layer.update(new.to(DEV))
@@ -219,7 +222,10 @@ def test_kv_layer_update(b, h, d, bits, chunks):
         hist = full[:, :, :r0].reshape(-1, d)
         want = O.kv_dequantize(gp.cpu().numpy(), _bits(gn), bits, d)
         check_bf16_values(_bits(hist), want, _bits(gn), f"layer history step {step}")
-        assert layer.memory_bytes() == gp.numel() + gn.numel() * 2 + b * h * min(S, R) * d * 2
+        cache_bytes = layer._expanded.numel() * 2 if keep else 0
+        assert (layer._expanded is not None) == keep
+        assert layer.memory_bytes() == (gp.numel() + gn.numel() * 2 + b * h * min(S, R) * d * 2
+                                        + cache_bytes)
 
 
 def test_kv_cache_and_attention_wrapper():

@@ -260,6 +260,28 @@ def test_hadamard_domain_equals_dense_route(bits):
     np.testing.assert_allclose(had, dense, rtol=1e-4, atol=1e-4)
 
 
+def test_hadamard_domain_row_chunks_equal_dense_route():
+    """Enough rows that the product runs in three row chunks."""
+    rng = np.random.default_rng(17)
+    codes, norms, ct = _rand_layer(rng, 8192, 256, 4)
+    x = rng.standard_normal((4300, 256)).astype(np.float32)
+    dense = x.astype(np.float64) @ O.dequant_weight(codes, norms, ct).astype(np.float64).T
+    had = O.hadamard_domain_matmul(codes, norms, ct, O.fwht_blocks(x))
+    np.testing.assert_allclose(had, dense, rtol=1e-4, atol=1e-4)
+
+
+def test_dequant_matmul_equals_linear_apply():
+    rng = np.random.default_rng(19)
+    w = (rng.standard_normal((72, 384)) * 0.02).astype(np.float32)
+    q = O.quantize_tensor(w, 4)
+    x = rng.standard_normal((6, 384)).astype(np.float16)
+    bias = rng.standard_normal(72).astype(np.float16)
+    wd = O.dequant_weight(q["codes"], q["norms"], q["ct_scaled"])
+    got = O.dequant_matmul(x, wd, bias).astype(np.float32)
+    want = O.linear_apply(x, q["codes"], q["norms"], q["ct_scaled"], 384, bias).astype(np.float32)
+    np.testing.assert_allclose(got, want, rtol=2e-3, atol=2e-3)
+
+
 def test_one_hot_probe_returns_codebook_entry():
     rng = np.random.default_rng(8)
     codes, _, ct = _rand_layer(rng, 16, 256, 4)
