@@ -77,7 +77,7 @@ class Linear:
         self.y = torch.empty(m, n, device=dev, dtype=torch.float16)
         L = _lib.lib()
         self.wsb = L.pe_linear_workspace_size(m, k, n, bits, self.packed)
-        self.ws = torch.empty(max(self.wsb, 256), device=dev, dtype=torch.uint8)
+        self.ws = torch.zeros(max(self.wsb, 256), device=dev, dtype=torch.uint8)
         self.dev = dev
 
     def __call__(self):

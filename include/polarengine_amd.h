@@ -9,6 +9,14 @@
  * owned by the caller. Entry points are re-entrant; concurrent calls on one
  * workspace race.
  *
+ * Workspaces: a workspace (any size query's bytes, 16-byte aligned) must be
+ * zero-filled once before its first use. Its first 4096 bytes hold
+ * completion counters of the kernels that split K over workgroups (the last
+ * workgroup of a group adds the partial sums, so no second kernel is
+ * launched); every call leaves them zero again and no entry point writes
+ * anything else there, so one zeroed buffer, sized for the largest query,
+ * can serve every entry point in turn.
+ *
  * Runtime weight layout (one quantized linear, N = out_f, Kp = in_f padded to
  * a multiple of 128, nb = Kp / 128), as registered by the reference's
  * PolarQuantLinearMethod.create_weights / process_weights_after_loading

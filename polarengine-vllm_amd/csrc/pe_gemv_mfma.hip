@@ -53,6 +53,7 @@ struct DecSrc {
 };
 
 constexpr int kBufNT = 2;              // cache policy: non-temporal (weights are read once)
+constexpr int kBufSC1 = 16;            // cache policy: device-coherent (sc1)
 constexpr int kBufFlags = 0x00020000;  // raw buffer, 32-bit data format (dword 3 of the resource)
 
 template <bool NIB, int TN>
@@ -175,8 +176,10 @@ __device__ __forceinline__ void dec_table_write(const DecTable<NIB>& t, int n_le
 // NW = TN * KS waves: wave w works on tile w % TN over the K-slice w / TN
 // (contiguous 128-blocks), streaming it D blocks deep. XC: activation
 // registers per lane. SPLIT: the K blocks are divided into gridDim.y groups,
-// blockIdx.y's group only (its activations alone in LDS); y then receives
-// fp32 partial sums [gridDim.y][M][N], added by dec_split_reduce_kernel.
+// blockIdx.y's group only (its activations alone in LDS); each workgroup
+// writes fp32 partial sums part[blockIdx.y][M][N], and the last of the
+// gridDim.y workgroups of a row group to finish (counted in cnt[blockIdx.x])
+// adds the groups' partials in group order, writes y and resets its counter.
 template <bool NIB, int TN, int KS, bool XRAW, bool MASK, int XC, int D, bool CTV, bool SPLIT,
           int MTD = 1>
 __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
@@ -184,7 +187,7 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
     const float* __restrict__ ct, int n_levels, uint32_t code_mask,
     const void* __restrict__ x, int64_t ldx, void* __restrict__ y, int64_t ldy,
     const uint16_t* __restrict__ bias, int M, int N, int nb, uint32_t xs_addr, WLayout lay,
-    DecCtArg<NIB> ctv, int io) {
+    DecCtArg<NIB> ctv, int io, float* __restrict__ part, uint32_t* __restrict__ cnt) {
   constexpr int NW = TN * KS;
   const bool xbf = (io & 1) != 0, ybf = (io & 2) != 0;  // raw x / y and bias are bfloat16
   const int tid = threadIdx.x;
@@ -393,21 +396,115 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
   __syncthreads();
   // outputs: rows m < M (D element e of lane l in m-tile i: row 16 i +
   // 4 (l / 16) + e), 16 TN columns
-  for (int o = tid; o < TN * MTD * 256; o += NW * 64) {
-    const int ji = o >> 8, le = o & 255, ln = le >> 2, e = le & 3;  // ji = j * MTD + i
-    const int j = ji / MTD, i = ji - j * MTD;
-    const int m = 16 * i + 4 * (ln >> 4) + e;
-    const int n = (blockIdx.x * TN + j) * 16 + (ln & 15);
-    if (m >= M || n >= N) continue;
-    float s = 0.f;
+  if constexpr (!SPLIT) {
+    for (int o = tid; o < TN * MTD * 256; o += NW * 64) {
+      const int ji = o >> 8, le = o & 255, ln = le >> 2, e = le & 3;  // ji = j * MTD + i
+      const int j = ji / MTD, i = ji - j * MTD;
+      const int m = 16 * i + 4 * (ln >> 4) + e;
+      const int n = (blockIdx.x * TN + j) * 16 + (ln & 15);
+      if (m >= M || n >= N) continue;
+      float s = 0.f;
 #pragma unroll
-    for (int w = 0; w < KS; ++w)
-      s += __builtin_bit_cast(float, lds_ld32((uint32_t)(((((w * TN + j) * MTD + i) * 64) * 4 + le) * 4)));
-    if constexpr (SPLIT) {
-      reinterpret_cast<float*>(y)[((int64_t)blockIdx.y * M + m) * N + n] = s;
-    } else {
+      for (int w = 0; w < KS; ++w)
+        s += __builtin_bit_cast(float, lds_ld32((uint32_t)(((((w * TN + j) * MTD + i) * 64) * 4 + le) * 4)));
       reinterpret_cast<uint16_t*>(y)[(int64_t)m * ldy + n] = out16(s, bias, n, ybf);
     }
+  } else {
+    // Partial sums of this K group, four consecutive columns per thread, as
+    // device-coherent stores (cache policy sc1: written through to the level
+    // every XCD reads); part[g][m][n] addressed through a buffer resource.
+    const int nq = 4 * TN;  // column quads of this workgroup
+    const bool vec = (N & 3) == 0;
+    const int64_t slab = (int64_t)M * N;
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)part, (short)0, (int)(gridDim.y * slab * 4), kBufFlags);
+    for (int o = tid; o < M * nq; o += NW * 64) {
+      const int m = o / nq, q = o - m * nq;
+      const int j = q >> 2, c0 = (q & 3) * 4, i = m >> 4, r = m & 15;
+      const int n = (blockIdx.x * TN + j) * 16 + c0;
+      if (n >= N) continue;
+      float v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int ln = c0 + u + 16 * (r >> 2);
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < KS; ++w)
+          sum += __builtin_bit_cast(
+              float, lds_ld32((uint32_t)(((((w * TN + j) * MTD + i) * 64 + ln) * 4 + (r & 3)) * 4)));
+        v[u] = sum;
+      }
+      const uint32_t off = (uint32_t)((((int64_t)blockIdx.y * M + m) * N + n) * 4);
+      if (vec) {
+        __builtin_amdgcn_raw_buffer_store_b128(
+            u32x4v{__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
+                   __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3])},
+            prs, off, 0, kBufSC1);
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (n + u < N)
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v[u]), prs,
+                                                  off + 4u * u, 0, kBufSC1);
+      }
+    }
+    // Once the stores have completed (vmcnt(0) counts stores on this
+    // architecture) the group is counted in; the workgroup that brings the
+    // count to gridDim.y adds all the groups. (A device-scope fence instead
+    // writes back and invalidates the whole XCD's L2 once per wave: 6x slower
+    // at M = 16.)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    const uint32_t flag = (uint32_t)(NW * MTD * 64 * 16);  // LDS word past the reduction buffer
+    if (tid == 0) {
+      const uint32_t done = atomicAdd(&cnt[blockIdx.x], 1u);
+      lds_st32(flag, done + 1 == gridDim.y ? 1u : 0u);
+    }
+    __syncthreads();
+    if (lds_ld32(flag) == 0) return;  // uniform: not the last group
+    const int G = gridDim.y;
+    for (int o = tid; o < M * nq; o += NW * 64) {
+      const int m = o / nq, q = o - m * nq;
+      const int n = (blockIdx.x * TN + (q >> 2)) * 16 + (q & 3) * 4;
+      if (n >= N) continue;
+      const uint32_t off0 = (uint32_t)(((int64_t)m * N + n) * 4);
+      const uint32_t gstep = (uint32_t)(slab * 4);
+      // groups in order 0, 1, .., eight loads in flight (coherent sc1 reads:
+      // the other groups' partials, never a stale line of this XCD's L2)
+      float a[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int g0 = 0; g0 < G; g0 += 8) {
+        u32x4v t[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          if (g0 + k < G) {
+            const uint32_t off = off0 + (uint32_t)(g0 + k) * gstep;
+            if (vec) {
+              t[k] = __builtin_bit_cast(u32x4v,
+                                        __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, kBufSC1));
+            } else {
+#pragma unroll
+              for (int u = 0; u < 4; ++u)
+                t[k][u] = n + u < N ? __builtin_amdgcn_raw_buffer_load_b32(prs, off + 4u * u, 0, kBufSC1)
+                                    : 0u;
+            }
+          }
+        }
+        // (bit_cast of a whole vector: this compiler reads element 0 when a
+        // bit_cast is applied to a vector element)
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (g0 + k < G) {
+            const float4v tf = __builtin_bit_cast(float4v, t[k]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) a[u] += tf[u];
+          }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (n + u < N)
+          reinterpret_cast<uint16_t*>(y)[(int64_t)m * ldy + n + u] = out16(a[u], bias, n + u, ybf);
+    }
+    if (tid == 0) __hip_atomic_store(&cnt[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -466,7 +563,7 @@ static int dec_mtd(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : 4; }
 
 static size_t dec_lds(bool nibble, int M, int nb, int n_levels, int nw) {
   size_t lds = (size_t)table_entries(nibble, n_levels) * 256 + (size_t)M * (nb * 256 + 16);
-  const size_t red = (size_t)nw * dec_mtd(M) * 64 * 16;
+  const size_t red = (size_t)nw * dec_mtd(M) * 64 * 16 + 16;  // + the K split's last-group flag
   return lds < red ? red : lds;
 }
 
@@ -501,15 +598,9 @@ static int launch_dec(const DecArgs& a, hipStream_t st, int groups = 1) {
     ctv.v[i] = w;
   }
   kern<<<dim3(tiles, groups), dim3(NW * 64), lds, st>>>(
-      a.codes, a.norms, a.ct, a.n_levels, 0x01010101u * mb, a.x, a.ldx, SPLIT ? a.ws : a.y, a.ldy,
-      a.bias, a.M, a.N, a.nb, xs_addr, a.lay, ctv, (a.xbf ? 1 : 0) | (a.ybf ? 2 : 0));
-  if constexpr (SPLIT) {
-    if (int rc = launch_status()) return rc;
-    const int64_t total = (int64_t)a.M * a.N;
-    dec_split_reduce_kernel<<<dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st>>>(
-        reinterpret_cast<const float*>(a.ws), groups, a.M, a.N, a.bias,
-        reinterpret_cast<uint16_t*>(a.y), a.ldy, a.ybf);
-  }
+      a.codes, a.norms, a.ct, a.n_levels, 0x01010101u * mb, a.x, a.ldx, a.y, a.ldy, a.bias, a.M,
+      a.N, a.nb, xs_addr, a.lay, ctv, (a.xbf ? 1 : 0) | (a.ybf ? 2 : 0),
+      SPLIT ? reinterpret_cast<float*>(a.ws) : nullptr, SPLIT ? a.cnt : nullptr);
   return launch_status();
 }
 
@@ -566,6 +657,7 @@ static int dec_split_groups(bool nibble, int M, int N, int nb, int n_levels) {
   const int wgn = ((N + 15) / 16 + kSplitTN - 1) / kSplitTN;
   // at most one round of workgroups (one per CU: the LDS holds one): a 257th
   // workgroup would run as a second round of its own
+  if (wgn > kWsCounters) return 0;  // one completion counter per row group
   int G = num_cus() / wgn;
   if (G > nb) G = nb;
   if (M > 16) {
@@ -575,6 +667,8 @@ static int dec_split_groups(bool nibble, int M, int N, int nb, int n_levels) {
       ++G;
   }
   if (G < 2) return 0;
+  // the partial sums are addressed through a buffer resource (31-bit offsets)
+  if ((int64_t)G * M * N * 4 >= ((int64_t)1 << 31)) return 0;
   const int nbg = (nb + G - 1) / G;
   if (dec_xc(M, nbg, kDecW) > 8 || dec_lds(nibble, M, nbg, n_levels, kDecW) > 160 * 1024) return 0;
   return G;
@@ -593,7 +687,7 @@ static bool dec_use_split(bool nibble, int M, int N, int nb, int n_levels) {
 template <bool NIB, bool XRAW, bool MASK>
 static int launch_dec_split(const DecArgs& a, hipStream_t st) {
   const int G = dec_split_groups(NIB, a.M, a.N, a.nb, a.n_levels);
-  if (!a.ws || a.ws_bytes < (size_t)G * a.M * a.N * 4) return PE_ERR_WORKSPACE;
+  if (!a.ws || !a.cnt || a.ws_bytes < (size_t)G * a.M * a.N * 4) return PE_ERR_WORKSPACE;
   const int xc = dec_xc(a.M, (a.nb + G - 1) / G, kDecW);
   const int mtd = dec_mtd(a.M);
   if (mtd > 1) {  // two m-tiles (kDecMaxRows = 32): activation registers 4 or 8

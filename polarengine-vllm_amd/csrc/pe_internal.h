@@ -121,11 +121,14 @@ struct DecArgs {
   size_t ws_bytes;
   int xbf = 0;           // raw x is bfloat16 (else fp16)
   int ybf = 0;           // y and bias are bfloat16 (else fp16)
+  uint32_t* cnt = nullptr;  // K split: completion counters (zero; left zero)
 };
 bool gemv_mfma_fits(bool nibble, int M, int N, int nb, int n_levels);
 // y[m, n] = fp16(sum over g = 0.. G-1 in order of part[g][m][n]) (+ fp16 bias)
 int split_reduce(const float* part, int G, int M, int N, const uint16_t* bias, void* y, int64_t ldy,
                  hipStream_t st, bool ybf = false);
+// bytes of fp32 partial sums of the K-split path (0 when it does not split);
+// the counters come on top (kWsCounterBytes, see above)
 size_t gemv_mfma_workspace(bool nibble, int M, int N, int nb, int n_levels);
 int gemv_mfma(bool nibble, bool xraw, const DecArgs& a, hipStream_t st);
 
@@ -144,5 +147,13 @@ int fwht128(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t ldx,
 int repack_pair(const float* x, int64_t rows, int64_t cols, void* y, hipStream_t st);
 
 inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Every workspace of this library starts with a block of completion counters
+// (one 32-bit word per group of workgroups that meet in a K split: the last
+// one to finish adds the partial sums). The block must be zero before the
+// workspace's first use; every call leaves it zero again, and no entry point
+// writes anything else into it, so one buffer can serve every entry point.
+constexpr size_t kWsCounterBytes = 4096;
+constexpr int kWsCounters = (int)(kWsCounterBytes / 4);
 
 }  // namespace pe

@@ -44,9 +44,12 @@ enum LinearRoute {
   LR_GEMV1 = 1,   // M = 1, row-major weights, K within the gemv1 LDS budget (raw x only)
   LR_MM = 2       // [FWHT-128 into the workspace], then the small-M / prefill matmul
 };
+// Workspace layout: [kWsCounterBytes of counters][pair-f16 x_tf (raw-x MM
+// route)][fp32 partial sums of a K split]; no workspace at all when the path
+// needs neither x_tf nor partials.
 struct LinearPlan {
   int route;
-  size_t xtf_bytes;  // pair-f16 x_tf at the workspace start (raw-x MM route only)
+  size_t xtf_bytes;  // pair-f16 x_tf after the counters (raw-x MM route only)
   size_t ws_bytes;   // total workspace
 };
 
@@ -54,12 +57,14 @@ static LinearPlan plan_linear(bool raw_x, int64_t M, int kp, int out_f, int bits
   const bool nib = (packed & PE_PACK_NIBBLE) != 0 && bits <= 4;
   const bool tiled = (packed & PE_LAYOUT_TILE16) != 0;
   const int nb = kp / kBlock, n_levels = 1 << bits;
+  auto with_counters = [](size_t data) { return data ? kWsCounterBytes + data : 0; };
   if (M >= 1 && M <= kDecMaxRows && gemv_mfma_fits(nib, (int)M, out_f, nb, n_levels))
-    return LinearPlan{LR_DECODE, 0,
-                      round_up(gemv_mfma_workspace(nib, (int)M, out_f, nb, n_levels), 256)};
+    return LinearPlan{LR_DECODE, 0, with_counters(round_up(
+                                        gemv_mfma_workspace(nib, (int)M, out_f, nb, n_levels), 256))};
   if (raw_x && M == 1 && !tiled && kp <= gemv1_max_kp(nib)) return LinearPlan{LR_GEMV1, 0, 0};
   const size_t xtf = raw_x ? round_up((size_t)M * kp * 2, 256) : 0;
-  return LinearPlan{LR_MM, xtf, xtf + round_up(mm_xtf_workspace(nib, M, out_f, nb), 256)};
+  return LinearPlan{LR_MM, xtf,
+                    with_counters(xtf + round_up(mm_xtf_workspace(nib, M, out_f, nb), 256))};
 }
 
 static bool plan_args_ok(int64_t M, int kp, int out_f, int bits) {
@@ -102,16 +107,19 @@ extern "C" int pe_linear_forward_xtf(const void* x_tf_pair, int64_t M, int in_f_
   const LinearPlan plan = plan_linear(false, M, in_f_padded, out_f, bits, packed);
   if (plan.ws_bytes && (!workspace || workspace_bytes < plan.ws_bytes)) return PE_ERR_WORKSPACE;
   if (workspace && !aligned16(workspace)) return PE_ERR_ALIGN;
+  uint32_t* cnt = reinterpret_cast<uint32_t*>(workspace);
+  char* data = plan.ws_bytes ? reinterpret_cast<char*>(workspace) + kWsCounterBytes : nullptr;
+  const size_t data_bytes = plan.ws_bytes ? workspace_bytes - kWsCounterBytes : 0;
   if (plan.route == LR_DECODE) {
     DecArgs a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels,
               x_tf_pair, (int64_t)in_f_padded, y, out_f, reinterpret_cast<const uint16_t*>(bias),
-              (int)M, out_f, nb, wlayout(nib, tiled, nb), ct_host, workspace, workspace_bytes,
-              0, ybf};
+              (int)M, out_f, nb, wlayout(nib, tiled, nb), ct_host, data, data_bytes,
+              0, ybf, cnt};
     return gemv_mfma(nib, false, a, st);
   }
   return mm_xtf(nib, tiled, codes, norms_f16, ct_scaled, n_levels, x_tf_pair, M, out_f, nb, y,
-                OM_F16, out_f, reinterpret_cast<const uint16_t*>(bias), workspace,
-                workspace_bytes, st, ybf != 0);
+                OM_F16, out_f, reinterpret_cast<const uint16_t*>(bias), data, data_bytes, st,
+                ybf != 0);
 }
 
 extern "C" int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f, int64_t ldx,
@@ -138,10 +146,13 @@ extern "C" int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f
   if (plan.ws_bytes && (!workspace || workspace_bytes < plan.ws_bytes)) return PE_ERR_WORKSPACE;
   if (workspace && !aligned16(workspace)) return PE_ERR_ALIGN;
   const uint16_t* b16 = reinterpret_cast<const uint16_t*>(bias);
+  uint32_t* cnt = reinterpret_cast<uint32_t*>(workspace);
+  char* data = plan.ws_bytes ? reinterpret_cast<char*>(workspace) + kWsCounterBytes : nullptr;
+  const size_t data_bytes = plan.ws_bytes ? workspace_bytes - kWsCounterBytes : 0;
   if (plan.route == LR_DECODE) {
     DecArgs a{reinterpret_cast<const uint8_t*>(codes), norms_f16, ct_scaled, n_levels, x, ldx, y,
-              out_f, b16, (int)M, out_f, nb, wlayout(nib, tiled, nb), ct_host, workspace,
-              workspace_bytes, xbf, xbf};
+              out_f, b16, (int)M, out_f, nb, wlayout(nib, tiled, nb), ct_host, data, data_bytes,
+              xbf, xbf, cnt};
     return gemv_mfma(nib, true, a, st);
   }
   if (plan.route == LR_GEMV1) {
@@ -149,19 +160,18 @@ extern "C" int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f
                 b16, out_f, nb, xbf, xbf};
     return gemv1(nib, XM_RAW_F16, OM_F16, a, st);
   }
-  char* ws = reinterpret_cast<char*>(workspace);
-  if (int rc = fwht128(x, x_dtype, M, in_f, ldx, ws, PE_XTF_PAIR_F16, st)) return rc;
-  return mm_xtf(nib, tiled, codes, norms_f16, ct_scaled, n_levels, ws, M, out_f, nb, y, OM_F16,
-                out_f, b16, ws + plan.xtf_bytes, workspace_bytes - plan.xtf_bytes, st, xbf != 0);
+  if (int rc = fwht128(x, x_dtype, M, in_f, ldx, data, PE_XTF_PAIR_F16, st)) return rc;
+  return mm_xtf(nib, tiled, codes, norms_f16, ct_scaled, n_levels, data, M, out_f, nb, y, OM_F16,
+                out_f, b16, data + plan.xtf_bytes, data_bytes - plan.xtf_bytes, st, xbf != 0);
 }
 
-// Workspace of pe_polar_matmul: the fp32 x_tf repacked to pair f16, except at
-// M = 1 when the GEMV takes x_tf directly (K within its LDS budget for either
-// code format: int8 is the smaller bound).
+// Workspace of pe_polar_matmul: the counter block, then the fp32 x_tf
+// repacked to pair f16; none at M = 1 when the GEMV takes x_tf directly (K
+// within its LDS budget for either code format: int8 is the smaller bound).
 extern "C" size_t pe_polar_matmul_workspace_size(int64_t M, int in_f_padded) {
   if (M <= 0 || in_f_padded <= 0) return 0;
   if (M == 1 && in_f_padded <= gemv1_max_kp(false)) return 0;
-  return round_up((size_t)M * in_f_padded * 2, 256);
+  return kWsCounterBytes + round_up((size_t)M * in_f_padded * 2, 256);
 }
 
 extern "C" int pe_polar_matmul(const void* codes, int packed, const float* x_tf, int64_t M,
@@ -183,10 +193,10 @@ extern "C" int pe_polar_matmul(const void* codes, int packed, const float* x_tf,
     return gemv1(nib, XM_XTF_F32, OM_F32, a, st);
   }
   const size_t need = round_up((size_t)M * in_f_padded * 2, 256);
-  if (!workspace || workspace_bytes < need) return PE_ERR_WORKSPACE;
+  if (!workspace || workspace_bytes < kWsCounterBytes + need) return PE_ERR_WORKSPACE;
   if (!aligned16(workspace)) return PE_ERR_ALIGN;
-  if (int rc = repack_pair(x_tf, M, in_f_padded, workspace, st)) return rc;
-  char* ws = reinterpret_cast<char*>(workspace);
+  char* ws = reinterpret_cast<char*>(workspace) + kWsCounterBytes;
+  if (int rc = repack_pair(x_tf, M, in_f_padded, ws, st)) return rc;
   return mm_xtf(nib, false, codes, norms_f16, ct_scaled, n_levels, ws, M, out_f, nb, out, OM_F32,
-                out_f, nullptr, ws + need, workspace_bytes - need, st);
+                out_f, nullptr, ws + need, workspace_bytes - kWsCounterBytes - need, st);
 }

@@ -294,7 +294,7 @@ static MoeWs moe_ws_layout(int64_t T, int top_k, int E, int H, int I) {
   const int64_t P = T * top_k;
   const int64_t Ip = (I + kBlock - 1) / kBlock * kBlock;
   MoeWs w{};
-  size_t o = 0;
+  size_t o = kWsCounterBytes;  // the library-wide counter block stays untouched
   auto take = [&](size_t bytes) {
     const size_t at = o;
     o += round_up(bytes, 256);

@@ -133,12 +133,14 @@ _WS_CACHE: dict = {}
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Per-device, per-stream growable workspace (uint8), reused across calls."""
+    """Per-device, per-stream growable workspace (uint8), reused across calls.
+    Zero-filled when allocated: the library keeps completion counters in its
+    first 4 KB, which must start at zero and which every call leaves zero."""
     if nbytes <= 0:
         return None
     key = (device, torch.cuda.current_stream(device).cuda_stream)
     buf = _WS_CACHE.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _WS_CACHE[key] = buf
     return buf

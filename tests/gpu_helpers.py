@@ -81,7 +81,7 @@ def linear_call(x, codes, norms, ct, bits, fmt, n, bias=None, ws_extra=0):
     m, k = x.shape
     code = _lib.act_dtype(x)
     wsb = L.pe_linear_workspace_size(m, k, n, bits, fmt)
-    ws = torch.empty(wsb + ws_extra, dtype=torch.uint8, device=DEV) if wsb + ws_extra else None
+    ws = torch.zeros(wsb + ws_extra, dtype=torch.uint8, device=DEV) if wsb + ws_extra else None
     y = torch.empty(m, n, dtype=x.dtype, device=DEV)
     cd = ct if isinstance(ct, torch.Tensor) else to_dev(np.asarray(ct, dtype=np.float32))
     ct_host = np.ascontiguousarray(cd.cpu().numpy(), dtype=np.float32)

@@ -101,7 +101,7 @@ def test_bf16_xtf_entry_and_fp32_input():
     fmt = _lib.PE_PACK_NIBBLE | _lib.PE_LAYOUT_TILE16
     L = _lib.lib()
     wsb = L.pe_linear_xtf_workspace_size(m, k, n, bits, fmt)
-    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+    ws = torch.zeros(max(wsb, 1), dtype=torch.uint8, device=DEV)
     y = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
     cd = to_dev(ct)
     rc = L.pe_linear_forward_xtf(xt.data_ptr(), m, k, dcodes.data_ptr(), bits, fmt,

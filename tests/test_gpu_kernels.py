@@ -247,7 +247,7 @@ def test_decode_linear_forward(m, n, k, bits):
     xd, nd, cd, bd = to_dev(xb), to_dev(norms), to_dev(ct), to_dev(bias)
     L = _lib.lib()
     wsb = L.pe_linear_workspace_size(m, k, n, bits, int(nib))
-    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+    ws = torch.zeros(max(wsb, 1), dtype=torch.uint8, device=DEV)
     ct_host = np.ascontiguousarray(ct, dtype=np.float32)  # codebook by value
     outs = []
     for host in (None, ct_host.ctypes.data, None):
@@ -279,7 +279,7 @@ def test_decode_linear_forward_xtf(m, n, k, bits):
     xp, nd, cd = to_dev(pair_f16(x_tf)), to_dev(norms), to_dev(ct)
     L = _lib.lib()
     wsb = L.pe_linear_xtf_workspace_size(m, k, n, bits, int(nib))
-    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+    ws = torch.zeros(max(wsb, 1), dtype=torch.uint8, device=DEV)
     y = torch.empty(m, n, dtype=torch.float16, device=DEV)
     rc = L.pe_linear_forward_xtf(xp.data_ptr(), m, k, dcodes.data_ptr(), bits, int(nib),
                                  nd.data_ptr(), cd.data_ptr(), None, 1 << bits, None, 0,
@@ -383,7 +383,7 @@ def test_linear_forward_tiled_layout(m, n, k, bits):
     xd, cd, bd = to_dev(x), to_dev(ct), to_dev(bias)
     L = _lib.lib()
     wsb = L.pe_linear_workspace_size(m, k, n, bits, fmt)
-    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+    ws = torch.zeros(max(wsb, 1), dtype=torch.uint8, device=DEV)
     y = torch.empty(m, n, dtype=torch.float16, device=DEV)
     ct_host = np.ascontiguousarray(ct, dtype=np.float32)
     rc = L.pe_linear_forward(xd.data_ptr(), 0, m, k, k, dcodes.data_ptr(), bits, fmt,
@@ -435,7 +435,7 @@ def test_prefill_gemm_full_size_row_sample(m, n, k, bits):
     y = torch.empty(m, n, dtype=torch.float16, device=DEV)
     L = _lib.lib()
     wsb = L.pe_linear_workspace_size(m, k, n, bits, int(nib))
-    ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+    ws = torch.zeros(wsb, dtype=torch.uint8, device=DEV)
     xd, nd, cd = to_dev(x), to_dev(norms), to_dev(ct)
     rc = L.pe_linear_forward(xd.data_ptr(), 0, m, k, k, dcodes.data_ptr(), bits, int(nib),
                              nd.data_ptr(), cd.data_ptr(), None, 1 << bits, None,
@@ -469,7 +469,7 @@ def test_prefill_ksplit_row_sample(m, n, k, bits):
     dcodes, nib = dev_codes(codes, bits)
     L = _lib.lib()
     wsb = L.pe_linear_workspace_size(m, k, n, bits, int(nib))
-    ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+    ws = torch.zeros(wsb, dtype=torch.uint8, device=DEV)
     xd, nd, cd, bd = to_dev(x), to_dev(norms), to_dev(ct), to_dev(bias)
     outs = []
     for _ in range(2):
@@ -517,7 +517,7 @@ def test_four_wave_prefill_row_sample(m, n, k, bits, out, with_bias, tiled):
     if out == "f16":
         y = torch.empty(m, n, dtype=torch.float16, device=DEV)
         wsb = L.pe_linear_workspace_size(m, k, n, bits, fmt)
-        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+        ws = torch.zeros(max(wsb, 1), dtype=torch.uint8, device=DEV)
         xd = to_dev(x)
         bd = to_dev(bias) if with_bias else None
         rc = L.pe_linear_forward(xd.data_ptr(), 0, m, k, k, dcodes.data_ptr(), bits, fmt,
@@ -535,7 +535,7 @@ def test_four_wave_prefill_row_sample(m, n, k, bits, out, with_bias, tiled):
         y = torch.empty(m, n, dtype=torch.float32, device=DEV)
         xt = to_dev(x_tf)
         wsb = L.pe_polar_matmul_workspace_size(m, k)
-        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+        ws = torch.zeros(max(wsb, 1), dtype=torch.uint8, device=DEV)
         rc = L.pe_polar_matmul(dcodes.data_ptr(), int(nib), xt.data_ptr(), m, dnorms.data_ptr(),
                                cd.data_ptr(), 1 << bits, y.data_ptr(), n, k,
                                ws.data_ptr(), wsb, _lib.stream_ptr(torch.device(DEV)))
@@ -621,7 +621,7 @@ def test_graph_replay_matches_eager():
         x = to_dev(O.seeded_normal((m, k), 1.0, 50 + m))
         y = torch.empty(m, n, dtype=torch.float16, device=DEV)
         wsb = L.pe_linear_workspace_size(m, k, n, bits, int(nib))
-        ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=DEV)
+        ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=DEV)
         args = (x, dcodes, to_dev(norms), to_dev(ct), y, ws, wsb, m, n, k, bits, nib)
         cases.append(args)
 
