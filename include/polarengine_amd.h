@@ -53,7 +53,9 @@ enum {
   PE_ERR_DTYPE = 5,     /* unsupported dtype or layout code                   */
   PE_ERR_WORKSPACE = 6, /* workspace NULL or smaller than the size query      */
   PE_ERR_LAUNCH = 7,    /* hipGetLastError reported a launch failure          */
-  PE_ERR_DEVICE = 8     /* device query failed                                */
+  PE_ERR_DEVICE = 8,    /* device query failed                                */
+  PE_ERR_SCRATCH = 9    /* call larger than the allocation-free entry point's
+                           static scratch (pe_linear_noalloc_max_bytes)       */
 };
 
 /* ---- weight format flags (the `packed` argument of the linear entry points) */
@@ -154,6 +156,27 @@ int pe_linear_forward(const void* x, int x_dtype, int64_t M, int in_f, int64_t l
                       const float* ct_scaled, const float* ct_host, int n_levels,
                       const void* bias, void* y, int out_f, void* workspace,
                       size_t workspace_bytes, void* stream);
+
+/*
+ * Allocation-free form of pe_linear_forward. No counterpart in the reference:
+ * it is for callers that cannot allocate or own a workspace (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments and results as pe_linear_forward without the workspace; the
+ * library uses a static device array of pe_linear_noalloc_max_bytes() bytes
+ * (32 MiB) per GPU instead, reserved when the library's code object loads on
+ * that GPU and held until the process ends. A call whose path needs more
+ * (pe_linear_workspace_size above that limit, e.g. a long prefill) returns
+ * PE_ERR_SCRATCH and launches nothing. Every call on one GPU uses the same
+ * array: calls that overlap on one GPU (other streams, other threads) race;
+ * calls ordered on one stream do not. The array keeps the last call's
+ * contents; the counters it needs at zero start at zero and every call
+ * leaves them zero.
+ */
+size_t pe_linear_noalloc_max_bytes(void);
+int pe_linear_forward_noalloc(const void* x, int x_dtype, int64_t M, int in_f, int64_t ldx,
+                              const void* codes, int bits, int packed, const uint16_t* norms_f16,
+                              const float* ct_scaled, const float* ct_host, int n_levels,
+                              const void* bias, void* y, int out_f, void* stream);
 
 /*
  * Same, starting from an already-transformed activation in the pair-f16

@@ -37,6 +37,9 @@ extern "C" const char* pe_status_string(int status) {
     case PE_ERR_WORKSPACE: return "workspace missing or too small";
     case PE_ERR_LAUNCH: return "kernel launch failed";
     case PE_ERR_DEVICE: return "device query failed";
+    case PE_ERR_SCRATCH:
+      return "the call needs more scratch than pe_linear_forward_noalloc holds "
+             "(pe_linear_noalloc_max_bytes)";
     default: return "unknown status";
   }
 }

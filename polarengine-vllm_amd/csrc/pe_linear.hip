@@ -20,6 +20,8 @@
 // The reference routes M = 1 to split-K GEMV and every M > 1 to its Triton
 // GEMM; results are the same function either way.
 
+#include <mutex>
+
 #include "pe_internal.h"
 
 namespace pe {
@@ -199,4 +201,59 @@ extern "C" int pe_polar_matmul(const void* codes, int packed, const float* x_tf,
   if (int rc = repack_pair(x_tf, M, in_f_padded, ws, st)) return rc;
   return mm_xtf(nib, false, codes, norms_f16, ct_scaled, n_levels, ws, M, out_f, nb, out, OM_F32,
                 out_f, nullptr, ws + need, workspace_bytes - kWsCounterBytes - need, st);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant of pe_linear_forward (no counterpart in the
+// reference): the workspace is a static device array, one per GPU, that the
+// code object reserves when it loads. Its first kWsCounterBytes are the
+// completion counters (zero when the module loads; every call leaves them
+// zero), the rest holds whatever the call's path needs (pair-f16 x_tf, fp32
+// partial sums). Calls on one GPU share it, so calls that overlap on one GPU
+// (concurrent streams, threads) race.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace pe {
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices];  // device address of `scratch` per device
+
+// The scratch array's device address on the current device, looked up once
+// per device (the array's name is a host-side stand-in, never an address).
+int scratch_address(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return PE_ERR_DEVICE;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return PE_ERR_DEVICE;
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return PE_OK;
+}
+}  // namespace
+}  // namespace pe
+
+extern "C" size_t pe_linear_noalloc_max_bytes(void) { return kScratchBytes; }
+
+extern "C" int pe_linear_forward_noalloc(const void* x, int x_dtype, int64_t M, int in_f,
+                                         int64_t ldx, const void* codes, int bits, int packed,
+                                         const uint16_t* norms_f16, const float* ct_scaled,
+                                         const float* ct_host, int n_levels, const void* bias,
+                                         void* y, int out_f, void* stream) {
+  // the path's workspace, by the rule pe_linear_forward applies (0 for
+  // arguments it rejects: the call below then returns that error)
+  const size_t need = pe_linear_workspace_size(M, in_f, out_f, bits, packed);
+  if (need > kScratchBytes) return PE_ERR_SCRATCH;
+  void* ws = nullptr;
+  if (need) {
+    if (int rc = scratch_address(&ws)) return rc;
+  }
+  return pe_linear_forward(x, x_dtype, M, in_f, ldx, codes, bits, packed, norms_f16, ct_scaled,
+                           ct_host, n_levels, bias, y, out_f, ws, need ? kScratchBytes : 0,
+                           stream);
 }

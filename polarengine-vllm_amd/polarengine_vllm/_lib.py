@@ -23,6 +23,7 @@ PE_OK = 0
 # status codes of include/polarengine_amd.h
 PE_ERR_NULL, PE_ERR_DIMS, PE_ERR_BITS, PE_ERR_ALIGN = 1, 2, 3, 4
 PE_ERR_DTYPE, PE_ERR_WORKSPACE, PE_ERR_LAUNCH, PE_ERR_DEVICE = 5, 6, 7, 8
+PE_ERR_SCRATCH = 9
 PE_PACK_NIBBLE, PE_LAYOUT_TILE16 = 1, 2
 PE_DTYPE_F16, PE_DTYPE_BF16, PE_DTYPE_F32 = 0, 1, 2
 PE_XTF_F32, PE_XTF_F16, PE_XTF_PAIR_F16, PE_XTF_BF16 = 0, 1, 2, 3
@@ -42,6 +43,9 @@ _SIGNATURES = {
     "pe_linear_workspace_size": (_c_sz, [_c_i64, _c_int, _c_int, _c_int, _c_int]),
     "pe_linear_forward": (_c_int, [_vp, _c_int, _c_i64, _c_int, _c_i64, _vp, _c_int, _c_int, _vp,
                                    _vp, _vp, _c_int, _vp, _vp, _c_int, _vp, _c_sz, _vp]),
+    "pe_linear_noalloc_max_bytes": (_c_sz, []),
+    "pe_linear_forward_noalloc": (_c_int, [_vp, _c_int, _c_i64, _c_int, _c_i64, _vp, _c_int,
+                                           _c_int, _vp, _vp, _vp, _c_int, _vp, _vp, _c_int, _vp]),
     "pe_linear_xtf_workspace_size": (_c_sz, [_c_i64, _c_int, _c_int, _c_int, _c_int]),
     "pe_linear_forward_xtf": (_c_int, [_vp, _c_i64, _c_int, _vp, _c_int, _c_int, _vp, _vp, _vp,
                                        _c_int, _vp, _c_int, _vp, _c_int, _vp, _c_sz, _vp]),
