@@ -1,18 +1,19 @@
 """Benchmark of the PolarEngine quantized-linear hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--repeats R]
 
 Headline (BASELINE.json metric): the Q4 12288x4096 M=1 decode linear --
 FWHT-128 of x fused into the nibble GEMV, fp16 in / fp16 out -- as HBM GB/s
 (algorithmic bytes / time) and us/call. One "step" is one call. Weights
 rotate over 16 independent copies (416 MB > the 256 MB Infinity Cache) so
-reads come from HBM; calls are captured in a HIP graph and replayed so the
-host does not gate the ~4 us kernels. Also measured: the same call with one
-weight copy (cache-hot), the M=2048 prefill GEMM (TFLOP/s vs dense fp16 MFMA
-peak), M=4/8/16 decode, the gate/up Q3 12288x4096 and down Q4 4096x12288 decode
-shapes at M=1 and 16, the Q3 4096x12288 prefill, KV-cache quantize / dequantize,
-the grouped MoE experts, and the oracle's CPU time for the headline call
-(cpu_baseline, numpy, 1 thread) on a bounded sample.
+reads come from HBM. W untimed calls first; then R samples, each exactly K
+calls captured in one HIP graph and replayed between two synchronizes, HIP
+events on the replay stream; the line reports the median sample. Also
+measured (under "extra"): the same call with one weight copy (cache-hot),
+batched decode on the headline and MLP shapes, C1 (Q5 4096x4096 M=1), the
+prefill GEMMs (TFLOP/s vs dense fp16 MFMA peak), the C4 decoder layer's
+linears at M=1 and M=512, KV-cache quantize / dequantize, the grouped MoE
+experts; and the oracle's CPU time on the host's cores (cpu_baseline).
 """
 
 from __future__ import annotations
@@ -92,33 +93,43 @@ class Linear:
             _lib.check(rc, "pe_linear_forward")
 
 
-def time_graph(calls, reps_per_graph, warmup, steps, dev):
-    """Capture `reps_per_graph` rounds over `calls` in one graph; replay.
-    Returns seconds per call."""
+def time_steps(calls, steps, warmup, dev, repeats=1):
+    """Exactly `steps` calls per timed sample (cycling through `calls`),
+    captured in one HIP graph and replayed on the current stream; `warmup`
+    untimed eager calls (at least one per call object) and one untimed replay
+    first. Each sample is bracketed by synchronize, with HIP events on the
+    replay stream. Returns (median seconds per call, per-sample list)."""
     s = torch.cuda.Stream(device=dev)
     s.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(s):
-        for c in calls:  # eager warm-up (attribute setup, first launches)
-            c()
+        for i in range(max(warmup, len(calls))):
+            calls[i % len(calls)]()
     torch.cuda.current_stream(dev).wait_stream(s)
     torch.cuda.synchronize(dev)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
-        for _ in range(reps_per_graph):
-            for c in calls:
-                c()
-    per_graph = reps_per_graph * len(calls)
-    n_replays = max(1, steps // per_graph)
-    for _ in range(max(1, warmup // per_graph)):
-        g.replay()
+        for i in range(steps):
+            calls[i % len(calls)]()
+    g.replay()
     torch.cuda.synchronize(dev)
+    samples = []
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(n_replays):
+    for _ in range(repeats):
+        torch.cuda.synchronize(dev)
+        e0.record()
         g.replay()
-    e1.record()
-    torch.cuda.synchronize(dev)
-    return e0.elapsed_time(e1) * 1e-3 / (n_replays * per_graph), n_replays * per_graph
+        e1.record()
+        torch.cuda.synchronize(dev)
+        samples.append(e0.elapsed_time(e1) * 1e-3 / steps)
+    return float(np.median(samples)), samples
+
+
+def time_graph(calls, reps_per_graph, warmup, steps, dev):
+    """Extras: about `steps` calls per sample in whole rounds over `calls`,
+    median of five samples. Returns (seconds per call, calls per sample)."""
+    n = max(len(calls), (steps // len(calls)) * len(calls))
+    t, _ = time_steps(calls, n, warmup, dev, repeats=5)
+    return t, n
 
 
 def time_eager(fn, warmup, steps, dev):
@@ -190,34 +201,74 @@ def moe_extra(dev, t=128, e=64, h=2048, inter=1408, k=8, b13=3, b2=4):
                                   "includes": "routing + x FWHT with expert bucketing + w13 SwiGLU (FWHT of h fused) + w2 + combine"}}
 
 
-def cpu_baseline(budget_s=15.0):
-    """Oracle per-call path of the headline config on the host, 1 thread."""
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_time(fn, budget_s, min_runs=20):
+    """Median seconds per call over at least `min_runs` runs (or as many as
+    fit in budget_s), after 3 warm-up calls."""
+    for _ in range(3):
+        fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_runs or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= min_runs and time.perf_counter() >= t_end:
+            break
+        if len(times) >= 4 * min_runs:
+            break
+    return float(np.median(times)), len(times)
+
+
+def cpu_baseline(budget_s=20.0):
+    """The oracle (numpy restatement of the reference's CPU-capable path) on
+    the host's affinity cores, two lines per config: (i) the reference
+    per-call path (x.float() -> FWHT -> Hadamard-domain product -> .half()),
+    (ii) dense dequantize-then-matmul with W materialised once (only x @ W.T
+    timed); on the headline config (Q4 12288x4096 M=1) and C1 (Q5 4096x4096
+    M=1). `value` is line (i) on the headline config."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import polar_oracle as O
-    try:
-        from threadpoolctl import threadpool_limits
-        limiter = threadpool_limits(limits=1)
-    except Exception:
-        limiter = None
-    n, k, bits = 12288, 4096, 4
-    rng = np.random.default_rng(0)
-    codes = rng.integers(0, 16, (n, k)).astype(np.int8)
-    norms = (np.abs(rng.standard_normal((n, k // 128))) * 0.2 + 0.05).astype(np.float16)
-    ct = O.ct_scaled(bits)
-    x = O.seeded_normal((1, k), 1.0, 1)
-    O.linear_apply(x, codes, norms, ct, k)  # warm-up
-    t0 = time.perf_counter()
-    calls = 0
-    while time.perf_counter() - t0 < budget_s:
-        O.linear_apply(x, codes, norms, ct, k)
-        calls += 1
-    dt = (time.perf_counter() - t0) / calls
-    if limiter is not None:
-        limiter.unregister()
-    return {"value": round(algo_bytes(1, n, k, bits) / dt / 1e9, 4), "unit": "GB/s",
-            "us_per_call": round(dt * 1e6, 1), "cores": 1, "kind": "port",
-            "sample": f"oracle linear_apply (numpy fp32: FWHT, Hadamard-domain GEMV, fp16 cast) "
-                      f"Q4 {n}x{k} M=1, {calls} calls in {budget_s:.0f} s"}
+    from threadpoolctl import threadpool_limits
+    cores = len(os.sched_getaffinity(0))
+    lines = {}
+    with threadpool_limits(limits=cores):
+        for name, (n, k, bits), share in (("headline_q4_12288x4096_m1", (12288, 4096, 4), 0.4),
+                                          ("c1_q5_4096x4096_m1", (4096, 4096, 5), 0.3)):
+            rng = np.random.default_rng(0)
+            codes = rng.integers(0, 1 << bits, (n, k)).astype(np.int8)
+            norms = (np.abs(rng.standard_normal((n, k // 128))) * 0.2 + 0.05).astype(np.float16)
+            ct = O.ct_scaled(bits)
+            x = O.seeded_normal((1, k), 1.0, 1)
+            B = algo_bytes(1, n, k, bits)
+            t1, r1 = _cpu_time(lambda: O.linear_apply(x, codes, norms, ct, k), budget_s * share)
+            w = O.dequant_weight(codes, norms, ct)  # materialised once, not timed
+            t2, r2 = _cpu_time(lambda: O.dequant_matmul(x, w), budget_s * share / 3)
+            lines[name] = {
+                "per_call_path": {"us_per_call": round(t1 * 1e6, 1),
+                                  "GB/s": round(B / t1 / 1e9, 4), "runs": r1},
+                "dense_dequant_matmul": {"us_per_call": round(t2 * 1e6, 1),
+                                         "GB/s": round(B / t2 / 1e9, 4), "runs": r2},
+            }
+            del w
+    head = lines["headline_q4_12288x4096_m1"]["per_call_path"]
+    return {"value": head["GB/s"], "unit": "GB/s", "us_per_call": head["us_per_call"],
+            "cores": cores, "cpu": _cpu_model(), "kind": "port",
+            "sample": f"oracle on {cores} host threads (numpy/OpenBLAS, fp32): line (i) "
+                      "linear_apply per call (FWHT, Hadamard-domain GEMV, fp16 cast) and line (ii) "
+                      "x @ W.T with W dequantised once, median of >= 20 runs after 3 warm-ups, on "
+                      "the headline config (Q4 12288x4096 M=1) and C1 (Q5 4096x4096 M=1); value = "
+                      "line (i), headline",
+            "lines": lines}
 
 
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic_gemv_q4_12288x4096_m1.json")
@@ -299,26 +350,148 @@ def prefill_extra(dev):
     return out
 
 
+class DecoderLayerLinears:
+    """The seven linears of the C4 decoder layer (hidden 4096, 32 q / 8 kv
+    heads of 128, intermediate 12288): q/k/v Q5 sharing one transform of the
+    normed hidden state, o Q6, gate/up Q3 sharing one transform, down Q4;
+    tiled-16 weights. M = 1: seven pe_linear_forward calls (transform fused
+    into each decode GEMV). M > 1: pe_fwht128 once for q/k/v and once for
+    gate/up, pe_linear_forward_xtf for those five, pe_linear_forward for o and
+    down (their inputs are new activations)."""
+
+    SPECS = [("q", 4096, 4096, 5, "qkv"), ("k", 1024, 4096, 5, "qkv"), ("v", 1024, 4096, 5, "qkv"),
+             ("o", 4096, 4096, 6, "o"), ("gate", 12288, 4096, 3, "gu"), ("up", 12288, 4096, 3, "gu"),
+             ("down", 4096, 12288, 4, "down")]
+
+    def __init__(self, m, dev, seed):
+        from polarengine_vllm.packing import tile_weights_16
+        self.m, self.dev = m, dev
+        L = _lib.lib()
+        self.x = {g: torch.randn(m, 12288 if g == "down" else 4096, device=dev,
+                                 dtype=torch.float16) for g in ("qkv", "o", "gu", "down")}
+        self.xtf = {g: torch.empty(m, 2048, dtype=torch.int32, device=dev) for g in ("qkv", "gu")}
+        self.lin = []
+        wsb = 0
+        for i, (name, n, k, bits, grp) in enumerate(self.SPECS):
+            codes, norms, ct = make_layer(n, k, bits, dev, seed + i)
+            codes, norms = tile_weights_16(codes, norms)
+            fmt = (_lib.PE_PACK_NIBBLE if bits <= 4 else 0) | _lib.PE_LAYOUT_TILE16
+            ct_host = np.ascontiguousarray(ct.cpu().numpy(), dtype=np.float32)
+            y = torch.empty(m, n, dtype=torch.float16, device=dev)
+            self.lin.append((name, n, k, bits, grp, codes, norms, ct, ct_host, fmt, y))
+            wsb = max(wsb, L.pe_linear_workspace_size(m, k, n, bits, fmt),
+                      L.pe_linear_xtf_workspace_size(m, k, n, bits, fmt))
+        self.wsb = wsb
+        self.ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
+
+    def __call__(self):
+        L = _lib.lib()
+        st = _lib.stream_ptr(self.dev)
+        m = self.m
+        if m > 1:
+            for g in ("qkv", "gu"):
+                _lib.check(L.pe_fwht128(self.x[g].data_ptr(), 0, m, 4096, 4096, self.xtf[g].data_ptr(),
+                                        _lib.PE_XTF_PAIR_F16, st), "pe_fwht128")
+        for (name, n, k, bits, grp, codes, norms, ct, ct_host, fmt, y) in self.lin:
+            if m > 1 and grp in ("qkv", "gu"):
+                rc = L.pe_linear_forward_xtf(self.xtf[grp].data_ptr(), m, k, codes.data_ptr(), bits,
+                                             fmt, norms.data_ptr(), ct.data_ptr(), ct_host.ctypes.data,
+                                             1 << bits, None, 0, y.data_ptr(), n, self.ws.data_ptr(),
+                                             self.wsb, st)
+            else:
+                rc = L.pe_linear_forward(self.x[grp].data_ptr(), 0, m, k, k, codes.data_ptr(), bits,
+                                         fmt, norms.data_ptr(), ct.data_ptr(), ct_host.ctypes.data,
+                                         1 << bits, None, y.data_ptr(), n, self.ws.data_ptr(),
+                                         self.wsb, st)
+            if rc:
+                _lib.check(rc, f"decoder layer {name}")
+
+
+def decoder_layer_extra(dev):
+    """C4: the decoder layer's seven quantized linears at M = 1 (GB/s of the
+    120.6 MB of algorithmic bytes) and M = 512 (TFLOP/s of 197.6 GFLOP); four
+    layer copies in turn (482 MB > the 256 MB Infinity Cache)."""
+    out = {}
+    specs = DecoderLayerLinears.SPECS
+    for m in (1, 512):
+        layers = [DecoderLayerLinears(m, dev, seed=500 + 10 * i) for i in range(4)]
+        t, _ = time_graph(layers, 1, 8, 64 if m == 1 else 16, dev)
+        B = sum(algo_bytes(m, n, k, b) for _, n, k, b, _ in specs)
+        fl = sum(2.0 * m * n * k for _, n, k, _, _ in specs)
+        ent = {"us_per_layer": round(t * 1e6, 2), "algorithmic_bytes": B,
+               "GB/s": round(B / t / 1e9, 1), "hbm_frac": round(B / t / 1e9 / HBM_PEAK_GBS, 4),
+               "TFLOP/s": round(fl / t / 1e12, 2),
+               "includes": "q/k/v Q5 (one shared transform at M>1), o Q6, gate/up Q3 (shared "
+                           "transform at M>1), down Q4; linears only (no attention or norms)"}
+        if m > 1:
+            ent["mfma_frac"] = round(fl / t / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
+        out[f"decoder_layer_m{m}"] = ent
+        del layers
+        torch.cuda.empty_cache()
+    return out
+
+
+TRACE_JSON = os.path.join(ROOT, "profiles", "trace_gemv_q4_12288x4096_m1.json")
+
+
+def summarize_trace(trace_csv, kernel_substr="gemv_mfma_kernel"):
+    """Headline dispatches in a rocprofv3 kernel-trace CSV: mean / median
+    kernel duration, and per timed replay (dispatches less than 50 us apart)
+    the span (last end - first start) / dispatches; the median over replays
+    of at least 100 dispatches."""
+    import csv
+    rows = []
+    for r in csv.DictReader(open(trace_csv)):
+        if kernel_substr in r["Kernel_Name"]:
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    if not rows:
+        raise SystemExit(f"{trace_csv}: no {kernel_substr} dispatches")
+    rows.sort()
+    dur = np.array([(e - b) * 1e-3 for b, e, _ in rows])
+    runs, cur = [], [rows[0]]
+    for r in rows[1:]:
+        if r[0] - cur[-1][1] > 50_000:
+            runs.append(cur)
+            cur = [r]
+        else:
+            cur.append(r)
+    runs.append(cur)
+    spans = [((run[-1][1] - run[0][0]) * 1e-3 / len(run), len(run)) for run in runs
+             if len(run) >= 100]
+    return {"kernel": rows[0][2], "dispatches": len(rows), "avg_us": round(float(dur.mean()), 3),
+            "median_us": round(float(np.median(dur)), 3),
+            "span_us_per_call": round(float(np.median([s for s, _ in spans])), 3) if spans else None,
+            "replays": len(spans), "calls_per_replay": int(np.median([c for _, c in spans]))
+            if spans else 0}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=2000, help="headline calls per timed sample")
+    ap.add_argument("--warmup", type=int, default=200, help="untimed headline calls first")
+    ap.add_argument("--repeats", type=int, default=10,
+                    help="timed samples of --steps calls each (the line reports their median)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--profile-traffic", action="store_true",
                     help="run only the workload of the FETCH_SIZE / WRITE_SIZE pmc passes")
     ap.add_argument("--headline-only", action="store_true",
                     help="time only the headline call (for a rocprofv3 kernel trace whose "
-                         "average covers exactly the headline dispatches)")
-    ap.add_argument("--only-extra", choices=("moe", "prefill", "kv"),
+                         "dispatches are exactly the headline's)")
+    ap.add_argument("--only-extra", choices=("moe", "prefill", "kv", "layer", "decode"),
                     help="time only one of the extra workloads and print its JSON (for a "
                          "rocprofv3 kernel trace of that path alone)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print the traffic JSON from the two pmc passes and exit")
+    ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
+                    help="print the headline kernel's trace summary JSON and exit")
     args = ap.parse_args()
     if args.summarize_pmc:
         print(json.dumps(summarize_pmc(*args.summarize_pmc), indent=1))
+        return
+    if args.summarize_trace:
+        print(json.dumps(summarize_trace(args.summarize_trace), indent=1))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build's hot path is a single-GPU kernel "
@@ -331,39 +504,28 @@ def main():
         profile_traffic(dev)
         return
     if args.only_extra:
-        fn = {"moe": moe_extra, "prefill": prefill_extra, "kv": kv_extra}[args.only_extra]
+        fn = {"moe": moe_extra, "prefill": prefill_extra, "kv": kv_extra,
+              "layer": decoder_layer_extra, "decode": decode_extra}[args.only_extra]
         print(json.dumps(fn(dev)))
         return
 
     n, k, bits, m = 12288, 4096, 4, 1
     x = torch.randn(m, k, device=dev, dtype=torch.float16)
     layers = [Linear(n, k, bits, m, dev, seed=100 + i, x=x) for i in range(N_COPIES)]
-    t_call, calls_timed = time_graph(layers, 8, args.warmup, args.steps, dev)
+    t_call, samples = time_steps(layers, args.steps, args.warmup, dev, repeats=args.repeats)
     B = algo_bytes(m, n, k, bits)
-    gbs = B / t_call / 1e9
     if args.headline_only:
         print(json.dumps({"workload": "headline only", "us_per_call": round(t_call * 1e6, 3),
-                          "GB/s": round(gbs, 1), "calls_timed": calls_timed}))
+                          "GB/s": round(B / t_call / 1e9, 1), "steps": args.steps,
+                          "repeats": args.repeats,
+                          "samples_us": [round(v * 1e6, 3) for v in samples]}))
         return
-    t_hot, _ = time_graph(layers[:1], 128, args.warmup, args.steps, dev)
+    t_hot, _ = time_graph(layers[:1], 1, args.warmup, 1024, dev)
+    del layers
 
-    extra = {}
-    for mm in (4, 8, 16, 32, 64):
-        lay = [Linear(n, k, bits, mm, dev, seed=200 + i) for i in range(N_COPIES)]
-        t, _ = time_graph(lay, 4, 64, 512, dev)
-        extra[f"decode_m{mm}"] = {"us_per_call": round(t * 1e6, 2),
-                                  "GB/s": round(algo_bytes(mm, n, k, bits) / t / 1e9, 1)}
-        del lay
-    # the MLP's other shapes: gate/up Q3 12288x4096 and down Q4 4096x12288
-    for name, (nn, kk, bb) in (("gateup_q3", (12288, 4096, 3)), ("down_q4", (4096, 12288, 4))):
-        for mm in (1, 16):
-            lay = [Linear(nn, kk, bb, mm, dev, seed=400 + i) for i in range(N_COPIES)]
-            t, _ = time_graph(lay, 4, 64, 512, dev)
-            gb = algo_bytes(mm, nn, kk, bb) / t / 1e9
-            extra[f"decode_{name}_m{mm}"] = {"us_per_call": round(t * 1e6, 2), "GB/s": round(gb, 1),
-                                             "hbm_frac": round(gb / HBM_PEAK_GBS, 4)}
-            del lay
+    extra = decode_extra(dev)
     extra.update(prefill_extra(dev))
+    extra.update(decoder_layer_extra(dev))
     extra["cache_hot_m1"] = {"us_per_call": round(t_hot * 1e6, 2),
                              "GB/s": round(B / t_hot / 1e9, 1),
                              "note": "one weight copy, Infinity-Cache resident"}
@@ -375,12 +537,22 @@ def main():
     if os.path.exists(TRAFFIC_JSON):
         with open(TRAFFIC_JSON) as f:
             traffic = round(json.load(f)["traffic_bytes"])
+    trace = None  # the committed kernel trace of `bench.py --headline-only`
+    if os.path.exists(TRACE_JSON):
+        with open(TRACE_JSON) as f:
+            trace = json.load(f)
+    # the kernel's launch duration: the event-timed period, or the traced mean
+    # kernel duration when that is longer (the conservative of the two)
+    us_event = t_call * 1e6
+    us_kernel = max(us_event, trace["avg_us"]) if trace else us_event
+    achieved = B / (us_kernel * 1e-6) / 1e9
+    gbs = B / t_call / 1e9
     out = {
         "metric": "HBM GB/s + us/call, Q4 GEMV 12288x4096 M=1; prefill GEMM TFLOPS M=2048",
         "value": round(gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": calls_timed,
+        "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(t_call * 1e3, 6),
         "us_per_call": round(t_call * 1e6, 3),
@@ -393,13 +565,45 @@ def main():
         "config": {"workload": "decode linear Q4 12288x4096 M=1 (FWHT fused + nibble GEMV), "
                                f"{N_COPIES} rotating weight copies",
                    "M": m, "N": n, "K": k, "bits": bits, "algorithmic_bytes": B},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic},
+        "timing": {"method": f"{args.repeats} samples of exactly {args.steps} calls (one HIP "
+                             "graph replay each, HIP events on the replay stream); median",
+                   "samples": args.repeats,
+                   "min_us": round(min(samples) * 1e6, 3), "max_us": round(max(samples) * 1e6, 3)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic,
+                     "kernel_us": round(us_kernel, 3),
+                     "kernel_us_source": "trace mean" if us_kernel > us_event else "HIP events",
+                     "trace": trace},
         "cpu_baseline": cpu,
         "extra": extra,
     }
     print(json.dumps(out))
+
+
+def decode_extra(dev):
+    """Decode at M = 4..64 on the headline shape, the MLP's gate/up Q3
+    12288x4096 and down Q4 4096x12288 at M = 1 / 4 / 16, and C1 (Q5
+    4096x4096 M = 1)."""
+    n, k, bits = 12288, 4096, 4
+    extra = {}
+    for mm in (4, 8, 16, 32, 64):
+        lay = [Linear(n, k, bits, mm, dev, seed=200 + i) for i in range(N_COPIES)]
+        t, _ = time_graph(lay, 4, 64, 512, dev)
+        extra[f"decode_m{mm}"] = {"us_per_call": round(t * 1e6, 2),
+                                  "GB/s": round(algo_bytes(mm, n, k, bits) / t / 1e9, 1)}
+        del lay
+    for name, (nn, kk, bb), ms in (("gateup_q3", (12288, 4096, 3), (1, 4, 16)),
+                                   ("down_q4", (4096, 12288, 4), (1, 4, 16)),
+                                   ("c1_q5_4096x4096", (4096, 4096, 5), (1,))):
+        for mm in ms:
+            lay = [Linear(nn, kk, bb, mm, dev, seed=400 + i) for i in range(N_COPIES)]
+            t, _ = time_graph(lay, 4, 64, 512, dev)
+            gb = algo_bytes(mm, nn, kk, bb) / t / 1e9
+            extra[f"decode_{name}_m{mm}"] = {"us_per_call": round(t * 1e6, 2), "GB/s": round(gb, 1),
+                                             "hbm_frac": round(gb / HBM_PEAK_GBS, 4)}
+            del lay
+    return extra
 
 
 if __name__ == "__main__":
