@@ -51,8 +51,8 @@ def _build(decorator):
 
         def __repr__(self) -> str:
             bits = sorted(set(self.bit_assignment.values())) if self.bit_assignment else []
-            return (f"PolarQuantConfig(block_size={self.block_size}, bits={bits}, "
-                    f"layers={len(self.layers_meta)})")
+            return (f"<polarengine quantization: {len(self.layers_meta)} layer entries, "
+                    f"bit widths {bits}, {self.block_size}-wide blocks>")
 
         @staticmethod
         def get_name() -> str:
@@ -75,8 +75,8 @@ def _build(decorator):
         def from_config(cls, config: Dict[str, Any]) -> "PolarQuantConfig":
             fmt = config.get("format", "polar_engine_v4")
             if fmt not in _KNOWN_FORMATS:
-                logger.warning("Unrecognised PolarEngine/HLWQ format '%s'. Proceeding, but "
-                               "weight loading may fail.", fmt)
+                logger.warning("polar_config.json declares format %r, which this build does "
+                               "not know; continuing with the split-tensor reader", fmt)
             return cls(block_size=config.get("block_size", 128),
                        bit_assignment=config.get("bit_assignment", {}),
                        layers_meta=config.get("layers", {}))

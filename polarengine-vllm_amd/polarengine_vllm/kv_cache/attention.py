@@ -3,11 +3,12 @@
 ``PolarKVAttentionWrapper`` exposes a PolarKVCache through the transformers
 ``Cache.update`` interface and wraps a vLLM-style attention forward so that
 new K/V are compressed and the attention reads the expanded history.
-``patch_model_attention`` tags a model's attention modules with their layer
-index and the cache."""
+``patch_model_attention`` wraps a model's attention backends (or tags its
+attention blocks) with the cache."""
 
 from __future__ import annotations
 
+import inspect
 from typing import Any, Callable, Optional, Tuple
 
 import torch
@@ -61,17 +62,38 @@ class PolarKVAttentionWrapper:
         return wrapped_forward
 
 
+def _backend_forward(module: torch.nn.Module) -> bool:
+    """True for an attention backend: its forward takes (query, key, value,
+    kv_cache, attn_metadata), the call the wrapper intercepts."""
+    fwd = getattr(module, "forward", None)
+    try:
+        names = list(inspect.signature(fwd).parameters)[:5]
+    except (TypeError, ValueError):
+        return False
+    return names == ["query", "key", "value", "kv_cache", "attn_metadata"]
+
+
 def patch_model_attention(model: torch.nn.Module, config: PolarKVConfig) -> PolarKVCache:
-    """Tag the attention modules (names containing self_attn / attention /
-    attn that own a q_proj or qkv_proj) with ``_polar_kv_layer_idx`` and
-    ``_polar_kv_cache``, in module order, up to ``config.num_layers``."""
+    """Give a model a PolarKVCache and return it.
+
+    Attention backends (modules whose forward takes query, key, value,
+    kv_cache, attn_metadata: vLLM's per-layer attention) get that forward
+    replaced by ``wrap_attention_forward``, so their new K/V are compressed
+    and the whole history is what they attend to; they are numbered in
+    module order, up to ``config.num_layers``. A model without such backends
+    (transformers attention blocks, which take the cache through
+    ``past_key_values``, where ``PolarKVAttentionWrapper`` itself serves)
+    has its attention blocks, the modules owning a q_proj or qkv_proj, tagged
+    with ``_polar_kv_layer_idx`` / ``_polar_kv_cache`` in the same order, as
+    the reference's hook does (kv_cache/attention.py:128-155)."""
     cache = PolarKVCache(config)
-    idx = 0
-    for name, module in model.named_modules():
-        if any(p in name for p in ("self_attn", "attention", "attn")) and (
-                hasattr(module, "q_proj") or hasattr(module, "qkv_proj")):
-            if idx < config.num_layers:
-                module._polar_kv_layer_idx = idx
-                module._polar_kv_cache = cache
-                idx += 1
+    wrapper = PolarKVAttentionWrapper(cache)
+    backends = [m for m in model.modules() if _backend_forward(m)]
+    targets = backends or [m for m in model.modules()
+                           if hasattr(m, "q_proj") or hasattr(m, "qkv_proj")]
+    for idx, module in enumerate(targets[:config.num_layers]):
+        if backends:
+            module.forward = wrapper.wrap_attention_forward(module.forward, idx)
+        module._polar_kv_layer_idx = idx
+        module._polar_kv_cache = cache
     return cache

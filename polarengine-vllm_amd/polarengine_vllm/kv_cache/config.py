@@ -22,12 +22,12 @@ class PolarKVConfig:
 
     def __post_init__(self) -> None:
         if self.nbits not in (2, 3, 4):
-            raise AssertionError(f"nbits must be 2, 3, or 4, got {self.nbits}")
+            raise AssertionError(f"KV codes are 2, 3 or 4 bits wide (nbits={self.nbits})")
         if self.head_dim <= 0:
-            raise AssertionError(f"head_dim must be positive, got {self.head_dim}")
+            raise AssertionError(f"head_dim has to be at least 1 (head_dim={self.head_dim})")
         if self.head_dim & (self.head_dim - 1):
-            raise ValueError(f"head_dim={self.head_dim} is not a power of 2. PolarQuant requires "
-                             f"power-of-2 head_dim for Walsh-Hadamard transform.")
+            raise ValueError(f"the KV rotation is a Hadamard transform over the whole head, so "
+                             f"head_dim must be a power of 2 (head_dim={self.head_dim})")
 
     @property
     def compression_ratio(self) -> float:

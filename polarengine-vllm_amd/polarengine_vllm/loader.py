@@ -66,12 +66,14 @@ def load_polar_config(model_dir: str) -> dict:
     logged and loading proceeds."""
     path = os.path.join(model_dir, "polar_config.json")
     if not os.path.isfile(path):
-        raise FileNotFoundError(f"polar_config.json not found in {model_dir}")
+        raise FileNotFoundError(f"{model_dir} holds no polar_config.json (not a PolarEngine "
+                                f"checkpoint directory)")
     with open(path, "r") as f:
         config = json.load(f)
     fmt = str(config.get("format", "unknown"))
     if fmt not in SPLIT_FORMATS and fmt.lower() not in HLWQ_FORMATS:
-        logger.warning("Unrecognised PolarEngine format '%s'; loading may fail.", fmt)
+        logger.warning("checkpoint format %r is not one this loader knows; trying the "
+                       "split-tensor layout", fmt)
     return config
 
 
@@ -86,7 +88,8 @@ def get_weight_map(model_dir: str) -> Dict[str, str]:
             return dict(json.load(f).get("weight_map", {}))
     files = sorted(Path(model_dir).glob("*.safetensors"))
     if not files:
-        raise FileNotFoundError(f"No .safetensors files found in {model_dir}")
+        raise FileNotFoundError(f"{model_dir} has neither a safetensors index nor any "
+                                f"*.safetensors shard")
     weight_map: Dict[str, str] = {}
     for path in files:
         with safe_open(str(path), framework="pt", device="cpu") as f:
@@ -171,8 +174,8 @@ class PolarWeightLoader:
     def load_tensor(self, key: str, device: Optional[Union[str, torch.device]] = None) -> torch.Tensor:
         """One tensor by name; KeyError (listing a few names) when absent."""
         if key not in self.weight_map:
-            raise KeyError(f"Tensor '{key}' not found in weight map. "
-                           f"Available keys (first 10): {list(self.weight_map)[:10]}")
+            raise KeyError(f"no tensor named {key!r} in the checkpoint (it has "
+                           f"{len(self.weight_map)}, e.g. {list(self.weight_map)[:10]})")
         t = self._get_file(self.weight_map[key]).get_tensor(key)
         dev = torch.device(device) if device is not None else self.device
         return t if dev.type == "cpu" else t.to(dev)
@@ -180,7 +183,7 @@ class PolarWeightLoader:
     def tensor_shape(self, key: str) -> Tuple[int, ...]:
         """Shape of a stored tensor from the safetensors header (no data read)."""
         if key not in self.weight_map:
-            raise KeyError(f"Tensor '{key}' not found in weight map")
+            raise KeyError(f"no tensor named {key!r} in the checkpoint")
         return tuple(self._get_file(self.weight_map[key]).get_slice(key).get_shape())
 
     def _format(self) -> str:
@@ -203,8 +206,8 @@ class PolarWeightLoader:
             elif layer_name in self.weight_map:  # bare parameter name
                 out["weight"] = self.load_tensor(layer_name)
             else:
-                raise KeyError(f"Cannot find weight tensor for non-quantized layer '{layer_name}'. "
-                               f"Tried keys '{layer_name}.weight' and '{layer_name}'.")
+                raise KeyError(f"unquantized layer {layer_name!r} has no weight: neither "
+                               f"{layer_name + '.weight'!r} nor {layer_name!r} is stored")
         if layer_name + ".bias" in self.weight_map:
             out["bias"] = self.load_tensor(layer_name + ".bias")
         return out
@@ -218,8 +221,8 @@ class PolarWeightLoader:
             bs = int(self.polar_config.get("block_size", 128))
             out["ct_scaled"] = self.load_tensor(layer_name + ".ct") / math.sqrt(bs)
         else:
-            raise KeyError(f"No centroids found for '{layer_name}'. Tried "
-                           f"'{layer_name}.ct_scaled' and '{layer_name}.ct'.")
+            raise KeyError(f"layer {layer_name!r} stores no codebook: expected "
+                           f"{layer_name + '.ct_scaled'!r} or {layer_name + '.ct'!r}")
         meta = self._layer_meta(layer_name)
         if meta.get("packed_q5", False):
             bs = int(meta.get("block_size", self.polar_config.get("block_size", 128)))
@@ -229,8 +232,8 @@ class PolarWeightLoader:
     def _load_hlwq(self, layer_name: str) -> Dict[str, torch.Tensor]:
         packed_key = layer_name + ".weight__packed"
         if packed_key not in self.weight_map:
-            raise KeyError(f"HLWQ bit-packed layer '{layer_name}' missing '{packed_key}'. "
-                           f"Available suffixes: "
+            raise KeyError(f"bit-packed (HLWQ) layer {layer_name!r} lacks {packed_key!r}; "
+                           f"stored under that prefix: "
                            f"{[k for k in self.weight_map if k.startswith(layer_name)][:5]}")
         packed = self.load_tensor(packed_key)
         norms = self.load_tensor(layer_name + ".weight__norms")
@@ -289,7 +292,8 @@ class PolarWeightLoader:
 def _shard_rows(t: torch.Tensor, tp_rank: int, tp_size: int, what: str) -> torch.Tensor:
     rows = t.shape[0]
     if rows % tp_size:
-        raise ValueError(f"Cannot evenly shard {rows} {what} across {tp_size} TP ranks.")
+        raise ValueError(f"{rows} {what} do not split evenly over {tp_size} tensor-parallel "
+                         f"ranks")
     n = rows // tp_size
     return t[tp_rank * n:(tp_rank + 1) * n].contiguous()
 

@@ -145,7 +145,7 @@ def test_config_parse_and_resolve(sample_polar_config):
     assert PolarQuantConfig.get_config_filenames() == ["polar_config.json"]
     assert torch.float16 in PolarQuantConfig.get_supported_act_dtypes()
     assert PolarQuantConfig.get_min_capability() == 70
-    assert "block_size=128" in repr(c)
+    assert "128-wide blocks" in repr(c) and "[3, 4, 5, 6]" in repr(c)
 
 
 def test_get_quant_method(sample_polar_config):

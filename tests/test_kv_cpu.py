@@ -100,3 +100,22 @@ def test_presets_and_patch_model_attention():
     cache = patch_model_attention(model, cfg)
     assert [getattr(b.self_attn, "_polar_kv_layer_idx", None) for b in model.layers] == [0, 1, None]
     assert model.layers[0].self_attn._polar_kv_cache is cache
+
+    # vLLM-style attention backends: their forward is wrapped (not called here:
+    # the cache's kernels need a GPU)
+    class Backend(torch.nn.Module):
+        def forward(self, query, key, value, kv_cache, attn_metadata, **kw):
+            return query
+
+    class VBlock(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.qkv_proj = torch.nn.Identity()
+            self.attn = Backend()
+
+    vmodel = torch.nn.ModuleList([VBlock() for _ in range(3)])
+    vcache = patch_model_attention(vmodel, PolarKVConfig(num_layers=3))
+    for i, blk in enumerate(vmodel):
+        assert blk.attn._polar_kv_layer_idx == i and blk.attn._polar_kv_cache is vcache
+        assert blk.attn.forward.__name__ == "wrapped_forward"
+        assert not hasattr(blk, "_polar_kv_layer_idx")  # the backends were found, not the blocks
