@@ -351,19 +351,26 @@ def prefill_extra(dev):
 
 
 class DecoderLayerLinears:
-    """The seven linears of the C4 decoder layer (hidden 4096, 32 q / 8 kv
-    heads of 128, intermediate 12288): q/k/v Q5 sharing one transform of the
-    normed hidden state, o Q6, gate/up Q3 sharing one transform, down Q4;
-    tiled-16 weights. M = 1: seven pe_linear_forward calls (transform fused
-    into each decode GEMV). M > 1: pe_fwht128 once for q/k/v and once for
-    gate/up, pe_linear_forward_xtf for those five, pe_linear_forward for o and
-    down (their inputs are new activations)."""
+    """The linears of the C4 decoder layer (hidden 4096, 32 q / 8 kv heads of
+    128, intermediate 12288): q/k/v Q5 sharing one transform of the normed
+    hidden state, o Q6, gate/up Q3 sharing one transform, down Q4; tiled-16
+    weights. `merged`: vLLM's form, q/k/v one qkv_proj (6144 rows) and
+    gate/up one gate_up_proj (24576 rows), as PolarQuantLinearMethod sees
+    them (create_weights sums output_partition_sizes); otherwise seven
+    separate modules (the transformers form). M = 1: one pe_linear_forward per
+    linear (transform fused into each decode GEMV). M > 1: pe_fwht128 once for
+    q/k/v and once for gate/up, pe_linear_forward_xtf for those,
+    pe_linear_forward for o and down (their inputs are new activations)."""
 
-    SPECS = [("q", 4096, 4096, 5, "qkv"), ("k", 1024, 4096, 5, "qkv"), ("v", 1024, 4096, 5, "qkv"),
-             ("o", 4096, 4096, 6, "o"), ("gate", 12288, 4096, 3, "gu"), ("up", 12288, 4096, 3, "gu"),
-             ("down", 4096, 12288, 4, "down")]
+    SEPARATE = [("q", 4096, 4096, 5, "qkv"), ("k", 1024, 4096, 5, "qkv"),
+                ("v", 1024, 4096, 5, "qkv"), ("o", 4096, 4096, 6, "o"),
+                ("gate", 12288, 4096, 3, "gu"), ("up", 12288, 4096, 3, "gu"),
+                ("down", 4096, 12288, 4, "down")]
+    MERGED = [("qkv", 6144, 4096, 5, "qkv"), ("o", 4096, 4096, 6, "o"),
+              ("gate_up", 24576, 4096, 3, "gu"), ("down", 4096, 12288, 4, "down")]
 
-    def __init__(self, m, dev, seed):
+    def __init__(self, m, dev, seed, merged=True):
+        self.SPECS = self.MERGED if merged else self.SEPARATE
         from polarengine_vllm.packing import tile_weights_16
         self.m, self.dev = m, dev
         L = _lib.lib()
@@ -408,26 +415,33 @@ class DecoderLayerLinears:
 
 
 def decoder_layer_extra(dev):
-    """C4: the decoder layer's seven quantized linears at M = 1 (GB/s of the
-    120.6 MB of algorithmic bytes) and M = 512 (TFLOP/s of 197.6 GFLOP); four
-    layer copies in turn (482 MB > the 256 MB Infinity Cache)."""
+    """C4: the decoder layer's quantized linears at M = 1 (GB/s of its
+    algorithmic bytes: 120.6 MB for the seven separate linears) and M = 512
+    (TFLOP/s of 197.6 GFLOP); four layer copies in turn (482 MB > the 256 MB
+    Infinity Cache). decoder_layer_m*: vLLM's merged qkv / gate_up form;
+    decoder_layer_separate_m*: seven separate modules."""
     out = {}
-    specs = DecoderLayerLinears.SPECS
-    for m in (1, 512):
-        layers = [DecoderLayerLinears(m, dev, seed=500 + 10 * i) for i in range(4)]
-        t, _ = time_graph(layers, 1, 8, 64 if m == 1 else 16, dev)
-        B = sum(algo_bytes(m, n, k, b) for _, n, k, b, _ in specs)
-        fl = sum(2.0 * m * n * k for _, n, k, _, _ in specs)
-        ent = {"us_per_layer": round(t * 1e6, 2), "algorithmic_bytes": B,
-               "GB/s": round(B / t / 1e9, 1), "hbm_frac": round(B / t / 1e9 / HBM_PEAK_GBS, 4),
-               "TFLOP/s": round(fl / t / 1e12, 2),
-               "includes": "q/k/v Q5 (one shared transform at M>1), o Q6, gate/up Q3 (shared "
-                           "transform at M>1), down Q4; linears only (no attention or norms)"}
-        if m > 1:
-            ent["mfma_frac"] = round(fl / t / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
-        out[f"decoder_layer_m{m}"] = ent
-        del layers
-        torch.cuda.empty_cache()
+    for merged, tag in ((True, "decoder_layer"), (False, "decoder_layer_separate")):
+        specs = DecoderLayerLinears.MERGED if merged else DecoderLayerLinears.SEPARATE
+        for m in (1, 512):
+            layers = [DecoderLayerLinears(m, dev, seed=500 + 10 * i, merged=merged)
+                      for i in range(4)]
+            t, _ = time_graph(layers, 1, 8, 64 if m == 1 else 16, dev)
+            B = sum(algo_bytes(m, n, k, b) for _, n, k, b, _ in specs)
+            fl = sum(2.0 * m * n * k for _, n, k, _, _ in specs)
+            ent = {"us_per_layer": round(t * 1e6, 2), "algorithmic_bytes": B,
+                   "GB/s": round(B / t / 1e9, 1),
+                   "hbm_frac": round(B / t / 1e9 / HBM_PEAK_GBS, 4),
+                   "TFLOP/s": round(fl / t / 1e12, 2),
+                   "launches": len(specs) + (2 if m > 1 else 0),
+                   "includes": ("qkv Q5, o Q6, gate_up Q3, down Q4 (vLLM merged modules)" if merged
+                                else "q/k/v Q5, o Q6, gate/up Q3, down Q4 (separate modules)")
+                   + "; a shared transform per input at M > 1; linears only"}
+            if m > 1:
+                ent["mfma_frac"] = round(fl / t / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
+            out[f"{tag}_m{m}"] = ent
+            del layers
+            torch.cuda.empty_cache()
     return out
 
 
