@@ -11,11 +11,12 @@
  *
  * Workspaces: a workspace (any size query's bytes, 16-byte aligned) must be
  * zero-filled once before its first use. Its first 4096 bytes hold
- * completion counters of the kernels that split K over workgroups (the last
- * workgroup of a group adds the partial sums, so no second kernel is
- * launched); every call leaves them zero again and no entry point writes
- * anything else there, so one zeroed buffer, sized for the largest query,
- * can serve every entry point in turn.
+ * completion counters of kernels whose workgroups hand work to one another
+ * within one launch (the K split's partial sums, added up by the last
+ * workgroup of a group; the MoE routing, bucketed by the last routing
+ * workgroup), so no second kernel is launched; every call leaves them zero
+ * again and no entry point writes anything else there, so one zeroed buffer,
+ * sized for the largest query, can serve every entry point in turn.
  *
  * Runtime weight layout (one quantized linear, N = out_f, Kp = in_f padded to
  * a multiple of 128, nb = Kp / 128), as registered by the reference's
@@ -304,7 +305,11 @@ int pe_moe_route_grouped(const float* logits, int64_t T, int E, int top_k, int r
  *             must then be multiples of 16)
  *   w2      : codes [E, H, ...] over in_f = I padded to Ip = ceil(I/128)*128,
  *             norms float16 [E, H, Ip/128], ct2 float32 [2**bits2]
- *   out     : [T, H] in x_dtype = sum_k topk_w[t,k] * expert_{ids[t,k]}(x_t)
+ *   out     : [T, H] in x_dtype = sum_k topk_w[t,k] * expert_{ids[t,k]}(x_t),
+ *             the terms added in slot order k = 0, 1, .. in fp32 (slots whose
+ *             id is outside 0..E-1 are skipped; a token with none is zero)
+ * Four launches: x transform with the bucketing of the pairs by expert;
+ * gate/up with SwiGLU; down; the weighted combine.
  * Workspace: pe_moe_workspace_size(T, top_k, E, H, I) bytes.
  */
 size_t pe_moe_workspace_size(int64_t T, int top_k, int E, int H, int I);
@@ -315,6 +320,26 @@ int pe_moe_forward(const void* x, int x_dtype, int64_t T, int H, int I, int E, i
                    const void* w2_codes, int bits2, int packed2,
                    const uint16_t* w2_norms, const float* ct2, int n_levels2,
                    void* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Routing and experts in one call: replaces PolarPassthroughMoEMethod.apply
+ * (moe_method.py:74-92), which takes the router logits and hands routing and
+ * experts to vLLM's fused MoE. Routing as pe_moe_route (num_expert_group = 0)
+ * or pe_moe_route_grouped (num_expert_group > 0), with the same limits; the
+ * rest as pe_moe_forward. The routing shares the first launch with the x
+ * transform (its last workgroup buckets the pairs), so the call is four
+ * launches, as pe_moe_forward's. The routing results stay in the workspace.
+ *   logits : float32 [T, E]
+ * Workspace: pe_moe_workspace_size(T, top_k, E, H, I) bytes.
+ */
+int pe_moe_forward_routed(const void* x, int x_dtype, int64_t T, int H, int I, int E, int top_k,
+                          const float* logits, int renormalize, int scoring,
+                          const float* correction_bias, int num_expert_group, int topk_group,
+                          const void* w13_codes, int bits13, int packed13,
+                          const uint16_t* w13_norms, const float* ct13, int n_levels13,
+                          const void* w2_codes, int bits2, int packed2,
+                          const uint16_t* w2_norms, const float* ct2, int n_levels2,
+                          void* out, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -560,7 +560,8 @@ def moe_forward(x: np.ndarray, topk_w: np.ndarray, topk_ids: np.ndarray,
             h = np.pad(h, ((0, 0), (0, kp2 - inter)))
         d = hadamard_domain_matmul(codes2[e], norms2[e], ct2, fwht_blocks(h, block_size),
                                    block_size)
-        out[rows] += topk_w[rows, slots][:, None] * d[:, :hdim]
+        # np.add.at: a token routed to one expert in two slots adds both
+        np.add.at(out, rows, topk_w[rows, slots][:, None] * d[:, :hdim])
     return out.astype(np.float16)
 
 

@@ -127,6 +127,21 @@ __device__ __forceinline__ void g2lds16(const void* src, uint32_t lds_addr) {
                                    (lds_void*)(static_cast<uintptr_t>(lds_addr)), 16, 0, 0);
 }
 
+// Device-coherent 32-bit accesses for data one workgroup hands to another
+// within one launch: agent-scope relaxed atomics, which compile to global
+// loads and stores with the sc1 cache policy (the level every XCD sees
+// alike). The producer stores with st_dev32, waits for its stores
+// (s_waitcnt vmcnt(0)), then counts itself in with a device-scope atomicAdd;
+// the workgroup whose increment completes the count reads with ld_dev32. A
+// device-scope release/acquire fence in their place would write back and
+// invalidate the XCD's whole L2 once per wave.
+__device__ __forceinline__ void st_dev32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_dev32(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // LDS table address for code byte `b` (0..3) of dword `w`: (byte << 8) | lane4.
 // v_perm_b32 picks byte 0 from src1 (= lane4 < 256) and byte 1 from byte b of
 // src0 (= w); bytes 2-3 are zero (selector 0x0c).

@@ -7,16 +7,18 @@
 // top-k, renormalise, gate = x W13[:I]^T, up = x W13[I:]^T,
 // h = silu(gate) * up, y = h W2^T, out = sum_k w_k y_k.
 //
-// Launch sequence of pe_moe_forward (no host synchronisation):
-//   1. moe_prep: FWHT-128 of x into pair f16 (shared by every expert) and, in
-//      the grid's last workgroup, the bucketing of the T*top_k (token, slot)
-//      pairs by expert (LDS histogram + scan + scatter) -> per-expert offsets,
-//      token of each sorted pair, sorted position of each pair;
+// Launch sequence of pe_moe_forward / pe_moe_forward_routed (no host
+// synchronisation):
+//   1. moe_front_kernel: the routing of pe_moe_forward_routed (the ids are
+//      given to pe_moe_forward), the FWHT-128 of x into pair f16 (shared by
+//      every expert), and the bucketing of the T*top_k (token, slot) pairs by
+//      expert -> per-expert offsets, token of each sorted pair, sorted
+//      position of each pair;
 //   2. grouped experts, W13: gate and up tiles with SwiGLU; each 128-column
 //      block of h goes through the FWHT in the same kernel -> pair-f16 h
 //      [pairs, Ip] (A rows gathered by token id; columns past I are zero);
 //   3. grouped experts, W2 -> y2 [pairs, H] fp32;
-//   4. combine: out[t] = sum_k w[t, k] * y2[pos(t, k)] in fixed k order, fp16.
+//   4. combine: out[t] = sum_k w[t, k] * y2[pos(t, k)] in fixed k order.
 // Each output row depends only on its own inputs, so bucket order inside an
 // expert (set by LDS atomics) does not change any result bit.
 
@@ -49,10 +51,25 @@ __device__ __forceinline__ uint64_t route_key(float s, int e) {
   return ((uint64_t)ord << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
 }
 
-__global__ __launch_bounds__(64 * kRouteWaves) void moe_route_kernel(
-    const float* __restrict__ logits, int64_t T, int E, int top_k, int renormalize, int scoring,
-    const float* __restrict__ bias, float* __restrict__ topk_w, int32_t* __restrict__ topk_ids,
-    int n_group, int topk_group) {
+struct RouteParams {
+  const float* logits;  // [T, E] fp32
+  int64_t T;
+  int E, top_k, renormalize, scoring;
+  const float* bias;    // nullable correction bias [E]
+  float* topk_w;        // [T, top_k]
+  int32_t* topk_ids;    // [T, top_k]
+  int n_group, topk_group;
+};
+
+// Routes tokens t0 + wave (wave = 0..kRouteWaves-1) of this workgroup. COH:
+// the ids are stored device-coherently, for a workgroup of the same launch
+// that buckets them.
+template <bool COH>
+__device__ void route_tokens(const RouteParams& p, int64_t t0) {
+  const float* __restrict__ logits = p.logits;
+  const float* __restrict__ bias = p.bias;
+  const int64_t T = p.T;
+  const int E = p.E, top_k = p.top_k, scoring = p.scoring, n_group = p.n_group;
   __shared__ uint64_t keys[kRouteWaves][256];
   __shared__ float sel_w[kRouteWaves][16];
   __shared__ int sel_e[kRouteWaves][16];
@@ -60,7 +77,7 @@ __global__ __launch_bounds__(64 * kRouteWaves) void moe_route_kernel(
   __shared__ float grp[kRouteWaves][kRouteMaxGroups];  // grouped: group scores
   __shared__ int gkeep[kRouteWaves][kRouteMaxGroups];  // grouped: group selected
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t t = (int64_t)blockIdx.x * kRouteWaves + wave;
+  const int64_t t = t0 + wave;
   const bool live = t < T;
   const int64_t tr = live ? t : T - 1;  // idle waves recompute a live row: barriers are per workgroup
   float v[4];
@@ -135,7 +152,7 @@ __global__ __launch_bounds__(64 * kRouteWaves) void moe_route_kernel(
         const float o = grp[wave][h];
         r += (o > mine_g || (o == mine_g && h < lane)) ? 1 : 0;
       }
-      gkeep[wave][lane] = r < topk_group;
+      gkeep[wave][lane] = r < p.topk_group;
     }
     __syncthreads();
 #pragma unroll
@@ -176,74 +193,160 @@ __global__ __launch_bounds__(64 * kRouteWaves) void moe_route_kernel(
     float wsum = 0.f;
     for (int k = 0; k < top_k; ++k) wsum += sel_w[wave][k];  // selection order
     const float w = sel_w[wave][lane];
-    topk_w[t * top_k + lane] = renormalize ? w / wsum : w;
-    topk_ids[t * top_k + lane] = sel_e[wave][lane];
+    p.topk_w[t * top_k + lane] = p.renormalize ? w / wsum : w;
+    if constexpr (COH)
+      st_dev32(reinterpret_cast<uint32_t*>(p.topk_ids) + t * top_k + lane, (uint32_t)sel_e[wave][lane]);
+    else
+      p.topk_ids[t * top_k + lane] = sel_e[wave][lane];
   }
 }
 
-// ---------------------------------------------------------------------------
-// moe_prep: workgroups 0..fwht_wgs-1 transform x (one 128-block per 16-lane
-// group) into pair f16; workgroup fwht_wgs buckets the pairs by expert.
-// ---------------------------------------------------------------------------
-constexpr int kPrepThreads = 256;
+__global__ __launch_bounds__(64 * kRouteWaves) void moe_route_kernel(RouteParams p) {
+  route_tokens<false>(p, (int64_t)blockIdx.x * kRouteWaves);
+}
 
-__device__ void moe_align_block(const int32_t* __restrict__ topk_ids, int64_t P, int top_k, int E,
-                                int32_t* __restrict__ offsets /* [E+1] */,
-                                int32_t* __restrict__ sorted_token /* [P] */,
-                                int32_t* __restrict__ pair_pos /* [P] */) {
+// ---------------------------------------------------------------------------
+// moe_front_kernel: what the expert products need, in one launch.
+//  * routing workgroups (route_wgs > 0): kRouteWaves tokens each; the last of
+//    them to finish (a device-scope counter in the workspace's counter block,
+//    which it resets) buckets the pairs;
+//  * transform workgroups: FWHT-128 of x into pair f16, one 128-block per
+//    16-lane group;
+//  * with the ids given (route_wgs == 0), one more workgroup buckets them.
+// Bucketing (one workgroup): LDS histogram of the T*top_k (token, slot) pairs
+// by expert, exclusive scan, scatter -> per-expert offsets, the token of each
+// sorted pair, the sorted position of each pair (-1 for an id outside
+// 0..E-1). Given ids may hold such slots: the output rows of tokens without
+// one valid slot are zeroed here, as no other kernel writes them.
+// ---------------------------------------------------------------------------
+constexpr int kFrontThreads = 64 * kRouteWaves;
+
+struct FrontArgs {
+  RouteParams r;          // r.logits null: the ids are given
+  int route_wgs, fwht_wgs;
+  const uint16_t* x;      // [T, H] fp16 or bf16
+  int nbc, xbf;           // 128-blocks per row; x is bfloat16
+  uint32_t* xtf;          // [T, H/2] pair f16
+  int32_t* offsets;       // [E + 1]
+  int32_t* sorted_token;  // [P]
+  int32_t* pair_pos;      // [P]
+  uint32_t* done;         // routing completion counter (zero; left zero)
+  uint16_t* out;          // [T, H]
+};
+
+constexpr int kAlignBatch = 8;  // ids per thread loaded before their use
+
+// COH: the ids were written by other workgroups of this launch (routing; all
+// valid by construction) and are read device-coherently; else they are the
+// caller's, read plainly, and may hold ids outside 0..E-1.
+template <bool COH>
+__device__ void moe_align_block(const FrontArgs& a) {
   __shared__ int cnt[256];
   __shared__ int base[257];
-  const int tid = threadIdx.x;
-  for (int e = tid; e < E; e += kPrepThreads) cnt[e] = 0;
+  __shared__ int wtot[kFrontThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int E = a.r.E, top_k = a.r.top_k;
+  const int64_t P = a.r.T * top_k;
+  const uint32_t* ids = reinterpret_cast<const uint32_t*>(a.r.topk_ids);
+  // the ids of pairs p0 + tid + kFrontThreads * u, all loads issued first
+  auto load_ids = [&](int64_t p0, int (&e)[kAlignBatch]) {
+#pragma unroll
+    for (int u = 0; u < kAlignBatch; ++u) {
+      const int64_t p = p0 + tid + (int64_t)kFrontThreads * u;
+      const int64_t pc = p < P ? p : P - 1;
+      e[u] = COH ? (int)ld_dev32(ids + pc) : (int)ids[pc];
+    }
+  };
+  constexpr int64_t kChunk = (int64_t)kFrontThreads * kAlignBatch;
+  for (int e = tid; e < E; e += kFrontThreads) cnt[e] = 0;
   __syncthreads();
-  for (int64_t p = tid; p < P; p += kPrepThreads) {
-    const int e = topk_ids[p];
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  for (int64_t p0 = 0; p0 < P; p0 += kChunk) {
+    int e[kAlignBatch];
+    load_ids(p0, e);
+#pragma unroll
+    for (int u = 0; u < kAlignBatch; ++u)
+      if (p0 + tid + (int64_t)kFrontThreads * u < P && e[u] >= 0 && e[u] < E) atomicAdd(&cnt[e[u]], 1);
   }
   __syncthreads();
-  if (tid == 0) {
-    int acc = 0;
-    for (int e = 0; e < E; ++e) {
-      base[e] = acc;
-      acc += cnt[e];
-    }
-    base[E] = acc;
+  // exclusive scan over the experts, thread e holding cnt[e] (E <= 256)
+  const int v = tid < E ? cnt[tid] : 0;
+  int incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += o;
   }
+  if (lane == 63) wtot[wave] = incl;
   __syncthreads();
-  for (int e = tid; e <= E; e += kPrepThreads) offsets[e] = base[e];
-  for (int e = tid; e < E; e += kPrepThreads) cnt[e] = 0;
+  int before = 0;
+  for (int w = 0; w < wave; ++w) before += wtot[w];
+  if (tid < E) {
+    base[tid] = before + incl - v;
+    cnt[tid] = 0;  // this thread's count, read above
+  }
+  if (tid == E - 1) base[E] = before + incl;
   __syncthreads();
-  for (int64_t p = tid; p < P; p += kPrepThreads) {
-    const int e = topk_ids[p];
-    int pos = -1;
-    if (e >= 0 && e < E) {
-      pos = base[e] + atomicAdd(&cnt[e], 1);
-      sorted_token[pos] = (int32_t)(p / top_k);
+  for (int e = tid; e <= E; e += kFrontThreads) a.offsets[e] = base[e];
+  for (int64_t p0 = 0; p0 < P; p0 += kChunk) {
+    int e[kAlignBatch];
+    load_ids(p0, e);
+#pragma unroll
+    for (int u = 0; u < kAlignBatch; ++u) {
+      const int64_t p = p0 + tid + (int64_t)kFrontThreads * u;
+      if (p >= P) continue;
+      int pos = -1;
+      if (e[u] >= 0 && e[u] < E) {
+        pos = base[e[u]] + atomicAdd(&cnt[e[u]], 1);
+        a.sorted_token[pos] = (int32_t)(p / top_k);
+      }
+      a.pair_pos[p] = pos;
     }
-    pair_pos[p] = pos;
+  }
+  if constexpr (!COH) {
+    const int64_t H = (int64_t)a.nbc * kBlock;
+    for (int64_t t = tid; t < a.r.T; t += kFrontThreads) {
+      bool any = false;
+      for (int k = 0; k < top_k; ++k) {
+        const int e = a.r.topk_ids[t * top_k + k];
+        any = any || (e >= 0 && e < E);
+      }
+      if (!any)
+        for (int64_t c = 0; c < H; ++c) a.out[t * H + c] = 0;
+    }
   }
 }
 
-__global__ __launch_bounds__(kPrepThreads) void moe_prep_kernel(
-    const uint16_t* __restrict__ x, int64_t T, int nbc, uint32_t* __restrict__ xtf, int fwht_wgs,
-    const int32_t* __restrict__ topk_ids, int64_t P, int top_k, int E, int32_t* __restrict__ offsets,
-    int32_t* __restrict__ sorted_token, int32_t* __restrict__ pair_pos, int xbf) {
-  if ((int)blockIdx.x == fwht_wgs) {  // whole workgroup
-    moe_align_block(topk_ids, P, top_k, E, offsets, sorted_token, pair_pos);
+__global__ __launch_bounds__(kFrontThreads) void moe_front_kernel(FrontArgs a) {
+  int bid = blockIdx.x;
+  if (bid < a.route_wgs) {
+    route_tokens<true>(a.r, (int64_t)bid * kRouteWaves);
+    // this workgroup's ids are stored once every thread's vmcnt drains
+    // (stores count there on this architecture); then it is counted in
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    __shared__ uint32_t last;
+    if (threadIdx.x == 0) last = atomicAdd(a.done, 1u) + 1 == (uint32_t)a.route_wgs ? 1u : 0u;
+    __syncthreads();
+    if (!last) return;  // uniform
+    moe_align_block<true>(a);
+    if (threadIdx.x == 0) __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
-  const int64_t total = T * (int64_t)nbc;
-  int64_t bid = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  bid -= a.route_wgs;
+  if (bid == a.fwht_wgs) {  // ids given: the bucketing workgroup (whole workgroup)
+    moe_align_block<false>(a);
+    return;
+  }
+  const int64_t total = a.r.T * (int64_t)a.nbc;
+  int64_t blk = (int64_t)bid * 16 + (threadIdx.x >> 4);
   const int q = threadIdx.x & 15;
-  const bool live = bid < total;
-  if (!live) bid = total - 1;  // the group stays converged; its store is masked
-  const int64_t r = bid / nbc;
-  const int cb = (int)(bid - r * nbc);
+  const bool live = blk < total;
+  if (!live) blk = total - 1;  // the group stays converged; its store is masked
   float v[8];
-  if (xbf) load8<PE_DTYPE_BF16>(x + (r * nbc + cb) * kBlock + q * 8, v);
-  else load8<PE_DTYPE_F16>(x + (r * nbc + cb) * kBlock + q * 8, v);
+  if (a.xbf) load8<PE_DTYPE_BF16>(a.x + blk * kBlock + q * 8, v);
+  else load8<PE_DTYPE_F16>(a.x + blk * kBlock + q * 8, v);
   fwht128_group16(v, q);
-  store_pair_block(v, q, xtf + bid * 64, live);
+  store_pair_block(v, q, a.xtf + blk * 64, live);
 }
 
 // out[t, c..c+3] = sum_k w[t, k] * y2[pos(t, k), c..c+3], k in order; 4
@@ -287,14 +390,14 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
 }
 
 struct MoeWs {
-  size_t offsets, sorted_token, pair_pos, xtf, htf, y2, total;
+  size_t offsets, sorted_token, pair_pos, topk_w, topk_ids, xtf, htf, y2, total;
 };
 
 static MoeWs moe_ws_layout(int64_t T, int top_k, int E, int H, int I) {
   const int64_t P = T * top_k;
   const int64_t Ip = (I + kBlock - 1) / kBlock * kBlock;
   MoeWs w{};
-  size_t o = kWsCounterBytes;  // the library-wide counter block stays untouched
+  size_t o = kWsCounterBytes;  // the library-wide counter block comes first
   auto take = [&](size_t bytes) {
     const size_t at = o;
     o += round_up(bytes, 256);
@@ -303,11 +406,140 @@ static MoeWs moe_ws_layout(int64_t T, int top_k, int E, int H, int I) {
   w.offsets = take((size_t)(E + 1) * 4);
   w.sorted_token = take((size_t)P * 4);
   w.pair_pos = take((size_t)P * 4);
+  w.topk_w = take((size_t)P * 4);
+  w.topk_ids = take((size_t)P * 4);
   w.xtf = take((size_t)T * H * 2);
   w.htf = take((size_t)P * Ip * 2);
   w.y2 = take((size_t)P * H * 4);
   w.total = o;
   return w;
+}
+
+// Checks of the routing arguments (n_group 0: plain top-k).
+static int route_check(int64_t T, int E, int top_k, int scoring, const float* bias, int n_group,
+                       int topk_group) {
+  if (T < 0 || E <= 0 || E > 256 || top_k <= 0 || top_k > 16 || top_k > E) return PE_ERR_DIMS;
+  if (scoring != 0 && scoring != 1) return PE_ERR_DTYPE;
+  // grouped: whole groups, at most 64 of them; the kept groups must hold
+  // top_k experts; a bias ranks groups by their two best experts
+  if (n_group != 0 &&
+      (n_group < 0 || n_group > kRouteMaxGroups || E % n_group || topk_group <= 0 ||
+       topk_group > n_group || top_k > topk_group * (E / n_group) || (bias && E / n_group < 2)))
+    return PE_ERR_DIMS;
+  return PE_OK;
+}
+
+struct MoeWeights {
+  const void* w13_codes;
+  int bits13, packed13;
+  const uint16_t* w13_norms;
+  const float* ct13;
+  int n_levels13;
+  const void* w2_codes;
+  int bits2, packed2;
+  const uint16_t* w2_norms;
+  const float* ct2;
+  int n_levels2;
+};
+
+// The launches of one MoE call. route: routing parameters (logits given) or
+// null (topk_w / topk_ids given).
+static int moe_run(const void* x, int x_dtype, int64_t T, int H, int I, int E, int top_k,
+                   const RouteParams* route, const float* topk_w, const int32_t* topk_ids,
+                   const MoeWeights& W, void* out, void* workspace, size_t workspace_bytes,
+                   hipStream_t st) {
+  if (!x || !W.w13_codes || !W.w13_norms || !W.ct13 || !W.w2_codes || !W.w2_norms || !W.ct2 || !out)
+    return PE_ERR_NULL;
+  if (!route && (!topk_w || !topk_ids)) return PE_ERR_NULL;
+  if (T < 0 || H <= 0 || I <= 0 || E <= 0 || E > 256 || top_k <= 0 || top_k > E) return PE_ERR_DIMS;
+  if (H % kBlock) return PE_ERR_DIMS;
+  const int xbf = bf16_flag(x_dtype);  // x and out: fp16 or bf16
+  if (xbf < 0) return PE_ERR_DTYPE;
+  for (int which = 0; which < 2; ++which) {
+    const int bits = which ? W.bits2 : W.bits13, packed = which ? W.packed2 : W.packed13;
+    const int nl = which ? W.n_levels2 : W.n_levels13;
+    if (bits < 2 || bits > 8 || (packed & ~(1 | PE_LAYOUT_TILE16)) || ((packed & 1) && bits > 4) ||
+        nl != (1 << bits))
+      return PE_ERR_BITS;
+  }
+  // tiled-16 experts: every expert's rows are whole 16-row tiles
+  if (((W.packed13 & PE_LAYOUT_TILE16) && (2 * I) % 16) || ((W.packed2 & PE_LAYOUT_TILE16) && H % 16))
+    return PE_ERR_DIMS;
+  if (!aligned16(x) || !aligned16(W.w13_codes) || !aligned16(W.w2_codes) || !aligned16(out))
+    return PE_ERR_ALIGN;
+  if (T == 0) return PE_OK;
+  const int64_t P = T * top_k;
+  if (P > INT32_MAX / 2) return PE_ERR_DIMS;
+  const MoeWs L = moe_ws_layout(T, top_k, E, H, I);
+  if (!workspace || workspace_bytes < L.total) return PE_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return PE_ERR_ALIGN;
+  char* ws = reinterpret_cast<char*>(workspace);
+  int32_t* offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
+  int32_t* sorted_token = reinterpret_cast<int32_t*>(ws + L.sorted_token);
+  int32_t* pair_pos = reinterpret_cast<int32_t*>(ws + L.pair_pos);
+  const int Ip = (I + kBlock - 1) / kBlock * kBlock;
+  const int nb13 = H / kBlock, nb2 = Ip / kBlock;
+  const bool nib13 = (W.packed13 & 1) != 0, nib2 = (W.packed2 & 1) != 0;
+  const bool tiled13 = (W.packed13 & PE_LAYOUT_TILE16) != 0, tiled2 = (W.packed2 & PE_LAYOUT_TILE16) != 0;
+  const int64_t row13 = nib13 ? (int64_t)nb13 * 64 : (int64_t)nb13 * kBlock;
+  const int64_t row2 = nib2 ? (int64_t)nb2 * 64 : (int64_t)nb2 * kBlock;
+
+  // 1. routing (or the given ids), x -> pair f16, the pairs bucketed by expert
+  {
+    FrontArgs f{};
+    if (route) {
+      f.r = *route;
+      f.r.topk_w = reinterpret_cast<float*>(ws + L.topk_w);
+      f.r.topk_ids = reinterpret_cast<int32_t*>(ws + L.topk_ids);
+      f.route_wgs = (int)((T + kRouteWaves - 1) / kRouteWaves);
+    } else {
+      f.r.T = T;
+      f.r.E = E;
+      f.r.top_k = top_k;
+      f.r.topk_w = const_cast<float*>(topk_w);
+      f.r.topk_ids = const_cast<int32_t*>(topk_ids);
+      f.route_wgs = 0;
+    }
+    const int64_t fwht_wgs = (T * (H / kBlock) + 15) / 16;
+    if (fwht_wgs + f.route_wgs + 1 > INT32_MAX) return PE_ERR_DIMS;
+    f.fwht_wgs = (int)fwht_wgs;
+    f.x = reinterpret_cast<const uint16_t*>(x);
+    f.nbc = H / kBlock;
+    f.xbf = xbf;
+    f.xtf = reinterpret_cast<uint32_t*>(ws + L.xtf);
+    f.offsets = offsets;
+    f.sorted_token = sorted_token;
+    f.pair_pos = pair_pos;
+    f.done = reinterpret_cast<uint32_t*>(ws);  // counter block word 0
+    f.out = reinterpret_cast<uint16_t*>(out);
+    const int grid = f.route_wgs + f.fwht_wgs + (route ? 0 : 1);
+    moe_front_kernel<<<dim3((unsigned)grid), dim3(kFrontThreads), 0, st>>>(f);
+    if (int rc = launch_status()) return rc;
+  }
+  const float* wts = route ? reinterpret_cast<const float*>(ws + L.topk_w) : topk_w;
+  // 2. gate/up + SwiGLU, each 128-column block of h transformed in the same
+  // kernel -> htf [P, Ip] pair f16 (columns past I are zero)
+  {
+    SmallArgs a{reinterpret_cast<const uint8_t*>(W.w13_codes), W.w13_norms, W.ct13, W.n_levels13,
+                reinterpret_cast<const uint32_t*>(ws + L.xtf), sorted_token, offsets,
+                2 * (int64_t)I * row13, 2 * (int64_t)I * nb13, ws + L.htf, Ip, nullptr, 0, I,
+                nb13, wlayout(nib13, tiled13, nb13)};
+    if (int rc = moe_grouped(nib13, SE_SWIGLU_XTF, a, E, st)) return rc;
+  }
+  // 3. down -> y2 [P, H] fp32
+  {
+    SmallArgs a{reinterpret_cast<const uint8_t*>(W.w2_codes), W.w2_norms, W.ct2, W.n_levels2,
+                reinterpret_cast<const uint32_t*>(ws + L.htf), nullptr, offsets,
+                (int64_t)H * row2, (int64_t)H * nb2, ws + L.y2, H, nullptr, 0, H, nb2,
+                wlayout(nib2, tiled2, nb2)};
+    if (int rc = moe_grouped(nib2, SE_F32, a, E, st)) return rc;
+  }
+  // 4. weighted combine -> out (x's dtype)
+  const int64_t work = T * (H / 4);
+  moe_combine_kernel<<<dim3((unsigned)((work + 255) / 256)), dim3(256), 0, st>>>(
+      reinterpret_cast<const float*>(ws + L.y2), wts, pair_pos, T, top_k, H,
+      reinterpret_cast<uint16_t*>(out), xbf);
+  return launch_status();
 }
 
 }  // namespace pe
@@ -318,14 +550,13 @@ static int route(const float* logits, int64_t T, int E, int top_k, int renormali
                  const float* correction_bias, int n_group, int topk_group, float* topk_w,
                  int32_t* topk_ids, hipStream_t st) {
   if (!logits || !topk_w || !topk_ids) return PE_ERR_NULL;
-  if (T < 0 || E <= 0 || E > 256 || top_k <= 0 || top_k > 16 || top_k > E) return PE_ERR_DIMS;
-  if (scoring != 0 && scoring != 1) return PE_ERR_DTYPE;
+  if (int rc = route_check(T, E, top_k, scoring, correction_bias, n_group, topk_group)) return rc;
   if (T == 0) return PE_OK;
   const int64_t wgs = (T + kRouteWaves - 1) / kRouteWaves;
   if (wgs > INT32_MAX) return PE_ERR_DIMS;
-  moe_route_kernel<<<dim3((unsigned)wgs), dim3(64 * kRouteWaves), 0, st>>>(
-      logits, T, E, top_k, renormalize, scoring, correction_bias, topk_w, topk_ids, n_group,
-      topk_group);
+  const RouteParams p{logits, T, E, top_k, renormalize, scoring, correction_bias, topk_w, topk_ids,
+                      n_group, topk_group};
+  moe_route_kernel<<<dim3((unsigned)wgs), dim3(64 * kRouteWaves), 0, st>>>(p);
   return launch_status();
 }
 
@@ -340,13 +571,7 @@ extern "C" int pe_moe_route_grouped(const float* logits, int64_t T, int E, int t
                                     int renormalize, int scoring, const float* correction_bias,
                                     int num_expert_group, int topk_group, float* topk_w,
                                     int32_t* topk_ids, void* stream) {
-  // whole groups, at most 64 of them; the kept groups must hold top_k experts;
-  // a bias ranks groups by their two best experts
-  if (num_expert_group <= 0 || num_expert_group > kRouteMaxGroups || E % num_expert_group ||
-      topk_group <= 0 || topk_group > num_expert_group ||
-      top_k > topk_group * (E / num_expert_group) ||
-      (correction_bias && E / num_expert_group < 2))
-    return PE_ERR_DIMS;
+  if (num_expert_group <= 0) return PE_ERR_DIMS;
   return route(logits, T, E, top_k, renormalize, scoring, correction_bias, num_expert_group,
                topk_group, topk_w, topk_ids, reinterpret_cast<hipStream_t>(stream));
 }
@@ -363,74 +588,29 @@ extern "C" int pe_moe_forward(const void* x, int x_dtype, int64_t T, int H, int 
                               const void* w2_codes, int bits2, int packed2,
                               const uint16_t* w2_norms, const float* ct2, int n_levels2,
                               void* out, void* workspace, size_t workspace_bytes, void* stream) {
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (!x || !topk_w || !topk_ids || !w13_codes || !w13_norms || !ct13 || !w2_codes ||
-      !w2_norms || !ct2 || !out)
-    return PE_ERR_NULL;
-  if (T < 0 || H <= 0 || I <= 0 || E <= 0 || E > 256 || top_k <= 0 || top_k > E) return PE_ERR_DIMS;
-  if (H % kBlock) return PE_ERR_DIMS;
-  const int xbf = bf16_flag(x_dtype);  // x and out: fp16 or bf16
-  if (xbf < 0) return PE_ERR_DTYPE;
-  for (int which = 0; which < 2; ++which) {
-    const int bits = which ? bits2 : bits13, packed = which ? packed2 : packed13;
-    const int nl = which ? n_levels2 : n_levels13;
-    if (bits < 2 || bits > 8 || (packed & ~(1 | PE_LAYOUT_TILE16)) || ((packed & 1) && bits > 4) ||
-        nl != (1 << bits))
-      return PE_ERR_BITS;
-  }
-  // tiled-16 experts: every expert's rows are whole 16-row tiles
-  if (((packed13 & PE_LAYOUT_TILE16) && (2 * I) % 16) || ((packed2 & PE_LAYOUT_TILE16) && H % 16))
-    return PE_ERR_DIMS;
-  if (!aligned16(x) || !aligned16(w13_codes) || !aligned16(w2_codes) || !aligned16(out))
-    return PE_ERR_ALIGN;
-  if (T == 0) return PE_OK;
-  const int64_t P = T * top_k;
-  if (P > INT32_MAX / 2) return PE_ERR_DIMS;
-  const MoeWs L = moe_ws_layout(T, top_k, E, H, I);
-  if (!workspace || workspace_bytes < L.total) return PE_ERR_WORKSPACE;
-  if (!aligned16(workspace)) return PE_ERR_ALIGN;
-  char* ws = reinterpret_cast<char*>(workspace);
-  int32_t* offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
-  int32_t* sorted_token = reinterpret_cast<int32_t*>(ws + L.sorted_token);
-  int32_t* pair_pos = reinterpret_cast<int32_t*>(ws + L.pair_pos);
-  const int Ip = (I + kBlock - 1) / kBlock * kBlock;
-  const int nb13 = H / kBlock, nb2 = Ip / kBlock;
-  const bool nib13 = (packed13 & 1) != 0, nib2 = (packed2 & 1) != 0;
-  const bool tiled13 = (packed13 & PE_LAYOUT_TILE16) != 0, tiled2 = (packed2 & PE_LAYOUT_TILE16) != 0;
-  const int64_t row13 = nib13 ? (int64_t)nb13 * 64 : (int64_t)nb13 * kBlock;
-  const int64_t row2 = nib2 ? (int64_t)nb2 * 64 : (int64_t)nb2 * kBlock;
+  const MoeWeights W{w13_codes, bits13, packed13, w13_norms, ct13, n_levels13,
+                     w2_codes,  bits2,  packed2,  w2_norms,  ct2,  n_levels2};
+  return moe_run(x, x_dtype, T, H, I, E, top_k, nullptr, topk_w, topk_ids, W, out, workspace,
+                 workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+}
 
-  // 1. x -> pair f16, and the pairs bucketed by expert (last workgroup)
-  {
-    const int nbc = H / kBlock;
-    const int64_t fwht_wgs = (T * nbc + 15) / 16;
-    if (fwht_wgs + 1 > INT32_MAX) return PE_ERR_DIMS;
-    moe_prep_kernel<<<dim3((unsigned)(fwht_wgs + 1)), dim3(kPrepThreads), 0, st>>>(
-        reinterpret_cast<const uint16_t*>(x), T, nbc, reinterpret_cast<uint32_t*>(ws + L.xtf),
-        (int)fwht_wgs, topk_ids, P, top_k, E, offsets, sorted_token, pair_pos, xbf);
-    if (int rc = launch_status()) return rc;
-  }
-  // 2. gate/up + SwiGLU, each 128-column block of h transformed in the same
-  // kernel -> htf [P, Ip] pair f16 (columns past I are zero)
-  {
-    SmallArgs a{reinterpret_cast<const uint8_t*>(w13_codes), w13_norms, ct13, n_levels13,
-                reinterpret_cast<const uint32_t*>(ws + L.xtf), sorted_token, offsets,
-                2 * (int64_t)I * row13, 2 * (int64_t)I * nb13, ws + L.htf, Ip, nullptr, 0, I,
-                nb13, wlayout(nib13, tiled13, nb13)};
-    if (int rc = moe_grouped(nib13, SE_SWIGLU_XTF, a, E, st)) return rc;
-  }
-  // 3. down -> y2 [P, H] fp32
-  {
-    SmallArgs a{reinterpret_cast<const uint8_t*>(w2_codes), w2_norms, ct2, n_levels2,
-                reinterpret_cast<const uint32_t*>(ws + L.htf), nullptr, offsets,
-                (int64_t)H * row2, (int64_t)H * nb2, ws + L.y2, H, nullptr, 0, H, nb2,
-                wlayout(nib2, tiled2, nb2)};
-    if (int rc = moe_grouped(nib2, SE_F32, a, E, st)) return rc;
-  }
-  // 4. weighted combine -> out (x's dtype)
-  const int64_t work = T * (H / 4);
-  moe_combine_kernel<<<dim3((unsigned)((work + 255) / 256)), dim3(256), 0, st>>>(
-      reinterpret_cast<const float*>(ws + L.y2), topk_w, pair_pos, T, top_k, H,
-      reinterpret_cast<uint16_t*>(out), xbf);
-  return launch_status();
+extern "C" int pe_moe_forward_routed(const void* x, int x_dtype, int64_t T, int H, int I, int E,
+                                     int top_k, const float* logits, int renormalize, int scoring,
+                                     const float* correction_bias, int num_expert_group,
+                                     int topk_group, const void* w13_codes, int bits13,
+                                     int packed13, const uint16_t* w13_norms, const float* ct13,
+                                     int n_levels13, const void* w2_codes, int bits2, int packed2,
+                                     const uint16_t* w2_norms, const float* ct2, int n_levels2,
+                                     void* out, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+  if (!logits) return PE_ERR_NULL;
+  if (int rc = route_check(T, E, top_k, scoring, correction_bias, num_expert_group, topk_group))
+    return rc;
+  if ((T + kRouteWaves - 1) / kRouteWaves > INT32_MAX / 2) return PE_ERR_DIMS;
+  const RouteParams r{logits, T, E, top_k, renormalize, scoring, correction_bias, nullptr, nullptr,
+                      num_expert_group, topk_group};
+  const MoeWeights W{w13_codes, bits13, packed13, w13_norms, ct13, n_levels13,
+                     w2_codes,  bits2,  packed2,  w2_norms,  ct2,  n_levels2};
+  return moe_run(x, x_dtype, T, H, I, E, top_k, &r, nullptr, nullptr, W, out, workspace,
+                 workspace_bytes, reinterpret_cast<hipStream_t>(stream));
 }

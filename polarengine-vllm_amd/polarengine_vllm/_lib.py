@@ -65,6 +65,11 @@ _SIGNATURES = {
                                 _vp, _c_int, _c_int, _vp, _vp, _c_int,
                                 _vp, _c_int, _c_int, _vp, _vp, _c_int,
                                 _vp, _vp, _c_sz, _vp]),
+    "pe_moe_forward_routed": (_c_int, [_vp, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_int,
+                                       _vp, _c_int, _c_int, _vp, _c_int, _c_int,
+                                       _vp, _c_int, _c_int, _vp, _vp, _c_int,
+                                       _vp, _c_int, _c_int, _vp, _vp, _c_int,
+                                       _vp, _vp, _c_sz, _vp]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

@@ -1,8 +1,9 @@
 """MoE methods (reference: polarengine_vllm/moe_method.py).
 
 * ``PolarQuantMoEMethod`` -- PolarQuant-quantized experts, all resident on
-  the GPU, run by the grouped-expert HIP path (``pe_moe_route`` +
-  ``pe_moe_forward``). The reference has no quantized expert compute (its
+  the GPU, run by the grouped-expert HIP path (``pe_moe_forward_routed``:
+  routing and experts in one call; ``pe_moe_forward`` when a custom routing
+  function supplies the ids). The reference has no quantized expert compute (its
   experts stay bf16 in vLLM's fused MoE); the math follows its in-repo MoE
   forward (nemotron_offload.py:172-226): scores -> top-k -> renormalise ->
   SwiGLU(w13 = [gate; up]) -> w2 -> weighted sum.
@@ -96,6 +97,28 @@ class PolarQuantMoEMethod:
                 setattr(layer, f"{name}_norms", nt.view(e, rows, norms.shape[2]))
                 setattr(layer, f"{name}_tiled", True)
 
+    @staticmethod
+    def _routing_args(router_logits: torch.Tensor, num_experts: int, scoring_func: str,
+                      e_score_correction_bias: Optional[torch.Tensor], use_grouped_topk: bool,
+                      num_expert_group: Optional[int], topk_group: Optional[int]):
+        """fp32 logits, fp32 bias (or None), scoring code, and the group
+        arguments of the C ABI (0, 0 for plain top-k)."""
+        dev = _lib.require_device(router_logits)
+        lg = router_logits.to(torch.float32).contiguous()
+        if lg.dim() != 2 or lg.shape[1] != num_experts:
+            raise ValueError(f"router logits of shape {tuple(lg.shape)} for {num_experts} experts")
+        bias = None
+        if e_score_correction_bias is not None:
+            bias = e_score_correction_bias.to(device=dev, dtype=torch.float32).contiguous()
+        scoring = {"softmax": 0, "sigmoid": 1}.get(scoring_func)
+        if scoring is None:
+            raise ValueError(f"unsupported scoring_func {scoring_func}")
+        if not use_grouped_topk:
+            return lg, bias, scoring, 0, 0
+        if num_expert_group is None or topk_group is None:
+            raise ValueError("grouped top-k needs num_expert_group and topk_group")
+        return lg, bias, scoring, int(num_expert_group), int(topk_group)
+
     def select_experts(self, router_logits: torch.Tensor, top_k: int, renormalize: bool,
                        scoring_func: str = "softmax",
                        e_score_correction_bias: Optional[torch.Tensor] = None,
@@ -104,29 +127,25 @@ class PolarQuantMoEMethod:
         """(topk_weights float32 [T, k], topk_ids int32 [T, k]) via pe_moe_route,
         or pe_moe_route_grouped for grouped top-k (vLLM's grouped_topk, the
         routing the reference's apply hands to vLLM with use_grouped_topk,
-        moe_method.py:74-89)."""
-        dev = _lib.require_device(router_logits)
-        lg = router_logits.to(torch.float32).contiguous()
-        t, e = lg.shape
+        moe_method.py:74-89). apply() routes inside pe_moe_forward_routed
+        instead; this is the routing alone, for callers that want the ids."""
+        lg, bias, scoring, n_group, t_group = self._routing_args(
+            router_logits, router_logits.shape[-1], scoring_func, e_score_correction_bias,
+            use_grouped_topk, num_expert_group, topk_group)
+        dev = lg.device
+        t = lg.shape[0]
         w = torch.empty(t, top_k, dtype=torch.float32, device=dev)
         ids = torch.empty(t, top_k, dtype=torch.int32, device=dev)
-        bias = None
-        if e_score_correction_bias is not None:
-            bias = e_score_correction_bias.to(device=dev, dtype=torch.float32).contiguous()
-        scoring = {"softmax": 0, "sigmoid": 1}.get(scoring_func)
-        if scoring is None:
-            raise ValueError(f"unsupported scoring_func {scoring_func}")
-        if use_grouped_topk:
-            if num_expert_group is None or topk_group is None:
-                raise ValueError("grouped top-k needs num_expert_group and topk_group")
+        if n_group:
             _lib.check(_lib.lib().pe_moe_route_grouped(
-                lg.data_ptr(), t, e, top_k, int(bool(renormalize)), scoring, _lib.ptr(bias),
-                int(num_expert_group), int(topk_group), w.data_ptr(), ids.data_ptr(),
+                lg.data_ptr(), t, lg.shape[1], top_k, int(bool(renormalize)), scoring,
+                _lib.ptr(bias), n_group, t_group, w.data_ptr(), ids.data_ptr(),
                 _lib.stream_ptr(dev)), "pe_moe_route_grouped")
             return w, ids
-        _lib.check(_lib.lib().pe_moe_route(lg.data_ptr(), t, e, top_k, int(bool(renormalize)),
-                                           scoring, _lib.ptr(bias), w.data_ptr(), ids.data_ptr(),
-                                           _lib.stream_ptr(dev)), "pe_moe_route")
+        _lib.check(_lib.lib().pe_moe_route(lg.data_ptr(), t, lg.shape[1], top_k,
+                                           int(bool(renormalize)), scoring, _lib.ptr(bias),
+                                           w.data_ptr(), ids.data_ptr(), _lib.stream_ptr(dev)),
+                   "pe_moe_route")
         return w, ids
 
     def apply(self, layer: torch.nn.Module, x: torch.Tensor, router_logits: torch.Tensor,
@@ -139,18 +158,42 @@ class PolarQuantMoEMethod:
         x_code = _lib.act_dtype(x)
         xs = x.reshape(-1, layer.hidden_size).contiguous()
         t = xs.shape[0]
-        if custom_routing_function is not None:
-            w, ids = custom_routing_function(hidden_states=xs, gating_output=router_logits,
-                                             topk=top_k, renormalize=renormalize)
-            w = w.to(torch.float32).contiguous()
-            ids = ids.to(torch.int32).contiguous()
-        else:
-            w, ids = self.select_experts(router_logits.reshape(t, -1), top_k, renormalize,
-                                         scoring_func, e_score_correction_bias, use_grouped_topk,
-                                         num_expert_group, topk_group)
         out = torch.empty_like(xs)
+        L = _lib.lib()
+        e, h, i = layer.num_experts, layer.hidden_size, layer.intermediate_size
+        weights = (layer.w13_codes.data_ptr(), self.bits13,
+                   _layout(layer.w13_packed, layer.w13_tiled), layer.w13_norms.data_ptr(),
+                   layer.w13_ct_scaled.data_ptr(), 1 << self.bits13,
+                   layer.w2_codes.data_ptr(), self.bits2, _layout(layer.w2_packed, layer.w2_tiled),
+                   layer.w2_norms.data_ptr(), layer.w2_ct_scaled.data_ptr(), 1 << self.bits2)
+        if custom_routing_function is None:
+            # routing and experts in one call (the routing shares the first launch)
+            lg, bias, scoring, n_group, t_group = self._routing_args(
+                router_logits.reshape(t, -1), e, scoring_func, e_score_correction_bias,
+                use_grouped_topk, num_expert_group, topk_group)
+            if t == 0:
+                return out.view(x.shape)
+            wsb = L.pe_moe_workspace_size(t, top_k, e, h, i)
+            ws = _lib.workspace(dev, wsb)
+            rc = L.pe_moe_forward_routed(
+                xs.data_ptr(), x_code, t, h, i, e, top_k, lg.data_ptr(), int(bool(renormalize)),
+                scoring, _lib.ptr(bias), n_group, t_group, *weights, out.data_ptr(), _lib.ptr(ws),
+                wsb, _lib.stream_ptr(dev))
+            _lib.check(rc, "pe_moe_forward_routed")
+            return out.view(x.shape)
+        w, ids = custom_routing_function(hidden_states=xs, gating_output=router_logits,
+                                         topk=top_k, renormalize=renormalize)
+        w = w.to(torch.float32).contiguous()
+        ids = ids.to(torch.int32).contiguous()
         if t == 0:
             return out.view(x.shape)
+        wsb = L.pe_moe_workspace_size(t, top_k, e, h, i)
+        ws = _lib.workspace(dev, wsb)
+        rc = L.pe_moe_forward(xs.data_ptr(), x_code, t, h, i, e, top_k, w.data_ptr(),
+                              ids.data_ptr(), *weights, out.data_ptr(), _lib.ptr(ws), wsb,
+                              _lib.stream_ptr(dev))
+        _lib.check(rc, "pe_moe_forward")
+        return out.view(x.shape)
         L = _lib.lib()
         e, h, i = layer.num_experts, layer.hidden_size, layer.intermediate_size
         wsb = L.pe_moe_workspace_size(t, top_k, e, h, i)

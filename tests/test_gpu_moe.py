@@ -1,0 +1,119 @@
+"""GPU tests of the MoE call's first launch, which routes the tokens,
+transforms x and buckets the pairs by expert (the last routing workgroup to
+finish buckets them, signalled through the workspace's counter block):
+
+* the routed entry (pe_moe_forward_routed, what apply() calls) and the
+  ids-given entry (pe_moe_forward, apply() with a custom routing function)
+  give bit-identical outputs on the same routing;
+* slots with an id outside 0..E-1 are skipped, a token without one valid
+  slot is exactly zero, a token routed twice to one expert adds both slots
+  (oracle.moe_forward at the north-star tolerance);
+* many routing workgroups (T = 2048: 512 of them);
+* the workspace's counter block is zero again after every call, and a
+  second call on the same workspace repeats the first bit for bit."""
+
+import numpy as np
+import pytest
+import torch
+
+import polar_oracle as O
+from gpu_helpers import DEV, check_close, say, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _layer(rng, e, hdim, inter, b13, b2, tile=True):
+    from test_gpu_kernels import _moe_layer
+    return _moe_layer(rng, e, hdim, inter, b13, b2, tile)
+
+
+@pytest.mark.parametrize("tile", [True, False])
+def test_routed_equals_given_ids(tile):
+    say(f"moe routed vs given ids tile={tile}")
+    rng = np.random.default_rng(901)
+    meth, layer, _ = _layer(rng, 16, 512, 384, 3, 4, tile)
+    x = to_dev(O.seeded_normal((64, 512), 1.0, 902))
+    logits = to_dev(O.seeded_normal((64, 16), 1.0, 903, np.float32))
+    w, ids = meth.select_experts(logits, 4, True)
+
+    def given(hidden_states, gating_output, topk, renormalize):
+        return w, ids
+
+    y_routed = meth.apply(layer, x, logits, 4, True)
+    y_given = meth.apply(layer, x, logits, 4, True, custom_routing_function=given)
+    torch.cuda.synchronize()
+    assert torch.equal(y_routed, y_given)
+
+
+@pytest.mark.parametrize("b2", [4, 6])  # w2 chunks of 256 (nibbles) and 128 (int8) columns
+def test_invalid_and_duplicate_slots(b2):
+    say(f"moe invalid/duplicate slots q{b2}")
+    rng = np.random.default_rng(910 + b2)
+    e, hdim, inter, t, k = 8, 384, 256, 12, 3
+    meth, layer, (w13, w2) = _layer(rng, e, hdim, inter, 3, b2)
+    x = O.seeded_normal((t, hdim), 1.0, 911)
+    ids = rng.integers(0, e, (t, k)).astype(np.int32)
+    ids[1, 2] = -1          # one slot without an expert
+    ids[2, :] = -1          # no valid slot: a zero row
+    ids[3, 0] = e           # an id past the experts
+    ids[4, :] = [5, 5, 2]   # twice to one expert
+    wts = (np.abs(O.seeded_normal((t, k), 1.0, 912, np.float32)) + 0.1).astype(np.float32)
+
+    def given(hidden_states, gating_output, topk, renormalize):
+        return to_dev(wts), to_dev(ids)
+
+    logits = to_dev(np.zeros((t, e), np.float32))
+    y = meth.apply(layer, to_dev(x), logits, k, True, custom_routing_function=given)
+    want = O.moe_forward(x, wts, ids, w13, w2).astype(np.float32)
+    got = y.float().cpu().numpy()
+    assert np.all(got[2] == 0.0)
+    check_close(got, want, f"moe slots q{b2}")
+
+
+def test_many_routing_workgroups():
+    say("moe T=2048 e=32 k=4")
+    rng = np.random.default_rng(920)
+    meth, layer, (w13, w2) = _layer(rng, 32, 256, 128, 3, 4)
+    x = O.seeded_normal((2048, 256), 1.0, 921)
+    logits = O.seeded_normal((2048, 32), 1.0, 922, np.float32)
+    y = meth.apply(layer, to_dev(x), to_dev(logits), 4, True)
+    w_ref, ids_ref = O.moe_route(logits, 4, True)
+    want = O.moe_forward(x, w_ref, ids_ref, w13, w2).astype(np.float32)
+    check_close(y.float().cpu().numpy(), want, "moe T=2048")
+
+
+def test_counter_block_left_zero():
+    say("moe counter block after calls")
+    from polarengine_vllm import _lib
+    from polarengine_vllm.moe_method import _layout
+    L = _lib.lib()
+    rng = np.random.default_rng(930)
+    meth, layer, _ = _layer(rng, 16, 512, 384, 3, 4)
+    t, e, h, i, k = 96, 16, 512, 384, 4
+    x = to_dev(O.seeded_normal((t, h), 1.0, 931)).half()
+    lg = to_dev(O.seeded_normal((t, e), 1.0, 932, np.float32))
+    wsb = L.pe_moe_workspace_size(t, k, e, h, i)
+    ws = torch.zeros(wsb, dtype=torch.uint8, device=DEV)
+    outs = []
+    for _ in range(2):
+        out = torch.empty_like(x)
+        rc = L.pe_moe_forward_routed(
+            x.data_ptr(), _lib.PE_DTYPE_F16, t, h, i, e, k, lg.data_ptr(), 1, 0, None, 0, 0,
+            layer.w13_codes.data_ptr(), 3, _layout(layer.w13_packed, layer.w13_tiled),
+            layer.w13_norms.data_ptr(), layer.w13_ct_scaled.data_ptr(), 8,
+            layer.w2_codes.data_ptr(), 4, _layout(layer.w2_packed, layer.w2_tiled),
+            layer.w2_norms.data_ptr(), layer.w2_ct_scaled.data_ptr(), 16,
+            out.data_ptr(), ws.data_ptr(), wsb, _lib.stream_ptr(torch.device(DEV)))
+        torch.cuda.synchronize()
+        _lib.check(rc, "pe_moe_forward_routed")
+        assert int(ws[:4096].count_nonzero()) == 0
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1])
+    assert L.pe_moe_forward_routed(
+        x.data_ptr(), _lib.PE_DTYPE_F16, t, h, i, e, k, lg.data_ptr(), 1, 0, None, 0, 0,
+        layer.w13_codes.data_ptr(), 3, _layout(layer.w13_packed, layer.w13_tiled),
+        layer.w13_norms.data_ptr(), layer.w13_ct_scaled.data_ptr(), 8,
+        layer.w2_codes.data_ptr(), 4, _layout(layer.w2_packed, layer.w2_tiled),
+        layer.w2_norms.data_ptr(), layer.w2_ct_scaled.data_ptr(), 16,
+        outs[0].data_ptr(), ws.data_ptr(), wsb - 256,
+        _lib.stream_ptr(torch.device(DEV))) == _lib.PE_ERR_WORKSPACE

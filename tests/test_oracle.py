@@ -350,3 +350,27 @@ def test_moe_forward_matches_per_token_loop():
             w2 = O.dequant_weight(c2[ex], n2[ex], ct2).astype(np.float64)[:, :inter]
             want[ti] += w[ti, j] * (w2 @ hh)
     np.testing.assert_allclose(got, want, rtol=2e-2, atol=2e-3)
+
+
+def test_moe_forward_duplicate_and_invalid_slots():
+    """A token routed twice to one expert adds both slots (the same as one
+    slot with the summed weight); ids outside 0..E-1 add nothing; a token
+    without one valid slot is zero."""
+    rng = np.random.default_rng(12)
+    e, hdim, inter, t = 4, 128, 128, 4
+    c13 = rng.integers(0, 8, (e, 2 * inter, hdim)).astype(np.int8)
+    n13 = (np.abs(rng.standard_normal((e, 2 * inter, 1))) * 0.3 + 0.05).astype(np.float16)
+    c2 = rng.integers(0, 16, (e, hdim, inter)).astype(np.int8)
+    n2 = (np.abs(rng.standard_normal((e, hdim, 1))) * 0.3 + 0.05).astype(np.float16)
+    w13, w2 = (c13, n13, O.ct_scaled(3)), (c2, n2, O.ct_scaled(4))
+    x = rng.standard_normal((t, hdim)).astype(np.float16)
+    ids = np.array([[1, 1], [2, -1], [-1, e], [3, 0]], np.int32)
+    w = np.array([[0.25, 0.5], [0.75, 0.5], [0.5, 0.5], [0.6, 0.4]], np.float32)
+    got = O.moe_forward(x, w, ids, w13, w2).astype(np.float32)
+    one = O.moe_forward(x, np.array([[0.75, 0.0]] * t, np.float32),
+                        np.array([[1, -1]] * t, np.int32), w13, w2).astype(np.float32)
+    np.testing.assert_allclose(got[0], one[0], rtol=1e-3, atol=1e-4)
+    two = O.moe_forward(x, np.array([[0.75, 0.0]] * t, np.float32),
+                        np.array([[2, -1]] * t, np.int32), w13, w2).astype(np.float32)
+    np.testing.assert_allclose(got[1], two[1], rtol=1e-3, atol=1e-5)
+    assert np.all(got[2] == 0.0)
