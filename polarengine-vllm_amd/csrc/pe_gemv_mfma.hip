@@ -558,8 +558,8 @@ constexpr int dec_ks() { return kDecW / TN; }
 // 16-lane groups of the workgroup
 static int dec_xc(int M, int nb, int nw) { return (M * nb + 4 * nw - 1) / (4 * nw); }
 
-// 16-row m-tiles per MFMA pass: 1 (M <= 16), 2 (M <= 32) or 4 (M <= 64)
-static int dec_mtd(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : 4; }
+// 16-row m-tiles per MFMA pass: 1 (M <= 16) or 2 (M <= 32 = kDecMaxRows)
+static int dec_mtd(int M) { return M <= 16 ? 1 : 2; }
 
 static size_t dec_lds(bool nibble, int M, int nb, int n_levels, int nw) {
   size_t lds = (size_t)table_entries(nibble, n_levels) * 256 + (size_t)M * (nb * 256 + 16);
@@ -650,7 +650,7 @@ static int launch_dec_tn(const DecArgs& a, hipStream_t st) {
 // K split over workgroups: 12 row tiles per workgroup (one K range per wave),
 // gridDim.y groups sized for at most one workgroup per CU. Returns the group
 // count, or 0 when the split does not apply (fewer than 2 groups, or one
-// group's activations still do not fit). M > 16 (two or four m-tiles) takes
+// group's activations still do not fit). M > 16 (two m-tiles) takes
 // more groups, and rounds, until one group's activations fit.
 constexpr int kSplitTN = 12;
 static int dec_split_groups(bool nibble, int M, int N, int nb, int n_levels) {
@@ -727,7 +727,7 @@ bool gemv_mfma_fits(bool nibble, int M, int N, int nb, int n_levels) {
   // layouts round N up to 16 rows)
   if ((int64_t)(N + 15) * nb * (nibble ? 64 : kBlock) >= (int64_t)1 << 31) return false;
   if (dec_use_split(nibble, M, N, nb, n_levels)) return true;
-  if (M > 16) return false;  // two or four m-tiles: the split path only
+  if (M > 16) return false;  // two m-tiles: the split path only
   // the workgroup's 4 * kDecW lane groups hold the activations in <= 8 registers
   return dec_xc(M, nb, kDecW) <= 8 && dec_lds(nibble, M, nb, n_levels, kDecW) <= 160 * 1024;
 }
