@@ -100,6 +100,55 @@ __device__ __forceinline__ void kv_unpack8(const uint8_t (&b)[NB], uint32_t (&c)
   }
 }
 
+// LDS table of the cell count (see kv_quantize_kernel)
+template <int NL>
+struct KvCells {
+  uint32_t* lo;   // [64] midpoints below cell c's lower bound (c - 32) w
+  float* mid;     // [64] the midpoint in cell c, divided by w; +inf if none
+  float inv_w;    // 1 / w = 2^-e
+};
+
+// Builds the table in LDS (the whole workgroup: it ends in a barrier) and
+// returns whether the midpoints fit: ascending, finite, at most one per cell.
+template <int NL>
+__device__ bool kv_cells_setup(const float (&mid)[NL - 1], KvCells<NL>& t) {
+  __shared__ uint32_t lo[64];
+  __shared__ float tm[64];
+  float amax = 0.f, gmin = INFINITY;
+  bool ok = true;
+#pragma unroll
+  for (int l = 0; l < NL - 1; ++l) {
+    ok = ok && (mid[l] == mid[l]) && fabsf(mid[l]) < 1e30f;
+    amax = fmaxf(amax, fabsf(mid[l]));
+    if (l + 1 < NL - 1) gmin = fminf(gmin, mid[l + 1] - mid[l]);
+  }
+  // smallest power of two w with 31 w >= amax
+  int e = 0;
+  (void)frexpf(amax / 31.f, &e);
+  float w = ldexpf(1.f, e);
+  if (31.f * w < amax) w *= 2.f;
+  ok = ok && amax > 0.f && w <= gmin && w >= 0x1p-100f;
+  t.lo = lo;
+  t.mid = tm;
+  t.inv_w = 1.f / w;  // exact: a power of two
+  if (ok && threadIdx.x < 64) {
+    const float b = (float)((int)threadIdx.x - 32) * w;  // exact
+    uint32_t n = 0;
+    float m = INFINITY;
+#pragma unroll
+    for (int l = 0; l < NL - 1; ++l) {
+      n += mid[l] < b ? 1u : 0u;
+      if (mid[l] >= b && (threadIdx.x == 63 || mid[l] < b + w)) m = mid[l] * t.inv_w;
+    }
+    lo[threadIdx.x] = threadIdx.x == 0 ? 0u : n;
+    tm[threadIdx.x] = m;
+  }
+  __syncthreads();
+  return ok;
+}
+
+// Grid-stride: each workgroup builds the cell table once, then quantizes
+// 256 / (D / 8) vectors per step.
 template <int D, int NBITS, int DT>
 __global__ __launch_bounds__(256) void kv_quantize_kernel(const void* __restrict__ x, int64_t ldx,
                                                           int64_t n_vec,
@@ -107,47 +156,73 @@ __global__ __launch_bounds__(256) void kv_quantize_kernel(const void* __restrict
                                                           uint8_t* __restrict__ packed,
                                                           uint16_t* __restrict__ norms) {
   constexpr int L = D / 8;
+  constexpr int VPS = 256 / L;        // vectors per workgroup step
   constexpr int RB = D * NBITS / 8;  // packed bytes per vector
   const int q = threadIdx.x & (L - 1);
-  const int64_t vec = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / L;
-  const bool live = vec < n_vec;
-  const int64_t vr = live ? vec : 0;  // dead groups work on vector 0, store nothing
-  float v[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = kv_load<DT>(x, vr * ldx + 8 * q + i);
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(v[i], v[i], ss);
-  ss = lanes_sum<L>(ss);
-  float nrm = __builtin_sqrtf(ss);
-  nrm = nrm > 1e-10f ? nrm : 1e-10f;
-  // rotated = (x / |x|) @ H * sqrt(D) = (raw transform of x) / |x|: the
-  // transform runs on x and one reciprocal scales the result
-  fwht_lanes_raw<L>(v, q);
-  const float inv = 1.f / nrm;
   // First-index argmin of |r - ct[l]| over ascending centroids = the number
   // of midpoints (ct[l] + ct[l+1]) / 2 strictly below r (a tie at a midpoint
-  // keeps the lower index); 2 VALU ops per level instead of a distance scan.
+  // keeps the lower index).
   constexpr int NL = 1 << NBITS;
   float mid[NL - 1];
 #pragma unroll
   for (int l = 0; l < NL - 1; ++l) mid[l] = (ct[l] + ct[l + 1]) * 0.5f;
-  uint32_t c[8];
+  // The count by cell: cells of width w = 2^e over [-32 w, 32 w), w chosen
+  // so that every midpoint lies in [-31 w, 31 w] and no cell holds two
+  // (uniform per workgroup). Scaling by a power of two is exact, so
+  // t = r / w computed as v * (inv / w) equals round(v * inv) / w, its floor
+  // is r's cell exactly, and r > m <=> t > m / w. Entry c holds the number
+  // of midpoints below the cell and the cell's own midpoint / w (+inf if
+  // none): one compare per element instead of NL - 1.
+  KvCells<NL> cells;
+  const bool by_cell = kv_cells_setup<NL>(mid, cells);
+  for (int64_t v0 = (int64_t)blockIdx.x * VPS; v0 < n_vec; v0 += (int64_t)gridDim.x * VPS) {
+    const int64_t vec = v0 + threadIdx.x / L;
+    const bool live = vec < n_vec;
+    const int64_t vr = live ? vec : 0;  // dead groups work on vector 0, store nothing
+    float v[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float r = v[i] * inv;
-    uint32_t k = 0;
+    for (int i = 0; i < 8; ++i) v[i] = kv_load<DT>(x, vr * ldx + 8 * q + i);
+    float ss = 0.f;
 #pragma unroll
-    for (int l = 0; l < NL - 1; ++l) k += r > mid[l] ? 1u : 0u;
-    c[i] = k;
+    for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(v[i], v[i], ss);
+    ss = lanes_sum<L>(ss);
+    float nrm = __builtin_sqrtf(ss);
+    nrm = nrm > 1e-10f ? nrm : 1e-10f;
+    // rotated = (x / |x|) @ H * sqrt(D) = (raw transform of x) / |x|: the
+    // transform runs on x and one reciprocal scales the result
+    fwht_lanes_raw<L>(v, q);
+    const float inv = 1.f / nrm;
+    uint32_t c[8];
+    if (by_cell) {  // uniform
+      const float s = inv * cells.inv_w;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        // the cell from t clamped to [-32, 31] (IEEE max: a NaN goes to
+        // cell 0, where it compares false: code 0, as the count gives); the
+        // compare on t itself
+        const float t = v[i] * s;
+        const int cell = (int)__builtin_floorf(fminf(fmaxf(t, -32.f), 31.f)) + 32;
+        c[i] = cells.lo[cell] + (t > cells.mid[cell] ? 1u : 0u);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float r = v[i] * inv;
+        uint32_t k = 0;
+#pragma unroll
+        for (int l = 0; l < NL - 1; ++l) k += r > mid[l] ? 1u : 0u;
+        c[i] = k;
+      }
+    }
+    if (live) {
+      uint8_t b[NBITS];
+      kv_pack8<NBITS>(c, b);
+      uint8_t* dst = packed + vec * RB + q * NBITS;
+#pragma unroll
+      for (int i = 0; i < NBITS; ++i) dst[i] = b[i];
+      if (q == 0) norms[vec] = f2bf_bits(nrm);
+    }
   }
-  if (!live) return;
-  uint8_t b[NBITS];
-  kv_pack8<NBITS>(c, b);
-  uint8_t* dst = packed + vec * RB + q * NBITS;
-#pragma unroll
-  for (int i = 0; i < NBITS; ++i) dst[i] = b[i];
-  if (q == 0) norms[vec] = f2bf_bits(nrm);
 }
 
 // bf16 pair; the conversion from float is gfx950's round-to-nearest-even
@@ -198,11 +273,15 @@ __global__ __launch_bounds__(256) void kv_dequantize_kernel(const uint8_t* __res
                  __builtin_bit_cast(uint32_t, o[2]), __builtin_bit_cast(uint32_t, o[3]));
 }
 
+// quantize workgroups: at most 8 per CU (grid-stride beyond that)
+constexpr int kKvqWgsPerCu = 8;
+
 template <int D, int NBITS>
 static int launch_kv_q(const void* x, int dt, int64_t ldx, int64_t n, const float* ct,
                        uint8_t* packed, uint16_t* norms, hipStream_t st) {
-  const int64_t threads = n * (D / 8);
-  const unsigned grid = (unsigned)((threads + 255) / 256);
+  const int64_t steps = (n * (D / 8) + 255) / 256;
+  const int64_t cap = (int64_t)num_cus() * kKvqWgsPerCu;
+  const unsigned grid = (unsigned)(steps < cap ? steps : cap);
   switch (dt) {
     case PE_DTYPE_BF16: kv_quantize_kernel<D, NBITS, PE_DTYPE_BF16><<<grid, 256, 0, st>>>(x, ldx, n, ct, packed, norms); break;
     case PE_DTYPE_F16: kv_quantize_kernel<D, NBITS, PE_DTYPE_F16><<<grid, 256, 0, st>>>(x, ldx, n, ct, packed, norms); break;

@@ -119,3 +119,61 @@ def test_presets_and_patch_model_attention():
         assert blk.attn._polar_kv_layer_idx == i and blk.attn._polar_kv_cache is vcache
         assert blk.attn.forward.__name__ == "wrapped_forward"
         assert not hasattr(blk, "_polar_kv_layer_idx")  # the backends were found, not the blocks
+
+
+def _count_codes(r, ct):
+    mid = ((ct[:-1] + ct[1:]) * np.float32(0.5)).astype(np.float32)
+    return (r[:, None] > mid[None, :]).sum(1)
+
+
+def _cell_codes(r, ct):
+    """The quantize kernel's count by cell (pe_kv.hip, kv_cells_setup and
+    the loop after it), restated on float32 numpy: power-of-two cells of
+    width w over [-32 w, 32 w) with every midpoint in [-31 w, 31 w] and at
+    most one per cell; code = midpoints below r's cell + (r > the cell's
+    midpoint), on t = r / w."""
+    mid = ((ct[:-1] + ct[1:]) * np.float32(0.5)).astype(np.float32)
+    amax = np.float32(np.abs(mid).max())
+    _, e = np.frexp(amax / np.float32(31))
+    w = np.float32(np.ldexp(1.0, int(e)))
+    if np.float32(31) * w < amax:
+        w = np.float32(w * 2)
+    assert w <= np.diff(mid).min()  # the table path applies to these codebooks
+    inv_w = np.float32(1) / w
+    lo = np.zeros(64, np.int64)
+    tm = np.full(64, np.inf, np.float32)
+    for c in range(64):
+        b = np.float32((c - 32) * w)
+        lo[c] = 0 if c == 0 else int((mid < b).sum())
+        for m in mid:
+            if m >= b and (c == 63 or m < b + w):
+                tm[c] = np.float32(m * inv_w)
+    t = (r * inv_w).astype(np.float32)
+    with np.errstate(invalid="ignore"):
+        cl = np.fmin(np.fmax(t, np.float32(-32)), np.float32(31))  # fmax: NaN -> -32
+        cell = np.floor(cl).astype(np.int64) + 32
+        return lo[cell] + (t > tm[cell])
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_kv_cell_count_equals_midpoint_count(bits):
+    """Pins the quantize kernel's one-compare code against the count of
+    midpoints below r on the values where an off-by-one would show: every
+    midpoint and its float neighbours, every cell boundary and its
+    neighbours, 0, +-inf, NaN, tiny and huge values, and random normals."""
+    ct = get_centroids(bits).numpy().astype(np.float32)
+    mid = ((ct[:-1] + ct[1:]) * np.float32(0.5)).astype(np.float32)
+    amax = np.float32(np.abs(mid).max())
+    _, e = np.frexp(amax / np.float32(31))
+    w = np.float32(np.ldexp(1.0, int(e)))
+    if np.float32(31) * w < amax:
+        w = np.float32(w * 2)
+    bounds = (np.arange(-33, 34) * w).astype(np.float32)
+    pts = np.concatenate([mid, bounds, np.array([0, -0.0, 1e-30, -1e-30, 1e30, -1e30], np.float32)])
+    near = np.concatenate([np.nextafter(pts, np.float32(np.inf)), np.nextafter(pts, np.float32(-np.inf))])
+    rng = np.random.default_rng(bits)
+    r = np.concatenate([pts, near, rng.standard_normal(200000).astype(np.float32) * 1.5,
+                        np.array([np.inf, -np.inf], np.float32)]).astype(np.float32)
+    np.testing.assert_array_equal(_cell_codes(r, ct), _count_codes(r, ct))
+    # NaN: code 0, as the count gives
+    assert _cell_codes(np.array([np.nan], np.float32), ct)[0] == 0 == _count_codes(np.array([np.nan], np.float32), ct)[0]
