@@ -225,6 +225,185 @@ __global__ __launch_bounds__(256) void kv_quantize_kernel(const void* __restrict
   }
 }
 
+// ---------------------------------------------------------------------------
+// D = 128 from bf16 or fp16: the transform on the matrix cores. One wave
+// quantizes 32 vectors per step, y^T = H x^T as 4 x 8 MFMAs 32x32x16 (A = a
+// 32 x 16 block of H, B = 16 positions x 32 vectors of x: lane l loads 8
+// consecutive positions of vector l % 32, one 16-byte load). Products of
+// bf16 / fp16 values by +-1 are exact and the sums fp32, as in the butterfly
+// (in another order). The sign blocks come from four register sets:
+// H[r][c] = (-1)^popcount(r & c), and for r = 32 mb + m (m = the lane's row)
+// and c = 16 kt + 8 h + j (h = lane / 32) the sign is the lane's base
+// F[j] = (-1)^(popcount(m & j & 7) + m3 h), times (-1)^(m4 kt0), times
+// (-1)^(mb0 kt1 + mb1 kt2), a compile-time constant: the block is +-F for
+// even kt and +-G, G = (-1)^m4 F, for odd kt. The accumulators come out with
+// lane l holding positions 32 mb + 8 (e / 4) + 4 h + e % 4 of vector l % 32:
+// half of every 8-position code group, the other half in lane l ^ 32.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+
+template <int DT>
+struct KvMfma {  // fp16
+  static constexpr uint32_t kOne2 = 0x3C003C00u;
+  static __device__ __forceinline__ float16v mma(u32x4v a, u32x4v b, float16v c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8v, a),
+                                                 __builtin_bit_cast(half8v, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float lo(uint32_t w) { return h2f((uint16_t)(w & 0xffff)); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return h2f((uint16_t)(w >> 16)); }
+};
+template <>
+struct KvMfma<PE_DTYPE_BF16> {
+  static constexpr uint32_t kOne2 = 0x3F803F80u;
+  static __device__ __forceinline__ float16v mma(u32x4v a, u32x4v b, float16v c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8v, a),
+                                                  __builtin_bit_cast(bf16x8v, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+};
+
+// MFMAs per step: 4 m-blocks x 8 k-steps
+constexpr int kKvmVecs = 32;  // vectors per wave step
+
+template <int NBITS, int DT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void kv_quantize_mfma_kernel(const void* __restrict__ x,
+                                                               int64_t ldx, int64_t n_vec,
+                                                               const float* __restrict__ ct,
+                                                               uint8_t* __restrict__ packed,
+                                                               uint16_t* __restrict__ norms) {
+  using K = KvMfma<DT>;
+  constexpr int D = 128, RB = D * NBITS / 8, NL = 1 << NBITS;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 31, h = lane >> 5;
+  float mid[NL - 1];
+#pragma unroll
+  for (int l = 0; l < NL - 1; ++l) mid[l] = (ct[l] + ct[l + 1]) * 0.5f;
+  KvCells<NL> cells;
+  const bool by_cell = kv_cells_setup<NL>(mid, cells);
+  // sign blocks F, -F, G, -G (pairs of 16-bit +-1)
+  u32x4v F, nF, G, nG;
+  {
+    const uint32_t hb = (uint32_t)(((n >> 3) & 1) & h);
+#pragma unroll
+    for (int jp = 0; jp < 4; ++jp) {
+      const uint32_t s0 = ((uint32_t)__builtin_popcount(n & (2 * jp) & 7) + hb) & 1u;
+      const uint32_t s1 = ((uint32_t)__builtin_popcount(n & (2 * jp + 1) & 7) + hb) & 1u;
+      F[jp] = K::kOne2 | (s0 << 15) | (s1 << 31);
+      nF[jp] = F[jp] ^ 0x80008000u;
+    }
+    const bool m4 = (n >> 4) & 1;
+#pragma unroll
+    for (int jp = 0; jp < 4; ++jp) {
+      G[jp] = m4 ? nF[jp] : F[jp];
+      nG[jp] = m4 ? F[jp] : nF[jp];
+    }
+  }
+  const int64_t stride = (int64_t)gridDim.x * 4 * kKvmVecs;
+  for (int64_t v0 = ((int64_t)blockIdx.x * 4 + wave) * kKvmVecs; v0 < n_vec; v0 += stride) {
+    const int64_t vec = v0 + n;
+    const bool live = vec < n_vec;
+    const int64_t vr = live ? vec : n_vec - 1;  // dead lanes repeat the last vector, store nothing
+    const char* src = reinterpret_cast<const char*>(x) + (vr * ldx + 8 * h) * 2;
+    u32x4v b[8];
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) b[kt] = *reinterpret_cast<const u32x4v*>(src + kt * 32);
+    // |x|: this lane's 64 positions, then the other half from lane ^ 32
+    float ss = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float a0 = K::lo(b[kt][w]), a1 = K::hi(b[kt][w]);
+        ss = __builtin_fmaf(a0, a0, ss);
+        ss = __builtin_fmaf(a1, a1, ss);
+      }
+    ss += __shfl_xor(ss, 32, 64);
+    float nrm = __builtin_sqrtf(ss);
+    nrm = nrm > 1e-10f ? nrm : 1e-10f;
+    const float inv = 1.f / nrm;
+    // m-blocks in pairs (two accumulators live); each pair's codes before
+    // the next pair's MFMAs. half[g]: the 4 codes of group g (positions
+    // 8 g + 4 h + 0..3)
+    uint32_t half[16];
+    const float s = inv * cells.inv_w;
+#pragma unroll
+    for (int mp = 0; mp < 2; ++mp) {
+      float16v acc[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[u][e] = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int mb = 2 * mp + u;
+          const bool neg = (((mb & 1) & (kt >> 1)) ^ ((mb >> 1) & (kt >> 2))) & 1;
+          const u32x4v a = (kt & 1) ? (neg ? nG : G) : (neg ? nF : F);
+          acc[u] = K::mma(a, b[kt], acc[u]);
+        }
+      uint32_t k[2][16];
+      if (by_cell) {  // uniform
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const float t = acc[u][e] * s;
+            const int cell = (int)__builtin_floorf(fminf(fmaxf(t, -32.f), 31.f)) + 32;
+            k[u][e] = cells.lo[cell] + (t > cells.mid[cell] ? 1u : 0u);
+          }
+      } else {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const float r = acc[u][e] * inv;
+            uint32_t c = 0;
+#pragma unroll
+            for (int l = 0; l < NL - 1; ++l) c += r > mid[l] ? 1u : 0u;
+            k[u][e] = c;
+          }
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          uint32_t hv = 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) hv |= k[u][4 * jj + i] << (NBITS * (3 - i));
+          half[4 * (2 * mp + u) + jj] = hv;
+        }
+    }
+    // whole groups: lane h = 0 keeps groups 0..7, h = 1 groups 8..15
+    uint32_t full[8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      const uint32_t send = h ? half[g] : half[8 + g];
+      const uint32_t recv = (uint32_t)__shfl_xor((int)send, 32, 64);
+      full[g] = h ? ((recv << (4 * NBITS)) | half[8 + g]) : ((half[g] << (4 * NBITS)) | recv);
+    }
+    // MSB-first bytes of the 8 groups: 8 NBITS bytes at byte 8 NBITS h of the row
+    uint32_t wds[2 * NBITS];
+#pragma unroll
+    for (int k = 0; k < 2 * NBITS; ++k) {
+      uint32_t wd = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int by = 4 * k + q, g = by / NBITS, bi = by % NBITS;
+        wd |= ((full[g] >> (8 * (NBITS - 1 - bi))) & 0xffu) << (8 * q);
+      }
+      wds[k] = wd;
+    }
+    if (live) {
+      uint2* dst = reinterpret_cast<uint2*>(packed + vec * RB + h * (8 * NBITS));
+#pragma unroll
+      for (int k = 0; k < NBITS; ++k) dst[k] = make_uint2(wds[2 * k], wds[2 * k + 1]);
+      if (h == 0) norms[vec] = f2bf_bits(nrm);
+    }
+  }
+}
+
 // bf16 pair; the conversion from float is gfx950's round-to-nearest-even
 // v_cvt_pk_bf16_f32
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
@@ -300,9 +479,33 @@ static int launch_kv_d(const uint8_t* packed, const uint16_t* norms, int64_t n, 
   return launch_status();
 }
 
+template <int NBITS>
+static int launch_kv_q_mfma(const void* x, int dt, int64_t ldx, int64_t n, const float* ct,
+                            uint8_t* packed, uint16_t* norms, hipStream_t st) {
+  const int64_t steps = (n + 4 * kKvmVecs - 1) / (4 * kKvmVecs);
+  const int64_t cap = (int64_t)num_cus() * kKvqWgsPerCu;
+  const unsigned grid = (unsigned)(steps < cap ? steps : cap);
+  if (dt == PE_DTYPE_BF16)
+    kv_quantize_mfma_kernel<NBITS, PE_DTYPE_BF16><<<grid, 256, 0, st>>>(x, ldx, n, ct, packed, norms);
+  else
+    kv_quantize_mfma_kernel<NBITS, PE_DTYPE_F16><<<grid, 256, 0, st>>>(x, ldx, n, ct, packed, norms);
+  return launch_status();
+}
+
 template <int D>
 static int kv_q_bits(int nbits, const void* x, int dt, int64_t ldx, int64_t n, const float* ct,
                      uint8_t* packed, uint16_t* norms, hipStream_t st) {
+  // D = 128 from 16-bit input with 16-byte aligned rows and codes: the
+  // transform on the matrix cores
+  if (D == 128 && (dt == PE_DTYPE_BF16 || dt == PE_DTYPE_F16) && aligned16(x) &&
+      (ldx * 2) % 16 == 0 && aligned16(packed)) {
+    switch (nbits) {
+      case 2: return launch_kv_q_mfma<2>(x, dt, ldx, n, ct, packed, norms, st);
+      case 3: return launch_kv_q_mfma<3>(x, dt, ldx, n, ct, packed, norms, st);
+      case 4: return launch_kv_q_mfma<4>(x, dt, ldx, n, ct, packed, norms, st);
+      default: return PE_ERR_BITS;
+    }
+  }
   switch (nbits) {
     case 2: return launch_kv_q<D, 2>(x, dt, ldx, n, ct, packed, norms, st);
     case 3: return launch_kv_q<D, 3>(x, dt, ldx, n, ct, packed, norms, st);

@@ -102,8 +102,12 @@ def test_kv_kernels_match_reference_golden(gkv, d, bits):
                       f"golden deq d{d} b{bits}")
 
 
+# D = 128 from bf16 / fp16 takes the matrix-core transform (counts that are
+# not multiples of the 32-vector wave step included); fp32 and D = 64 / 256
+# the butterfly kernel
 CASES = [(1, 128, 3, "bf16"), (37, 64, 2, "f16"), (1000, 128, 4, "f32"), (513, 256, 3, "bf16"),
-         (4096, 128, 2, "bf16"), (77, 256, 4, "f16"), (300, 64, 4, "f32"), (2049, 256, 2, "f32")]
+         (4096, 128, 2, "bf16"), (77, 256, 4, "f16"), (300, 64, 4, "f32"), (2049, 256, 2, "f32"),
+         (999, 128, 3, "f16"), (130, 128, 4, "bf16"), (33, 128, 2, "f16")]
 
 
 @pytest.mark.parametrize("n,d,bits,dt", CASES)
