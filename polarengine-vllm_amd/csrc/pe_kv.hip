@@ -267,11 +267,10 @@ struct KvMfma<PE_DTYPE_BF16> {
 constexpr int kKvmVecs = 32;  // vectors per wave step
 
 template <int NBITS, int DT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void kv_quantize_mfma_kernel(const void* __restrict__ x,
-                                                               int64_t ldx, int64_t n_vec,
-                                                               const float* __restrict__ ct,
-                                                               uint8_t* __restrict__ packed,
-                                                               uint16_t* __restrict__ norms) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+void kv_quantize_mfma_kernel(const void* __restrict__ x, int64_t ldx, int64_t n_vec,
+                             const float* __restrict__ ct, uint8_t* __restrict__ packed,
+                             uint16_t* __restrict__ norms) {
   using K = KvMfma<DT>;
   constexpr int D = 128, RB = D * NBITS / 8, NL = 1 << NBITS;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -408,6 +407,148 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
 // v_cvt_pk_bf16_f32
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 
+// ---------------------------------------------------------------------------
+// Expansion at D = 128 on the matrix cores: x^T = H v^T with
+// v = ct[code] / sqrt(D) / sqrt(D) (fp32, split into an fp16 hi + lo pair so
+// the two products keep fp32 accuracy), then x * norm in bf16. The
+// B operand (8 consecutive positions of one vector per lane) comes from the
+// lane's 8-code group: group 2 kt + h of the packed row, read as one 8-byte
+// window and a per-lane shift, the values by ds_bpermute from the lanes
+// holding the codebook. The compile-time part of the sign, (-1)^(mb0 kt1 +
+// mb1 kt2), is a 4-point Hadamard over the m-blocks: four partial sums
+// S[kt1 + 2 kt2] = sum over kt0 of (F or G) x B(kt) take 16 MFMAs per 32
+// vectors (8 k-steps x hi/lo), and D[mb] = sum (-1)^(mb0 a + mb1 b) S[a + 2b]
+// two add stages.
+// ---------------------------------------------------------------------------
+template <int NBITS>
+__device__ __forceinline__ uint32_t kv_group(const uint32_t (&d)[4 * NBITS], int kt, int h) {
+  // bytes [(2 kt + h) NBITS, + NBITS) of the row, MSB first
+  constexpr int W = 4 * NBITS;
+  const int off0 = 2 * kt * NBITS, w0 = off0 / 4;
+  const uint64_t win = (uint64_t)d[w0] | ((uint64_t)(w0 + 1 < W ? d[w0 + 1] : 0u) << 32);
+  const uint32_t b = (uint32_t)(win >> (8 * (off0 % 4) + 8 * NBITS * h));
+  if constexpr (NBITS == 2) return ((b & 0xffu) << 8) | ((b >> 8) & 0xffu);
+  else if constexpr (NBITS == 3) return ((b & 0xffu) << 16) | (b & 0xff00u) | ((b >> 16) & 0xffu);
+  else return __builtin_bswap32(b);
+}
+
+constexpr int kKvtRow = 66;  // dwords per LDS tile row: 256 bytes + 8 of padding
+
+template <int NBITS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+void kv_dequantize_mfma_kernel(const uint8_t* __restrict__ packed,
+                               const uint16_t* __restrict__ norms, int64_t n_vec,
+                               const float* __restrict__ ct, uint16_t* __restrict__ out,
+                               int64_t ldo) {
+  constexpr int RB = 128 * NBITS / 8, NL = 1 << NBITS;
+  __shared__ uint32_t kvt[4 * kKvmVecs * kKvtRow];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 31, h = lane >> 5;
+  // lane j holds (hi, lo) of the value of code j mod 2^NBITS as two fp16
+  uint32_t tv;
+  {
+    // ct / sqrt(D) as the reference divides, times 1 / sqrt(D) of the
+    // normalised transform (one product per output left: the norm)
+    const float val = ct[lane & (NL - 1)] / 11.313708498984761f * kInvSqrt128;
+    const _Float16 vh = (_Float16)val;
+    const _Float16 vl = (_Float16)(val - (float)vh);
+    tv = (uint32_t)__builtin_bit_cast(uint16_t, vh) | ((uint32_t)__builtin_bit_cast(uint16_t, vl) << 16);
+  }
+  u32x4v F, G;
+  {
+    const uint32_t hb = (uint32_t)(((n >> 3) & 1) & h);
+#pragma unroll
+    for (int jp = 0; jp < 4; ++jp) {
+      const uint32_t s0 = ((uint32_t)__builtin_popcount(n & (2 * jp) & 7) + hb) & 1u;
+      const uint32_t s1 = ((uint32_t)__builtin_popcount(n & (2 * jp + 1) & 7) + hb) & 1u;
+      F[jp] = 0x3C003C00u | (s0 << 15) | (s1 << 31);
+    }
+    const uint32_t m4 = ((n >> 4) & 1) ? 0x80008000u : 0u;
+#pragma unroll
+    for (int jp = 0; jp < 4; ++jp) G[jp] = F[jp] ^ m4;
+  }
+  const int64_t stride = (int64_t)gridDim.x * 4 * kKvmVecs;
+  for (int64_t v0 = ((int64_t)blockIdx.x * 4 + wave) * kKvmVecs; v0 < n_vec; v0 += stride) {
+    const int64_t vr = v0 + n < n_vec ? v0 + n : n_vec - 1;  // past the end: the last vector
+    uint32_t d[4 * NBITS];
+    {
+      const u32x4v* src = reinterpret_cast<const u32x4v*>(packed + vr * RB);
+#pragma unroll
+      for (int i = 0; i < NBITS; ++i) {
+        const u32x4v q = src[i];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) d[4 * i + k] = q[k];
+      }
+    }
+    const float nrm = bf2f(norms[vr]);
+    float16v S[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) S[u][e] = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) {
+      const uint32_t grp = kv_group<NBITS>(d, kt, h);
+      uint32_t w[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        // code j at address bits 2.. (ds_bpermute takes lane = bits 2..7);
+        // higher codes left in bits 2 + NBITS..7 select the same value, the
+        // table repeating every 2^NBITS lanes
+        const int s2 = NBITS * (7 - j) - 2;
+        const uint32_t addr = s2 >= 0 ? grp >> (s2 >= 0 ? s2 : 0) : grp << (s2 < 0 ? -s2 : 0);
+        w[j] = (uint32_t)__builtin_amdgcn_ds_bpermute((int)addr, (int)tv);
+      }
+      u32x4v bh, bl;
+#pragma unroll
+      for (int jp = 0; jp < 4; ++jp) {
+        bh[jp] = __builtin_amdgcn_perm(w[2 * jp + 1], w[2 * jp], 0x05040100u);
+        bl[jp] = __builtin_amdgcn_perm(w[2 * jp + 1], w[2 * jp], 0x07060302u);
+      }
+      const u32x4v a = (kt & 1) ? G : F;
+      const int ab = (kt >> 1) & 3;  // kt1 + 2 kt2
+      S[ab] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8v, a),
+                                                     __builtin_bit_cast(half8v, bh), S[ab], 0, 0, 0);
+      S[ab] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8v, a),
+                                                     __builtin_bit_cast(half8v, bl), S[ab], 0, 0, 0);
+    }
+    // D[0] = S0 + S1 + S2 + S3, D[1] = S0 - S1 + S2 - S3, D[2] = S0 + S1 - S2 - S3,
+    // D[3] = S0 - S1 - S2 + S3; lane l holds positions 32 mb + 8 (e / 4) + 4 h + e % 4
+    // of vector l % 32. The wave's 32 x 256-byte tile goes through LDS (rows
+    // padded by 8 bytes so the 8-byte writes of 32 rows hit distinct banks)
+    // and leaves as 16-byte stores, 16 lanes per row.
+    uint32_t* tile = kvt + wave * (kKvmVecs * kKvtRow);
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        float y[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int e = 4 * jj + i;
+          const float t0 = S[0][e] + S[1][e], t1 = S[0][e] - S[1][e];
+          const float t2 = S[2][e] + S[3][e], t3 = S[2][e] - S[3][e];
+          const float yy = mb == 0 ? t0 + t2 : mb == 1 ? t1 + t3 : mb == 2 ? t0 - t2 : t1 - t3;
+          y[i] = yy * nrm;
+        }
+        bf16x2v o0, o1;
+        o0.x = (__bf16)y[0];
+        o0.y = (__bf16)y[1];
+        o1.x = (__bf16)y[2];
+        o1.y = (__bf16)y[3];
+        *reinterpret_cast<uint2*>(tile + n * kKvtRow + 16 * mb + 4 * jj + 2 * h) =
+            make_uint2(__builtin_bit_cast(uint32_t, o0), __builtin_bit_cast(uint32_t, o1));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kKvmVecs / 4; ++i) {
+      const int r = 4 * i + (lane >> 4), c = lane & 15;
+      const uint4 q = *reinterpret_cast<const uint4*>(tile + r * kKvtRow + 4 * c);
+      if (v0 + r < n_vec) *reinterpret_cast<uint4*>(out + (v0 + r) * ldo + 8 * c) = q;
+    }
+  }
+}
+
 template <int D, int NBITS>
 __global__ __launch_bounds__(256) void kv_dequantize_kernel(const uint8_t* __restrict__ packed,
                                                             const uint16_t* __restrict__ norms,
@@ -473,6 +614,14 @@ static int launch_kv_q(const void* x, int dt, int64_t ldx, int64_t n, const floa
 template <int D, int NBITS>
 static int launch_kv_d(const uint8_t* packed, const uint16_t* norms, int64_t n, const float* ct,
                        uint16_t* out, int64_t ldo, hipStream_t st) {
+  // D = 128 with 16-byte aligned packed rows: the transform on the matrix cores
+  if (D == 128 && aligned16(packed)) {
+    const int64_t steps = (n + 4 * kKvmVecs - 1) / (4 * kKvmVecs);
+    const int64_t cap = (int64_t)num_cus() * kKvqWgsPerCu;
+    const unsigned g = (unsigned)(steps < cap ? steps : cap);
+    kv_dequantize_mfma_kernel<NBITS><<<g, 256, 0, st>>>(packed, norms, n, ct, out, ldo);
+    return launch_status();
+  }
   const int64_t threads = n * (D / 8);
   const unsigned grid = (unsigned)((threads + 255) / 256);
   kv_dequantize_kernel<D, NBITS><<<grid, 256, 0, st>>>(packed, norms, n, ct, out, ldo);
