@@ -445,6 +445,50 @@ def decoder_layer_extra(dev):
     return out
 
 
+def e2e_extra(dev, context=1024, steps=32):
+    """End-to-end greedy decode through polarengine_vllm.decode_runner (the
+    model runner vLLM would provide; vLLM is not in this image): a model of
+    Qwen3-8B's shapes (36 layers, hidden 4096, 32 / 8 heads of 128,
+    intermediate 12288, vocabulary 151936) with random codes at the C4 bits
+    (qkv Q5, o Q6, gate_up Q3, down Q4), bf16 embeddings / lm_head, a static
+    bf16 KV cache of context + 64 positions, attention over it in torch. The
+    step (all 36 layers, the lm_head and the argmax) is one HIP graph replay;
+    tokens/s for the batch from `context`. quantized_linears_ms: the step's
+    144 quantized linears alone (one graph replay of all of them); the rest
+    of the step is torch (norms, rotary, cache writes, attention, SiLU,
+    residual, lm_head)."""
+    from polarengine_vllm.decode_runner import DecodeRunner, qwen3_8b_shapes
+    cfg = qwen3_8b_shapes()
+    out = {}
+    for batch in (1, 16):
+        run = DecodeRunner(cfg, batch, context + 64, dev, seed=7)
+        r = run.greedy_tokens_per_s(context, steps, warmup=2)
+        # the step's quantized linears alone (all layers, same inputs shapes)
+        ins = {"qkv_proj": torch.randn(batch, cfg.hidden, device=dev, dtype=torch.bfloat16),
+               "o_proj": torch.randn(batch, cfg.heads * cfg.head_dim, device=dev,
+                                     dtype=torch.bfloat16),
+               "gate_up_proj": torch.randn(batch, cfg.hidden, device=dev, dtype=torch.bfloat16),
+               "down_proj": torch.randn(batch, cfg.intermediate, device=dev, dtype=torch.bfloat16)}
+
+        def linears(run=run, ins=ins):
+            for ly in run.layers:
+                for nm in ("qkv_proj", "o_proj", "gate_up_proj", "down_proj"):
+                    ly[nm](ins[nm])
+        t_lin, _ = time_graph([linears], 1, 2, 4, dev)
+        lin_bytes = sum(ly[nm].codes_packed.numel() if ly[nm].packed else ly[nm].codes.numel()
+                        for ly in run.layers for nm in ("qkv_proj", "o_proj", "gate_up_proj",
+                                                        "down_proj"))
+        out[f"e2e_decode_b{batch}"] = {
+            "tok_per_s": round(r["tok_per_s"], 1), "ms_per_step": round(r["ms_per_step"], 3),
+            "quantized_linears_ms": round(t_lin * 1e3, 3),
+            "context": context, "steps": steps, "layers": cfg.layers,
+            "quantized_code_bytes": int(lin_bytes),
+            "model": "Qwen3-8B shapes, random codes (qkv Q5, o Q6, gate_up Q3, down Q4), bf16 lm_head"}
+        del run
+        torch.cuda.empty_cache()
+    return out
+
+
 TRACE_JSON = os.path.join(ROOT, "profiles", "trace_gemv_q4_12288x4096_m1.json")
 
 
@@ -493,7 +537,7 @@ def main():
     ap.add_argument("--headline-only", action="store_true",
                     help="time only the headline call (for a rocprofv3 kernel trace whose "
                          "dispatches are exactly the headline's)")
-    ap.add_argument("--only-extra", choices=("moe", "prefill", "kv", "layer", "decode"),
+    ap.add_argument("--only-extra", choices=("moe", "prefill", "kv", "layer", "decode", "e2e"),
                     help="time only one of the extra workloads and print its JSON (for a "
                          "rocprofv3 kernel trace of that path alone)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -519,7 +563,7 @@ def main():
         return
     if args.only_extra:
         fn = {"moe": moe_extra, "prefill": prefill_extra, "kv": kv_extra,
-              "layer": decoder_layer_extra, "decode": decode_extra}[args.only_extra]
+              "layer": decoder_layer_extra, "decode": decode_extra, "e2e": e2e_extra}[args.only_extra]
         print(json.dumps(fn(dev)))
         return
 
@@ -545,6 +589,7 @@ def main():
                              "note": "one weight copy, Infinity-Cache resident"}
     extra.update(kv_extra(dev))
     extra.update(moe_extra(dev))
+    extra.update(e2e_extra(dev))
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     traffic = None  # HBM bytes per launch from the committed pmc summary, if any
