@@ -180,6 +180,9 @@ __device__ __forceinline__ void dec_table_write(const DecTable<NIB>& t, int n_le
 // writes fp32 partial sums part[blockIdx.y][M][N], and the last of the
 // gridDim.y workgroups of a row group to finish (counted in cnt[blockIdx.x])
 // adds the groups' partials in group order, writes y and resets its counter.
+// partial-sum slabs the last group loads at once
+constexpr int kSplitBatch = 16;
+
 template <bool NIB, int TN, int KS, bool XRAW, bool MASK, int XC, int D, bool CTV, bool SPLIT,
           int MTD = 1>
 __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
@@ -469,13 +472,14 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
       if (n >= N) continue;
       const uint32_t off0 = (uint32_t)(((int64_t)m * N + n) * 4);
       const uint32_t gstep = (uint32_t)(slab * 4);
-      // groups in order 0, 1, .., eight loads in flight (coherent sc1 reads:
-      // the other groups' partials, never a stale line of this XCD's L2)
+      // groups in order 0, 1, .., sixteen loads in flight (coherent sc1
+      // reads: the other groups' partials, never a stale line of this XCD's
+      // L2); G <= 16 (on 256 CUs every N >= 3072) takes one round trip
       float a[4] = {0.f, 0.f, 0.f, 0.f};
-      for (int g0 = 0; g0 < G; g0 += 8) {
-        u32x4v t[8];
+      for (int g0 = 0; g0 < G; g0 += kSplitBatch) {
+        u32x4v t[kSplitBatch];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
+        for (int k = 0; k < kSplitBatch; ++k) {
           if (g0 + k < G) {
             const uint32_t off = off0 + (uint32_t)(g0 + k) * gstep;
             if (vec) {
@@ -492,7 +496,7 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
         // (bit_cast of a whole vector: this compiler reads element 0 when a
         // bit_cast is applied to a vector element)
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
+        for (int k = 0; k < kSplitBatch; ++k)
           if (g0 + k < G) {
             const float4v tf = __builtin_bit_cast(float4v, t[k]);
 #pragma unroll
