@@ -226,6 +226,80 @@ __device__ __forceinline__ void fwht128_group16(float v[8], int q) {
   for (int i = 0; i < 8; ++i) v[i] *= kInvSqrt128;
 }
 
+// ---------------------------------------------------------------------------
+// H128 on the matrix cores: y^T = H x^T for 32 vectors of 128 as 4 m-blocks x
+// 8 k-steps of v_mfma_f32_32x32x16 (A = a 32 x 16 block of H, B = 16
+// positions x 32 vectors: lane l holds positions 16 kt + 8 h .. + 7 of
+// vector l % 32, h = l / 32). Products of 16-bit values by +-1 are exact and
+// the sums fp32. For r = 32 mb + m (m = l % 32) and c = 16 kt + 8 h + j,
+// H[r][c] = (-1)^popcount(r & c) = F[j] * (-1)^(m4 kt0) * (-1)^(mb0 kt1 +
+// mb1 kt2) with the lane's base F[j] = (-1)^(popcount(m & j & 7) + m3 h), so
+// every A block is one of F, -F, G = (-1)^m4 F, -G (16 registers). The
+// accumulator of m-block mb holds, in lane l, positions
+// 32 mb + 8 (e / 4) + 4 h + e % 4 (e = 0..15) of vector l % 32.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+
+struct H128Signs {
+  u32x4v F, nF, G, nG;
+};
+
+// ONE2: two 16-bit ones (fp16 0x3C003C00, bf16 0x3F803F80); the sign bits
+// sit at 15 and 31 in both formats
+template <uint32_t ONE2>
+__device__ __forceinline__ H128Signs h128_signs(int lane) {
+  const int n = lane & 31, h = lane >> 5;
+  const uint32_t hb = (uint32_t)(((n >> 3) & 1) & h);
+  H128Signs s;
+#pragma unroll
+  for (int jp = 0; jp < 4; ++jp) {
+    const uint32_t s0 = ((uint32_t)__builtin_popcount(n & (2 * jp) & 7) + hb) & 1u;
+    const uint32_t s1 = ((uint32_t)__builtin_popcount(n & (2 * jp + 1) & 7) + hb) & 1u;
+    s.F[jp] = ONE2 | (s0 << 15) | (s1 << 31);
+    s.nF[jp] = s.F[jp] ^ 0x80008000u;
+  }
+  const bool m4 = (n >> 4) & 1;
+#pragma unroll
+  for (int jp = 0; jp < 4; ++jp) {
+    s.G[jp] = m4 ? s.nF[jp] : s.F[jp];
+    s.nG[jp] = m4 ? s.F[jp] : s.nF[jp];
+  }
+  return s;
+}
+
+// the A block of H for m-block mb, k-step kt (mb, kt compile-time after unrolling)
+__device__ __forceinline__ u32x4v h128_block(const H128Signs& s, int mb, int kt) {
+  const bool neg = (((mb & 1) & (kt >> 1)) ^ ((mb >> 1) & (kt >> 2))) & 1;
+  return (kt & 1) ? (neg ? s.nG : s.G) : (neg ? s.nF : s.F);
+}
+
+// accumulators of m-blocks mb0 and mb1 (raw H x, no normalisation) from the
+// lane's eight 16-byte position groups b[kt]; BF: the values are bfloat16
+template <bool BF>
+__device__ __forceinline__ void h128_mfma_pair(const H128Signs& s, const u32x4v (&b)[8], int mb0,
+                                               int mb1, float16v& a0, float16v& a1) {
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    a0[e] = 0.f;
+    a1[e] = 0.f;
+  }
+#pragma unroll
+  for (int kt = 0; kt < 8; ++kt) {
+    const u32x4v k0 = h128_block(s, mb0, kt), k1 = h128_block(s, mb1, kt);
+    if constexpr (BF) {
+      a0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8v, k0),
+                                                   __builtin_bit_cast(bf16x8v, b[kt]), a0, 0, 0, 0);
+      a1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8v, k1),
+                                                   __builtin_bit_cast(bf16x8v, b[kt]), a1, 0, 0, 0);
+    } else {
+      a0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8v, k0),
+                                                  __builtin_bit_cast(half8v, b[kt]), a0, 0, 0, 0);
+      a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8v, k1),
+                                                  __builtin_bit_cast(half8v, b[kt]), a1, 0, 0, 0);
+    }
+  }
+}
+
 // Pair-f16 store of one 128-block held by a 16-lane group (lane q holds
 // elements 8q..8q+7): dword p of the block's 64 dwords at `blk` is
 // (x[p], x[p + 64]). Lanes q < 8 write dwords 8q..8q+3, lanes q >= 8 dwords

@@ -171,6 +171,36 @@ __device__ __forceinline__ void dec_table_write(const DecTable<NIB>& t, int n_le
   }
 }
 
+// partial-sum slabs the last group loads at once
+constexpr int kSplitBatch = 16;
+
+// FWHT-128 of the wave's 32 items on the matrix cores, stored as pair f16
+// into each item's 256-byte LDS slot: pair p = 32 mp + 8 q + 4 h + r holds
+// positions p (m-block mp) and p + 64 (m-block mp + 2), so each lane writes
+// four 16-byte runs per m-block pair. Every lane takes part; only live lanes
+// store.
+template <bool BF>
+__device__ __forceinline__ void dec_xform_mfma(const u32x4v (&xq)[8], uint32_t slot, bool live,
+                                               int lane) {
+  const H128Signs sg = h128_signs<BF ? 0x3F803F80u : 0x3C003C00u>(lane);
+  const uint32_t h = (uint32_t)lane >> 5;
+#pragma unroll
+  for (int mp = 0; mp < 2; ++mp) {
+    float16v a0, a1;
+    h128_mfma_pair<BF>(sg, xq, mp, mp + 2, a0, a1);
+    if (live) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        u32x4v w;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          w[r] = pack_h2(a0[4 * q + r] * kInvSqrt128, a1[4 * q + r] * kInvSqrt128);
+        lds_st128(slot + 4u * (32u * mp + 8u * q + 4u * h), w);
+      }
+    }
+  }
+}
+
 // x: raw fp16 activations [M, K] (XRAW) or pair-f16 x_tf [M][nb][64] (else),
 // row stride ldx fp16 elements. The workgroup covers TN 16-row tiles with
 // NW = TN * KS waves: wave w works on tile w % TN over the K-slice w / TN
@@ -180,11 +210,11 @@ __device__ __forceinline__ void dec_table_write(const DecTable<NIB>& t, int n_le
 // writes fp32 partial sums part[blockIdx.y][M][N], and the last of the
 // gridDim.y workgroups of a row group to finish (counted in cnt[blockIdx.x])
 // adds the groups' partials in group order, writes y and resets its counter.
-// partial-sum slabs the last group loads at once
-constexpr int kSplitBatch = 16;
-
+// XMF (raw x, at most 32 items per wave): the activations' FWHT runs on the
+// matrix cores, 32 (row, block) items per wave (dec_xform_mfma), instead of
+// one item per 16-lane group on the VALU.
 template <bool NIB, int TN, int KS, bool XRAW, bool MASK, int XC, int D, bool CTV, bool SPLIT,
-          int MTD = 1>
+          int MTD = 1, bool XMF = false>
 __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
     const float* __restrict__ ct, int n_levels, uint32_t code_mask,
@@ -246,8 +276,29 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
     it_m = it / nbr;
     it_b = it - it_m * nbr;
   }
+  constexpr bool XM = XMF && XRAW;
+  // XM: wave w transforms items 32 w .. 32 w + 31, rows fastest (item i is
+  // row i % M of block i / M, so the 16 lanes of one LDS write phase cover
+  // up to 16 rows, whose padded slots start in different banks); lane l
+  // loads positions 16 kt + 8 (l / 32) .. + 7 of item 32 w + l % 32
+  u32x4v xq[XM ? 8 : 1];
+  int q_m = 0, q_b = 0;
+  bool q_live = false;
+  if constexpr (XM) {
+    const int i = 32 * wave + (lane & 31);
+    q_live = i < nitems;
+    const int ic = q_live ? i : nitems - 1;
+    q_m = ic % M;
+    q_b = ic / M;
+    if (32 * wave < nitems) {  // uniform
+      const char* src = reinterpret_cast<const char*>(x) +
+                        ((int64_t)q_m * ldx + (int64_t)(kb0 + q_b) * kBlock + 8 * (lane >> 5)) * 2;
+#pragma unroll
+      for (int kt = 0; kt < 8; ++kt) xq[kt] = *reinterpret_cast<const u32x4v*>(src + kt * 32);
+    }
+  }
   u32x4v xr[XC];
-  {
+  if constexpr (!XM) {
     const char* xb = reinterpret_cast<const char*>(x);
     int m = it_m, b = it_b;
 #pragma unroll
@@ -282,8 +333,14 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
 
   // ---- 2. activations into LDS as pair f16: 256 B per (row, block), pair p
   // = (x_tf[128 b + p], x_tf[128 b + 64 + p]) at byte 4 p. XRAW: FWHT of the
-  // item by its 16-lane group first.
-  {
+  // item by its 16-lane group first (XM: by the wave's MFMAs).
+  if constexpr (XM) {
+    if (32 * wave < nitems) {  // uniform
+      const uint32_t slot = xs_addr + (uint32_t)q_m * xrow_b + (uint32_t)q_b * 256u;
+      if (xbf) dec_xform_mfma<true>(xq, slot, q_live, lane);
+      else dec_xform_mfma<false>(xq, slot, q_live, lane);
+    }
+  } else {
     int m = it_m, b = it_b;
 #pragma unroll
     for (int i = 0; i < XC; ++i) {
@@ -571,17 +628,19 @@ static size_t dec_lds(bool nibble, int M, int nb, int n_levels, int nw) {
   return lds < red ? red : lds;
 }
 
-template <bool NIB, int TN, bool XRAW, bool MASK, int XC, bool CTV, bool SPLIT = false, int MTD = 1>
+template <bool NIB, int TN, bool XRAW, bool MASK, int XC, bool CTV, bool SPLIT = false, int MTD = 1,
+          bool XMF = false>
 static int launch_dec(const DecArgs& a, hipStream_t st, int groups = 1) {
   constexpr int KS = dec_ks<TN>(), NW = TN * KS;
   // blocks in flight per wave (nibble 1 KB, int8 2 KB each); deeper rings
   // measured slower (3 -> 8: 7.6 -> 8.8 us on Q4 12288 x 4096)
   constexpr int D = NIB ? 3 : 2;
-  auto kern = gemv_mfma_kernel<NIB, TN, KS, XRAW, MASK, XC, D, CTV, SPLIT, MTD>;
+  auto kern = gemv_mfma_kernel<NIB, TN, KS, XRAW, MASK, XC, D, CTV, SPLIT, MTD, XMF>;
   if (dec_mtd(a.M) != MTD) return PE_ERR_DIMS;
   const int nbg = (a.nb + groups - 1) / groups;  // most blocks of one group
   const size_t lds = dec_lds(NIB, a.M, nbg, a.n_levels, NW);
-  if (lds > 160 * 1024 || dec_xc(a.M, nbg, NW) > XC) return PE_ERR_DIMS;
+  // XMF: 32 items per wave (the same capacity as XC = 8: 8 per 16-lane group)
+  if (lds > 160 * 1024 || dec_xc(a.M, nbg, NW) > (XMF ? 8 : XC)) return PE_ERR_DIMS;
   static const bool attr_ok = [&] {
     return hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
@@ -608,9 +667,17 @@ static int launch_dec(const DecArgs& a, hipStream_t st, int groups = 1) {
   return launch_status();
 }
 
+// activation registers per lane from which the transform moves to the
+// matrix cores (32 items per wave): at one or two items per 16-lane group the
+// VALU butterfly is cheaper
+constexpr int kDecXformMfmaXc = 3;
+
 template <bool NIB, int TN, bool XRAW, bool MASK>
 static int launch_dec_xc(const DecArgs& a, hipStream_t st) {
   const int xc = dec_xc(a.M, a.nb, TN * dec_ks<TN>());
+  if (XRAW && xc >= kDecXformMfmaXc)
+    return a.ct_host ? launch_dec<NIB, TN, XRAW, MASK, 1, true, false, 1, XRAW>(a, st)
+                     : launch_dec<NIB, TN, XRAW, MASK, 1, false, false, 1, XRAW>(a, st);
   if (a.ct_host) {
     if (xc <= 1) return launch_dec<NIB, TN, XRAW, MASK, 1, true>(a, st);
     if (xc <= 2) return launch_dec<NIB, TN, XRAW, MASK, 2, true>(a, st);
@@ -694,6 +761,14 @@ static int launch_dec_split(const DecArgs& a, hipStream_t st) {
   if (!a.ws || !a.cnt || a.ws_bytes < (size_t)G * a.M * a.N * 4) return PE_ERR_WORKSPACE;
   const int xc = dec_xc(a.M, (a.nb + G - 1) / G, kDecW);
   const int mtd = dec_mtd(a.M);
+  if (XRAW && xc >= kDecXformMfmaXc) {
+    if (mtd > 2) return PE_ERR_DIMS;
+    if (mtd == 2)
+      return a.ct_host ? launch_dec<NIB, kSplitTN, XRAW, MASK, 1, true, true, 2, XRAW>(a, st, G)
+                       : launch_dec<NIB, kSplitTN, XRAW, MASK, 1, false, true, 2, XRAW>(a, st, G);
+    return a.ct_host ? launch_dec<NIB, kSplitTN, XRAW, MASK, 1, true, true, 1, XRAW>(a, st, G)
+                     : launch_dec<NIB, kSplitTN, XRAW, MASK, 1, false, true, 1, XRAW>(a, st, G);
+  }
   if (mtd > 1) {  // two m-tiles (kDecMaxRows = 32): activation registers 4 or 8
     if (mtd != 2) return PE_ERR_DIMS;
     if (a.ct_host)

@@ -240,8 +240,6 @@ __global__ __launch_bounds__(256) void kv_quantize_kernel(const void* __restrict
 // lane l holding positions 32 mb + 8 (e / 4) + 4 h + e % 4 of vector l % 32:
 // half of every 8-position code group, the other half in lane l ^ 32.
 // ---------------------------------------------------------------------------
-typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
-
 template <int DT>
 struct KvMfma {  // fp16
   static constexpr uint32_t kOne2 = 0x3C003C00u;
