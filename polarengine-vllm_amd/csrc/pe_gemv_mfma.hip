@@ -668,9 +668,10 @@ static int launch_dec(const DecArgs& a, hipStream_t st, int groups = 1) {
 }
 
 // activation registers per lane from which the transform moves to the
-// matrix cores (32 items per wave): at one or two items per 16-lane group the
-// VALU butterfly is cheaper
-constexpr int kDecXformMfmaXc = 3;
+// matrix cores (32 items per wave): at one item per 16-lane group (M = 1 at
+// K <= 6144) the VALU butterfly is cheaper; from two on the MFMAs are
+// (down projection 4096 x 12288 at M = 1: 7.89 -> 7.57 us)
+constexpr int kDecXformMfmaXc = 2;
 
 template <bool NIB, int TN, bool XRAW, bool MASK>
 static int launch_dec_xc(const DecArgs& a, hipStream_t st) {
