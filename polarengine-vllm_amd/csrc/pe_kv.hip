@@ -271,7 +271,8 @@ void kv_quantize_mfma_kernel(const void* __restrict__ x, int64_t ldx, int64_t n_
                              uint16_t* __restrict__ norms) {
   using K = KvMfma<DT>;
   constexpr int D = 128, RB = D * NBITS / 8, NL = 1 << NBITS;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar step bases
   const int n = lane & 31, h = lane >> 5;
   float mid[NL - 1];
 #pragma unroll
@@ -431,6 +432,7 @@ __device__ __forceinline__ uint32_t kv_group(const uint32_t (&d)[4 * NBITS], int
 }
 
 constexpr int kKvtRow = 66;  // dwords per LDS tile row: 256 bytes + 8 of padding
+constexpr int kKvBufFlags = 0x00020000;  // raw buffer, 32-bit data format (dword 3 of the resource)
 
 template <int NBITS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
@@ -440,7 +442,8 @@ void kv_dequantize_mfma_kernel(const uint8_t* __restrict__ packed,
                                int64_t ldo) {
   constexpr int RB = 128 * NBITS / 8, NL = 1 << NBITS;
   __shared__ uint32_t kvt[4 * kKvmVecs * kKvtRow];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar step bases
   const int n = lane & 31, h = lane >> 5;
   // lane j holds (hi, lo) of the value of code j mod 2^NBITS as two fp16
   uint32_t tv;
@@ -465,6 +468,9 @@ void kv_dequantize_mfma_kernel(const uint8_t* __restrict__ packed,
 #pragma unroll
     for (int jp = 0; jp < 4; ++jp) G[jp] = F[jp] ^ m4;
   }
+  // this lane's store offset within a step's rows: row lane / 16 of each
+  // group of four, 16-byte chunk lane % 16
+  const uint32_t o_voff = (uint32_t)(((lane >> 4) * ldo + 8 * (lane & 15)) * 2);
   const int64_t stride = (int64_t)gridDim.x * 4 * kKvmVecs;
   for (int64_t v0 = ((int64_t)blockIdx.x * 4 + wave) * kKvmVecs; v0 < n_vec; v0 += stride) {
     const int64_t vr = v0 + n < n_vec ? v0 + n : n_vec - 1;  // past the end: the last vector
@@ -538,11 +544,18 @@ void kv_dequantize_mfma_kernel(const uint8_t* __restrict__ packed,
             make_uint2(__builtin_bit_cast(uint32_t, o0), __builtin_bit_cast(uint32_t, o1));
       }
     }
+    // the step's rows through a buffer resource whose extent ends at the
+    // last vector: stores past it are dropped by the hardware, so each
+    // address is the lane's offset plus a scalar row offset (host: ldo <
+    // 2^24, so every offset fits 31 bits)
+    const int64_t rows = n_vec - v0 < kKvmVecs ? n_vec - v0 : kKvmVecs;
+    const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+        out + v0 * ldo, (short)0, (int)(rows * ldo * 2), kKvBufFlags);
 #pragma unroll
     for (int i = 0; i < kKvmVecs / 4; ++i) {
       const int r = 4 * i + (lane >> 4), c = lane & 15;
-      const uint4 q = *reinterpret_cast<const uint4*>(tile + r * kKvtRow + 4 * c);
-      if (v0 + r < n_vec) *reinterpret_cast<uint4*>(out + (v0 + r) * ldo + 8 * c) = q;
+      const u32x4v q = *reinterpret_cast<const u32x4v*>(tile + r * kKvtRow + 4 * c);
+      __builtin_amdgcn_raw_buffer_store_b128(q, ors, o_voff, (int)(4 * i * ldo * 2), 0);
     }
   }
 }
@@ -612,8 +625,9 @@ static int launch_kv_q(const void* x, int dt, int64_t ldx, int64_t n, const floa
 template <int D, int NBITS>
 static int launch_kv_d(const uint8_t* packed, const uint16_t* norms, int64_t n, const float* ct,
                        uint16_t* out, int64_t ldo, hipStream_t st) {
-  // D = 128 with 16-byte aligned packed rows: the transform on the matrix cores
-  if (D == 128 && aligned16(packed)) {
+  // D = 128 with 16-byte aligned packed rows: the transform on the matrix
+  // cores (its buffer stores take 31-bit offsets: ldo < 2^24)
+  if (D == 128 && aligned16(packed) && ldo < ((int64_t)1 << 24)) {
     const int64_t steps = (n + 4 * kKvmVecs - 1) / (4 * kKvmVecs);
     const int64_t cap = (int64_t)num_cus() * kKvqWgsPerCu;
     const unsigned g = (unsigned)(steps < cap ? steps : cap);
