@@ -195,15 +195,20 @@ __global__ __launch_bounds__(256) void kv_quantize_kernel(const void* __restrict
     uint32_t c[8];
     if (by_cell) {  // uniform
       const float s = inv * cells.inv_w;
+      // the cell from t clamped to [-32, 31] (IEEE max: a NaN goes to cell
+      // 0, where it compares false: code 0, as the count gives); the compare
+      // on t itself. All eight table reads go out before the first compare.
+      float t[8], md[8];
+      uint32_t lo[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        // the cell from t clamped to [-32, 31] (IEEE max: a NaN goes to
-        // cell 0, where it compares false: code 0, as the count gives); the
-        // compare on t itself
-        const float t = v[i] * s;
-        const int cell = (int)__builtin_floorf(fminf(fmaxf(t, -32.f), 31.f)) + 32;
-        c[i] = cells.lo[cell] + (t > cells.mid[cell] ? 1u : 0u);
+        t[i] = v[i] * s;
+        const int cell = (int)__builtin_floorf(fminf(fmaxf(t[i], -32.f), 31.f)) + 32;
+        lo[i] = cells.lo[cell];
+        md[i] = cells.mid[cell];
       }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) c[i] = lo[i] + (t[i] > md[i] ? 1u : 0u);
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -343,14 +348,22 @@ void kv_quantize_mfma_kernel(const void* __restrict__ x, int64_t ldx, int64_t n_
         }
       uint32_t k[2][16];
       if (by_cell) {  // uniform
+        // every table read of an m-block issued before the first compare
+        // (read, wait, compare per element left each read's latency exposed)
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < 2; ++u) {
+          float t[16], md[16];
+          uint32_t lo[16];
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
-            const float t = acc[u][e] * s;
-            const int cell = (int)__builtin_floorf(fminf(fmaxf(t, -32.f), 31.f)) + 32;
-            k[u][e] = cells.lo[cell] + (t > cells.mid[cell] ? 1u : 0u);
+            t[e] = acc[u][e] * s;
+            const int cell = (int)__builtin_floorf(fminf(fmaxf(t[e], -32.f), 31.f)) + 32;
+            lo[e] = cells.lo[cell];
+            md[e] = cells.mid[cell];
           }
+#pragma unroll
+          for (int e = 0; e < 16; ++e) k[u][e] = lo[e] + (t[e] > md[e] ? 1u : 0u);
+        }
       } else {
 #pragma unroll
         for (int u = 0; u < 2; ++u)
