@@ -325,9 +325,32 @@ def summarize_pmc(fetch_csv, write_csv):
 
 def prefill_extra(dev):
     """Prefill linear at M=2048 (FWHT-128 of x into pair f16, then the MFMA
-    GEMM): Q4 12288x4096 and the Q3 4096x12288 down projection; and the Q4
-    down projection at M=128 / 512 (K split over workgroups)."""
+    GEMM): Q4 12288x4096 and the Q3 4096x12288 down projection; the same two
+    at the other C3 sizes, M=256 (from HIP graphs over rotating weight
+    copies) and M=8192; and the Q4 down projection at M=128 / 512 (K split
+    over workgroups)."""
     out = {}
+    for mm, reps in ((8192, 8),):
+        for name, (nn, kk, bb, seed) in ((f"prefill_m{mm}", (12288, 4096, 4, 320)),
+                                         (f"prefill_down_q3_m{mm}", (4096, 12288, 3, 321))):
+            pf = Linear(nn, kk, bb, mm, dev, seed=seed)
+            t_pf = time_eager(pf, 2, reps, dev)
+            fl = 2.0 * mm * nn * kk
+            out[name] = {"us_per_call": round(t_pf * 1e6, 1),
+                         "TFLOP/s": round(fl / t_pf / 1e12, 1),
+                         "mfma_frac": round(fl / t_pf / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                         "includes": "FWHT-128 of x (pair f16) + MFMA GEMM"}
+            del pf
+    for name, (nn, kk, bb, seed) in (("prefill_m256", (12288, 4096, 4, 330)),
+                                     ("prefill_down_q3_m256", (4096, 12288, 3, 331))):
+        lay = [Linear(nn, kk, bb, 256, dev, seed=seed + 2 * i) for i in range(4)]
+        t, _ = time_graph(lay, 4, 32, 256, dev)
+        fl = 2.0 * 256 * nn * kk
+        out[name] = {"us_per_call": round(t * 1e6, 1), "TFLOP/s": round(fl / t / 1e12, 1),
+                     "mfma_frac": round(fl / t / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                     "GB/s": round(algo_bytes(256, nn, kk, bb) / t / 1e9, 1),
+                     "includes": "FWHT-128 of x (pair f16) + MFMA GEMM (K split where the tiles are few)"}
+        del lay
     flops = 2.0 * 2048 * 12288 * 4096
     for name, (nn, kk, bb, seed) in (("prefill_m2048", (12288, 4096, 4, 300)),
                                      ("prefill_down_q3_m2048", (4096, 12288, 3, 301))):
