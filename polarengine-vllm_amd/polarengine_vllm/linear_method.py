@@ -4,9 +4,9 @@ Same buffers and interface as the reference (``create_weights``, ``apply``,
 ``process_weights_after_loading``), with the forward running on the gfx950
 HIP library:
 
-* M = 1 (decode): one launch of ``pe_linear_forward`` -- the FWHT-128 of x
+* M <= 32 (decode): one launch of ``pe_linear_forward`` -- the FWHT-128 of x
   is fused into the GEMV prologue;
-* M > 1: ``pe_fwht128`` once into the pair-f16 layout (cached for Q/K/V and
+* M > 32: ``pe_fwht128`` once into the pair-f16 layout (cached for Q/K/V and
   gate/up reading the same hidden state), then ``pe_linear_forward_xtf``
   (MFMA GEMM) per projection;
 * bias and the fp16 output cast are fused into the kernel epilogue.
@@ -46,9 +46,13 @@ except Exception:  # vLLM absent: plain attribute setter
 
 logger = logging.getLogger(__name__)
 
-# M above which the transformed activation is materialised and shared
-# (below it the GEMV fuses the transform and sharing saves nothing).
-_SHARE_FWHT_MIN_M = 2
+# M above which the transformed activation is materialised (one FWHT launch)
+# and shared through the FWHT cache. Up to it the decode GEMV transforms the
+# activations in its own prologue (on the matrix cores from M = 2), which
+# costs less than the extra launch even when q/k/v are separate modules that
+# each transform the same input; vLLM's merged qkv_proj / gate_up_proj have
+# one consumer per input, so there is nothing to share.
+_FUSED_FWHT_MAX_M = 32
 
 
 class PolarQuantLinearMethod:
@@ -152,7 +156,7 @@ class PolarQuantLinearMethod:
             _lib.PE_LAYOUT_TILE16 if getattr(layer, "tiled", False) else 0)
         out_code = _lib.act_dtype(y)
 
-        if m >= _SHARE_FWHT_MIN_M or x.dtype != out_dtype:
+        if m > _FUSED_FWHT_MAX_M or x.dtype != out_dtype:
             x_tf = self._fwht_cache.get(x, layer.in_f)
             if x_tf is None:
                 xp = x2 if kp == layer.in_f else F.pad(x2, (0, kp - layer.in_f))

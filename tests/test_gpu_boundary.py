@@ -289,18 +289,20 @@ def _raw_overwrite(dst, src):
 
 
 def test_fwht_cache_scoped_by_hooks_against_raw_writes():
+    """M = 64: above the decode range, where the transform is materialised
+    and shared through the cache."""
     from polarengine_vllm.kernels.fwht import GLOBAL_FWHT_CACHE
     from polarengine_vllm.linear_method import install_fwht_cache_hooks
     say("fwht cache hooks vs raw writes")
     parent = _qkv_parent()
     assert install_fwht_cache_hooks(parent) == 1
     assert install_fwht_cache_hooks(parent) == 0  # idempotent
-    x = to_dev(O.seeded_normal((8, 512), 1.0, 690))
+    x = to_dev(O.seeded_normal((64, 512), 1.0, 690))
     GLOBAL_FWHT_CACHE.clear()
     parent(x)
     assert GLOBAL_FWHT_CACHE.get(x, 512) is not None  # shared by q/k/v
     ver = x._version
-    x2 = O.seeded_normal((8, 512), 1.0, 691)
+    x2 = O.seeded_normal((64, 512), 1.0, 691)
     _raw_overwrite(x, to_dev(x2))
     assert x._version == ver  # torch did not see the write
     outs = parent(x)  # the pre-hook cleared the entry: transformed afresh
@@ -314,15 +316,16 @@ def test_fwht_cache_scoped_by_hooks_against_raw_writes():
 
 def test_fwht_matmul_out_write_invalidates_cache():
     """The package's own raw-pointer writes into a caller tensor record a
-    version bump, so a cached transform of that tensor misses."""
+    version bump, so a cached transform of that tensor misses (M = 64, the
+    cached range)."""
     from polarengine_vllm.kernels.fwht import GLOBAL_FWHT_CACHE, fwht_matmul
     say("fwht_matmul out= bumps the version")
     parent = _qkv_parent(seed=700)  # no hooks
-    x = to_dev(O.seeded_normal((8, 512), 1.0, 701))
+    x = to_dev(O.seeded_normal((64, 512), 1.0, 701))
     GLOBAL_FWHT_CACHE.clear()
     parent.q(x)
     assert GLOBAL_FWHT_CACHE.get(x, 512) is not None
-    fwht_matmul(to_dev(O.seeded_normal((8, 512), 1.0, 702)), out=x)
+    fwht_matmul(to_dev(O.seeded_normal((64, 512), 1.0, 702)), out=x)
     assert GLOBAL_FWHT_CACHE.get(x, 512) is None
     y = parent.k(x)
     c, nrm, ct = parent.k.o

@@ -579,13 +579,14 @@ def test_linear_method_apply(m, bits, n, k):
 
 
 def test_fwht_shared_across_qkv():
-    """q/k/v modules on one hidden state: one transform, three projections."""
+    """q/k/v modules on one hidden state above the decode range (M = 64):
+    one transform, three projections."""
     from polarengine_vllm.kernels.fwht import GLOBAL_FWHT_CACHE
     from polarengine_vllm.linear_method import PolarQuantLinearMethod
     _say("qkv sharing")
     rng = np.random.default_rng(9)
     k = 1024
-    x = to_dev(O.seeded_normal((8, k), 1.0, 43))
+    x = to_dev(O.seeded_normal((64, k), 1.0, 43))
     GLOBAL_FWHT_CACHE.clear()
     outs = []
     for n in (1024, 256, 256):

@@ -114,7 +114,7 @@ def c4_layer():
     return layer
 
 
-@pytest.mark.parametrize("m", [1, 512])
+@pytest.mark.parametrize("m", [1, 16, 512])
 def test_decoder_layer_c4(c4_layer, m, monkeypatch):
     import polarengine_vllm.linear_method as lm
     from polarengine_vllm.kernels.fwht import GLOBAL_FWHT_CACHE
@@ -136,7 +136,7 @@ def test_decoder_layer_c4(c4_layer, m, monkeypatch):
     out = c4_layer(h)
     torch.cuda.synchronize()
     assert out.shape == (m, HID) and out.dtype == torch.float16 and torch.isfinite(out).all()
-    if m == 1:
+    if m <= 32:
         assert calls == []  # the transform is fused into every decode GEMV
     else:
         # one transform for Q/K/V, one for O, one for gate/up, one for down
