@@ -380,10 +380,12 @@ class DecoderLayerLinears:
     weights. `merged`: vLLM's form, q/k/v one qkv_proj (6144 rows) and
     gate/up one gate_up_proj (24576 rows), as PolarQuantLinearMethod sees
     them (create_weights sums output_partition_sizes); otherwise seven
-    separate modules (the transformers form). M = 1: one pe_linear_forward per
-    linear (transform fused into each decode GEMV). M > 1: pe_fwht128 once for
-    q/k/v and once for gate/up, pe_linear_forward_xtf for those,
-    pe_linear_forward for o and down (their inputs are new activations)."""
+    separate modules (the transformers form). As PolarQuantLinearMethod.apply
+    runs them: M <= 32, one pe_linear_forward per linear (transform fused into
+    each decode GEMV); M > 32, pe_fwht128 once for q/k/v and once for gate/up,
+    pe_linear_forward_xtf for those, pe_linear_forward for o and down (their
+    inputs are new activations)."""
+    FUSED_MAX_M = 32
 
     SEPARATE = [("q", 4096, 4096, 5, "qkv"), ("k", 1024, 4096, 5, "qkv"),
                 ("v", 1024, 4096, 5, "qkv"), ("o", 4096, 4096, 6, "o"),
@@ -418,12 +420,13 @@ class DecoderLayerLinears:
         L = _lib.lib()
         st = _lib.stream_ptr(self.dev)
         m = self.m
-        if m > 1:
+        shared = m > self.FUSED_MAX_M
+        if shared:
             for g in ("qkv", "gu"):
                 _lib.check(L.pe_fwht128(self.x[g].data_ptr(), 0, m, 4096, 4096, self.xtf[g].data_ptr(),
                                         _lib.PE_XTF_PAIR_F16, st), "pe_fwht128")
         for (name, n, k, bits, grp, codes, norms, ct, ct_host, fmt, y) in self.lin:
-            if m > 1 and grp in ("qkv", "gu"):
+            if shared and grp in ("qkv", "gu"):
                 rc = L.pe_linear_forward_xtf(self.xtf[grp].data_ptr(), m, k, codes.data_ptr(), bits,
                                              fmt, norms.data_ptr(), ct.data_ptr(), ct_host.ctypes.data,
                                              1 << bits, None, 0, y.data_ptr(), n, self.ws.data_ptr(),
@@ -439,28 +442,30 @@ class DecoderLayerLinears:
 
 def decoder_layer_extra(dev):
     """C4: the decoder layer's quantized linears at M = 1 (GB/s of its
-    algorithmic bytes: 120.6 MB for the seven separate linears) and M = 512
-    (TFLOP/s of 197.6 GFLOP); four layer copies in turn (482 MB > the 256 MB
-    Infinity Cache). decoder_layer_m*: vLLM's merged qkv / gate_up form;
-    decoder_layer_separate_m*: seven separate modules."""
+    algorithmic bytes: 120.6 MB for the seven separate linears), at a decode
+    batch of M = 16, and at M = 512 (TFLOP/s of 197.6 GFLOP); four layer
+    copies in turn (482 MB > the 256 MB Infinity Cache). decoder_layer_m*:
+    vLLM's merged qkv / gate_up form; decoder_layer_separate_m*: seven
+    separate modules."""
     out = {}
     for merged, tag in ((True, "decoder_layer"), (False, "decoder_layer_separate")):
         specs = DecoderLayerLinears.MERGED if merged else DecoderLayerLinears.SEPARATE
-        for m in (1, 512):
+        for m in (1, 16, 512):
             layers = [DecoderLayerLinears(m, dev, seed=500 + 10 * i, merged=merged)
                       for i in range(4)]
-            t, _ = time_graph(layers, 1, 8, 64 if m == 1 else 16, dev)
+            t, _ = time_graph(layers, 1, 8, 64 if m <= 32 else 16, dev)
             B = sum(algo_bytes(m, n, k, b) for _, n, k, b, _ in specs)
             fl = sum(2.0 * m * n * k for _, n, k, _, _ in specs)
             ent = {"us_per_layer": round(t * 1e6, 2), "algorithmic_bytes": B,
                    "GB/s": round(B / t / 1e9, 1),
                    "hbm_frac": round(B / t / 1e9 / HBM_PEAK_GBS, 4),
                    "TFLOP/s": round(fl / t / 1e12, 2),
-                   "launches": len(specs) + (2 if m > 1 else 0),
+                   "launches": len(specs) + (2 if m > DecoderLayerLinears.FUSED_MAX_M else 0),
                    "includes": ("qkv Q5, o Q6, gate_up Q3, down Q4 (vLLM merged modules)" if merged
                                 else "q/k/v Q5, o Q6, gate/up Q3, down Q4 (separate modules)")
-                   + "; a shared transform per input at M > 1; linears only"}
-            if m > 1:
+                   + "; the transform fused into each decode GEMV up to M = 32, "
+                   "shared per input above; linears only"}
+            if m > DecoderLayerLinears.FUSED_MAX_M:
                 ent["mfma_frac"] = round(fl / t / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
             out[f"{tag}_m{m}"] = ent
             del layers
