@@ -731,7 +731,11 @@ static int dec_split_groups(bool nibble, int M, int N, int nb, int n_levels) {
   // workgroup would run as a second round of its own
   if (wgn > kWsCounters) return 0;  // one completion counter per row group
   int G = num_cus() / wgn;
-  if (G > nb) G = nb;
+  // at least four 128-blocks per group: with fewer, every workgroup's fixed
+  // costs (prologue, partial stores) outweigh its share of the stream, and
+  // the last group reads more slabs (1024 x 4096 at M = 16: G = 32 -> 8,
+  // 97 -> 85 us for the seven separate C4 linears)
+  if (G > nb / 4) G = nb / 4;
   if (M > 16) {
     if (G < 2) G = nb < 2 ? nb : 2;
     while (G < nb && (dec_xc(M, (nb + G - 1) / G, kDecW) > 8 ||
