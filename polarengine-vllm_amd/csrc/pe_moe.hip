@@ -350,7 +350,10 @@ __global__ __launch_bounds__(kFrontThreads) void moe_front_kernel(FrontArgs a) {
 }
 
 // out[t, c..c+3] = sum_k w[t, k] * y2[pos(t, k), c..c+3], k in order; 4
-// columns per lane, the loads of four slots issued before their sums
+// columns per lane, the loads of eight slots issued before their sums (top-8
+// in one memory round trip)
+constexpr int kCombineBatch = 8;
+
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ y2,
                                                           const float* __restrict__ topk_w,
                                                           const int32_t* __restrict__ pair_pos,
@@ -362,12 +365,12 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
   const int64_t t = i / per_row;
   const int c = (int)(i - t * per_row) * 4;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int k0 = 0; k0 < top_k; k0 += 4) {
-    int pos[4];
-    float w[4];
-    float4 yv[4];
+  for (int k0 = 0; k0 < top_k; k0 += kCombineBatch) {
+    int pos[kCombineBatch];
+    float w[kCombineBatch];
+    float4 yv[kCombineBatch];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kCombineBatch; ++u) {
       const int k = k0 + u;
       pos[u] = k < top_k ? pair_pos[t * top_k + k] : -1;
       w[u] = pos[u] >= 0 ? topk_w[t * top_k + k] : 0.f;
@@ -375,7 +378,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
                           : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kCombineBatch; ++u) {
       if (pos[u] < 0) continue;
       acc[0] += w[u] * yv[u].x;
       acc[1] += w[u] * yv[u].y;
