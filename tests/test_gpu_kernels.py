@@ -609,14 +609,17 @@ def test_fwht_shared_across_qkv():
 
 def test_graph_replay_matches_eager():
     """The bench replays captured HIP graphs: every replay, with eager work in
-    between, must equal the eager result (decode M=1 and small-M paths)."""
+    between, must equal the eager result (decode at M=1, with the transform on
+    the matrix cores at M=4, the K split with its completion counters at
+    M=16 and M=24 (two m-tiles), and the prefill GEMM)."""
     from polarengine_vllm import _lib
     _say("graph replay")
     rng = np.random.default_rng(12)
     L = _lib.lib()
     st = lambda: _lib.stream_ptr(torch.device(DEV))
     cases = []
-    for m, n, k, bits in [(1, 4096, 4096, 4), (4, 2048, 4096, 3), (80, 1024, 1024, 5)]:
+    for m, n, k, bits in [(1, 4096, 4096, 4), (4, 2048, 4096, 3), (16, 12288, 4096, 4),
+                          (24, 4096, 12288, 3), (80, 1024, 1024, 5)]:
         codes, norms, ct = rand_layer(rng, n, k, bits)
         dcodes, nib = dev_codes(codes, bits)
         x = to_dev(O.seeded_normal((m, k), 1.0, 50 + m))
