@@ -117,3 +117,33 @@ def test_counter_block_left_zero():
         layer.w2_norms.data_ptr(), layer.w2_ct_scaled.data_ptr(), 16,
         outs[0].data_ptr(), ws.data_ptr(), wsb - 256,
         _lib.stream_ptr(torch.device(DEV))) == _lib.PE_ERR_WORKSPACE
+
+
+def test_graph_replay_matches_eager():
+    """The MoE call at the C5 shapes (64 experts, I = 1408, top-8), captured
+    in a HIP graph and replayed with eager work in between: every replay
+    equals the eager call bit for bit (the routing counter block is reset by
+    each call, the bench replays this graph)."""
+    say("moe graph replay")
+    rng = np.random.default_rng(940)
+    meth, layer, _ = _layer(rng, 64, 2048, 1408, 3, 4)
+    x = to_dev(O.seeded_normal((128, 2048), 1.0, 941))
+    logits = to_dev(O.seeded_normal((128, 64), 1.0, 942, np.float32))
+    want = meth.apply(layer, x, logits, 8, True)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        meth.apply(layer, x, logits, 8, True)  # workspace at full size before capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        y = meth.apply(layer, x, logits, 8, True)
+    for rep in range(3):
+        y.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, want), f"replay {rep} differs"
+        junk = torch.randn(1 << 20, device=DEV).sum()  # eager work between replays
+        torch.cuda.synchronize()
+        del junk
