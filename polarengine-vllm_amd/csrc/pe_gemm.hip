@@ -776,7 +776,7 @@ int mm_xtf(bool nibble, bool tiled, const void* codes, const uint16_t* norms, co
     SmallArgs s{reinterpret_cast<const uint8_t*>(codes), norms, ct, n_levels,
                 reinterpret_cast<const uint32_t*>(x_pair), nullptr, nullptr, 0, 0, y, ldy, bias,
                 (int)M, N, nb, lay, ybf ? 1 : 0};
-    return gemm_small(nibble, out_mode == OM_F32 ? SE_F32 : SE_F16, s, 1, st);
+    return gemm_small(nibble, out_mode == OM_F32 ? SE_F32 : SE_F16, s, st);
   }
   GemmArgs a{reinterpret_cast<const uint8_t*>(codes), norms, ct, n_levels, x_pair, y, bias,
              (int)M, N, nb, ldy, lay, ybf ? 1 : 0};

@@ -1,5 +1,6 @@
-// Small-M quantized matmul for gfx950 (decode batches M = 2..64, and the
-// grouped-expert MoE products): Y[m, n] = sum_k X_tf[m, k] * W~[n, k].
+// Small-M quantized matmul for gfx950 (batches M = 2..64 that the decode
+// kernel does not take), and the grouped-expert MoE products:
+// Y[m, n] = sum_k X_tf[m, k] * W~[n, k].
 //
 // Replaces the reference's M > 1 path for small batches (polar_gemm /
 // polar_gemm_packed, kernels/polar_gemm.py:81-418, autotuned Triton tiles) and
@@ -19,11 +20,10 @@
 //    x_tf (16 contiguous bytes per lane per slab);
 //  * the per-block fp16 norm multiplies the 4 fp32 MFMA results of each block
 //    (fp32, as the reference applies it), not the fp16 operands;
-//  * grouped mode (MoE): blockIdx.y selects an expert, whose rows are
-//    [off[e], off[e+1]) of a row list; weights advance by per-expert strides;
-//  * epilogues: fp32 out, fp16 out (+ bias), or SwiGLU: the workgroup also
-//    computes the "up" tile at row n + I for every "gate" tile at row n and
-//    writes fp16 silu(gate) * up.
+//  * epilogues: fp32 out, or 16-bit out (+ bias).
+// The MoE expert products (moe_gemv_kernel, further down) have their own
+// kernel: blockIdx.y selects an expert, whose rows are [off[e], off[e+1]) of
+// a row list, and the weights advance by per-expert strides.
 
 #include "pe_internal.h"
 
@@ -121,12 +121,13 @@ __device__ __forceinline__ void compute_sblk(float4v (&acc)[MTM][NT], const Smal
   }
 }
 
-// TN: n-tiles of 16 weight rows per workgroup (SwiGLU doubles them: gate+up);
-// MTM: m-tiles of 16 rows per pass over the weights.
+// TN: n-tiles of 16 weight rows per workgroup; MTM: m-tiles of 16 rows per
+// pass over the weights; EP: SE_F32 or SE_F16.
 template <bool NIB, int TN, int EP, int MTM>
 __global__ __launch_bounds__(kSmallThreads) void gemm_small_kernel(
     SmallArgs a, uint32_t code_mask, int tbl_entries) {
-  constexpr int NT = EP == SE_SWIGLU ? 2 * TN : TN;  // tiles actually computed
+  static_assert(EP == SE_F32 || EP == SE_F16, "small-M epilogues: fp32 or 16-bit out");
+  constexpr int NT = TN;
   extern __shared__ uint4 smem4[];
   char* smem = reinterpret_cast<char*>(smem4);
   char* tbl = smem;
@@ -138,30 +139,16 @@ __global__ __launch_bounds__(kSmallThreads) void gemm_small_kernel(
   const int l16 = lane & 15, g = lane >> 4;
   const uint32_t lane4 = (uint32_t)lane << 2;
 
-  // ---- group / rows
-  int row0 = 0, M = a.M;
-  const uint8_t* codes = a.codes;
-  const uint16_t* norms = a.norms;
-  if (a.group_off) {
-    row0 = a.group_off[blockIdx.y];
-    M = a.group_off[blockIdx.y + 1] - row0;
-    codes += (int64_t)blockIdx.y * a.codes_stride;
-    norms += (int64_t)blockIdx.y * a.norms_stride;
-  }
-  if (M <= 0) return;  // whole workgroup exits together (uniform)
-
+  const int M = a.M;
   // ---- this lane's weight rows (clamped; clamped rows are never stored)
-  const int wrows = EP == SE_SWIGLU ? 2 * a.N : a.N;
   const uint8_t* brow[NT];
   const uint16_t* nrow[NT];
 #pragma unroll
   for (int j = 0; j < NT; ++j) {
-    int n = blockIdx.x * TN * 16 + (j % TN) * 16 + l16;
+    int n = blockIdx.x * TN * 16 + j * 16 + l16;
     if (n >= a.N) n = a.N - 1;
-    if (EP == SE_SWIGLU && j >= TN) n += a.N;  // the matching "up" row
-    if (n >= wrows) n = wrows - 1;
-    brow[j] = codes + a.lay.codes_off(n) + 16 * g;
-    nrow[j] = norms + a.lay.norms_off(n);
+    brow[j] = a.codes + a.lay.codes_off(n) + 16 * g;
+    nrow[j] = a.norms + a.lay.norms_off(n);
   }
   const int64_t xrow = (int64_t)a.nb * 64;
   // K range of this wave
@@ -185,9 +172,7 @@ __global__ __launch_bounds__(kSmallThreads) void gemm_small_kernel(
     for (int i = 0; i < MTM; ++i) {
       const int m = mbase + i * 16 + l16;
       alive[i] = i < MT && m < M;
-      int r = row0 + (alive[i] ? m : 0);
-      if (a.a_rows) r = a.a_rows[r];
-      arow[i] = a.xp + (int64_t)r * xrow + 16 * g;
+      arow[i] = a.xp + (int64_t)(alive[i] ? m : 0) * xrow + 16 * g;
     }
 
     float4v acc[MTM][NT];
@@ -233,30 +218,22 @@ __global__ __launch_bounds__(kSmallThreads) void gemm_small_kernel(
       const int m = mbase + i * 16 + 4 * (ln >> 4) + e;
       const int n = blockIdx.x * TN * 16 + j * 16 + (ln & 15);
       if (m >= M || n >= a.N) continue;
-      float s = 0.f, u = 0.f;
+      float s = 0.f;
 #pragma unroll
-      for (int w = 0; w < kSmallWaves; ++w) {
-        s += red[(((int64_t)w * MTM + i) * NT + j) * 256 + le];
-        if constexpr (EP == SE_SWIGLU)
-          u += red[(((int64_t)w * MTM + i) * NT + j + TN) * 256 + le];
-      }
-      const int64_t row = row0 + m;
-      if constexpr (EP == SE_F32) {
+      for (int w = 0; w < kSmallWaves; ++w) s += red[(((int64_t)w * MTM + i) * NT + j) * 256 + le];
+      const int64_t row = m;
+      if constexpr (EP == SE_F32)
         reinterpret_cast<float*>(a.y)[row * a.ldy + n] = s;
-      } else if constexpr (EP == SE_F16) {
+      else
         reinterpret_cast<uint16_t*>(a.y)[row * a.ldy + n] = out16(s, a.bias, n, a.ybf != 0);
-      } else {
-        const float act = s / (1.f + __expf(-s)) * u;
-        reinterpret_cast<_Float16*>(a.y)[row * a.ldy + n] = (_Float16)act;
-      }
     }
     __syncthreads();  // reduction reads done before the next pass's table fill
   }
 }
 
 template <bool NIB, int TN, int EP, int MTM>
-static int launch_small_t(const SmallArgs& a, int groups, hipStream_t st) {
-  constexpr int NT = EP == SE_SWIGLU ? 2 * TN : TN;
+static int launch_small_t(const SmallArgs& a, hipStream_t st) {
+  constexpr int NT = TN;
   auto kern = gemm_small_kernel<NIB, TN, EP, MTM>;
   const int entries = table_entries(NIB, a.n_levels);
   const size_t red_bytes = (size_t)kSmallWaves * MTM * NT * 64 * 16;
@@ -269,23 +246,18 @@ static int launch_small_t(const SmallArgs& a, int groups, hipStream_t st) {
   (void)attr_ok;
   const int tiles = (a.N + TN * 16 - 1) / (TN * 16);
   const uint8_t mb = NIB ? (uint8_t)((a.n_levels - 1) * 0x11) : (uint8_t)(a.n_levels - 1);
-  kern<<<dim3(tiles, groups), dim3(kSmallThreads), lds, st>>>(a, 0x01010101u * mb, entries);
+  kern<<<dim3(tiles), dim3(kSmallThreads), lds, st>>>(a, 0x01010101u * mb, entries);
   return launch_status();
 }
 
 template <bool NIB, int EP>
-static int launch_small_ep(const SmallArgs& a, int groups, hipStream_t st) {
-  // one m-tile per pass when every group fits in 16 rows (decode batches);
-  // otherwise two (grouped launches do not know their sizes on the host).
-  const bool one = !a.group_off && a.M <= 16;
+static int launch_small_ep(const SmallArgs& a, hipStream_t st) {
+  // one m-tile per pass when M fits in 16 rows, otherwise two
+  const bool one = a.M <= 16;
   // two n-tiles per workgroup when that still leaves >= 1 workgroup per CU
-  // (the SwiGLU epilogue already computes gate and up tiles: keep TN = 1)
-  const int cus = num_cus();
-  if constexpr (EP != SE_SWIGLU) {
-    if ((int64_t)((a.N + 31) / 32) * groups >= cus)
-      return one ? launch_small_t<NIB, 2, EP, 1>(a, groups, st) : launch_small_t<NIB, 2, EP, 2>(a, groups, st);
-  }
-  return one ? launch_small_t<NIB, 1, EP, 1>(a, groups, st) : launch_small_t<NIB, 1, EP, 2>(a, groups, st);
+  if ((a.N + 31) / 32 >= num_cus())
+    return one ? launch_small_t<NIB, 2, EP, 1>(a, st) : launch_small_t<NIB, 2, EP, 2>(a, st);
+  return one ? launch_small_t<NIB, 1, EP, 1>(a, st) : launch_small_t<NIB, 1, EP, 2>(a, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -638,11 +610,11 @@ int moe_grouped(bool nibble, int epilogue, const SmallArgs& a, int groups, hipSt
   }
 }
 
-int gemm_small(bool nibble, int epilogue, const SmallArgs& a, int groups, hipStream_t st) {
+int gemm_small(bool nibble, int epilogue, const SmallArgs& a, hipStream_t st) {
+  if (a.M <= 0 || a.N <= 0 || a.nb <= 0) return PE_ERR_DIMS;
   switch (epilogue) {
-    case SE_F32: return nibble ? launch_small_ep<true, SE_F32>(a, groups, st) : launch_small_ep<false, SE_F32>(a, groups, st);
-    case SE_F16: return nibble ? launch_small_ep<true, SE_F16>(a, groups, st) : launch_small_ep<false, SE_F16>(a, groups, st);
-    case SE_SWIGLU: return nibble ? launch_small_ep<true, SE_SWIGLU>(a, groups, st) : launch_small_ep<false, SE_SWIGLU>(a, groups, st);
+    case SE_F32: return nibble ? launch_small_ep<true, SE_F32>(a, st) : launch_small_ep<false, SE_F32>(a, st);
+    case SE_F16: return nibble ? launch_small_ep<true, SE_F16>(a, st) : launch_small_ep<false, SE_F16>(a, st);
     default: return PE_ERR_DTYPE;
   }
 }

@@ -79,14 +79,14 @@ struct SmallArgs {
   const float* ct;
   int n_levels;
   const uint32_t* xp;        // pair-f16 activations, rows of nb*64 uint32
-  const int32_t* a_rows;     // nullable: A row m reads xp row a_rows[m]
-  const int32_t* group_off;  // nullable: grouped mode, gridDim.y groups
-  int64_t codes_stride;      // bytes between experts' codes (grouped)
-  int64_t norms_stride;      // uint16 between experts' norms (grouped)
+  const int32_t* a_rows;     // nullable (MoE): A row m reads xp row a_rows[m]
+  const int32_t* group_off;  // MoE: expert e owns rows [off[e], off[e+1]), gridDim.y experts
+  int64_t codes_stride;      // bytes between experts' codes (MoE)
+  int64_t norms_stride;      // uint16 between experts' norms (MoE)
   void* y;
   int64_t ldy;
   const uint16_t* bias;
-  int M;                     // rows (non-grouped)
+  int M;                     // rows (small-M matmul)
   int N;                     // output columns (SwiGLU: I; the weights hold 2I rows)
   int nb;
   WLayout lay;               // per-expert layout (row-major for the MoE path)
@@ -95,7 +95,9 @@ struct SmallArgs {
 
 // pe_gemm_small.hip: M <= kSmallMaxRows per pass is cheapest (larger M loops)
 constexpr int kSmallMaxRows = 64;
-int gemm_small(bool nibble, int epilogue, const SmallArgs& a, int groups, hipStream_t st);
+// small-M matmul: M rows of xp, epilogue SE_F32 or SE_F16 (+ bias); the
+// MoE fields of SmallArgs are ignored
+int gemm_small(bool nibble, int epilogue, const SmallArgs& a, hipStream_t st);
 // grouped expert products (group_off required; epilogue SE_F32, SE_SWIGLU or
 // SE_SWIGLU_XTF)
 int moe_grouped(bool nibble, int epilogue, const SmallArgs& a, int groups, hipStream_t st);

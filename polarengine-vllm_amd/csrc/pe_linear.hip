@@ -6,11 +6,13 @@
 //   M <= 16 (when x, or one K group of it, fits in LDS beside the codebook
 //   table), or 17 <= M <= 32 when one K group fits
 //                     -> gemv_mfma: decode GEMV on 16x16x32 MFMA, FWHT fused
-//                        into its prologue (one launch per linear; with the K
-//                        split over workgroups, plus a partial-sum reduction;
-//                        M > 16 with two m-tiles per weight lookup);
-//   M == 1 otherwise  -> gemv1 (register-resident dot2 GEMV, LDS activations);
-//   2 <= M <= 64 else -> FWHT-128 to pair-f16 x_tf, then the small-M MFMA
+//                        into its prologue (one launch per linear, also with
+//                        the K split over workgroups: the last workgroup of
+//                        each row group adds the partial sums; M > 16 with
+//                        two m-tiles per weight lookup);
+//   M == 1 otherwise  -> gemv1 (register-resident dot2 GEMV, LDS activations)
+//                        for row-major weights with K within its LDS budget;
+//   M <= 64 else      -> FWHT-128 to pair-f16 x_tf, then the small-M MFMA
 //                        kernel (16x16x32 f16, K split across waves); at
 //                        M = 33..64 with fp16 out, the prefill GEMM instead
 //                        when its K split over workgroups applies;
