@@ -117,16 +117,6 @@ __device__ __forceinline__ u32x4v lds_ld128(uint32_t addr) {
   return *reinterpret_cast<const lds_u32x4*>(static_cast<uintptr_t>(addr));
 }
 
-// 16 bytes per lane from global memory straight into LDS (gfx950
-// global_load_lds_dwordx4, no VGPRs): lane i's bytes land at lds_addr + 16 i,
-// lds_addr wave-uniform. Counted by vmcnt like any other global load.
-typedef __attribute__((address_space(1))) void glb_void;
-typedef __attribute__((address_space(3))) void lds_void;
-__device__ __forceinline__ void g2lds16(const void* src, uint32_t lds_addr) {
-  __builtin_amdgcn_global_load_lds((const glb_void*)src,
-                                   (lds_void*)(static_cast<uintptr_t>(lds_addr)), 16, 0, 0);
-}
-
 // Device-coherent 32-bit accesses for data one workgroup hands to another
 // within one launch: agent-scope relaxed atomics, which compile to global
 // loads and stores with the sc1 cache policy (the level every XCD sees
