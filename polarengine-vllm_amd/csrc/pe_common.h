@@ -43,7 +43,6 @@ __device__ __forceinline__ uint4 ld_nt16(const void* p) {
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
-__device__ __forceinline__ uint32_t as_u32(half2v h) { return __builtin_bit_cast(uint32_t, h); }
 __device__ __forceinline__ half2v as_h2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
 
 __device__ __forceinline__ float h2f(uint16_t bits) {
