@@ -187,3 +187,24 @@ def test_fwht_cache_semantics():
     cache.put(x, 128, r)
     cache.clear()
     assert cache.get(x, 128) is None
+
+
+def test_fwht_clear_hook_as_forward_pre_hook():
+    """create_fwht_clear_hook (reference linear_method.py:265-288): a forward
+    pre-hook that empties the method's cache before the module runs."""
+    from polarengine_vllm.linear_method import PolarQuantLinearMethod, create_fwht_clear_hook
+    method = PolarQuantLinearMethod(128, 4)
+    x, r = torch.randn(4, 128), torch.randn(4, 128)
+    method._fwht_cache.put(x, 128, r)
+    seen = []
+
+    class Block(torch.nn.Module):
+        def forward(self, t):
+            seen.append(method._fwht_cache.get(x, 128))
+            return t
+
+    blk = Block()
+    blk.register_forward_pre_hook(create_fwht_clear_hook(method))
+    blk(x)
+    assert seen == [None]  # cleared before the forward ran
+    method._fwht_cache.clear()
