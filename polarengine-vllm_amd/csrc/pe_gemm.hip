@@ -270,10 +270,13 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Four-wave variant: one wave per SIMD, each wave owning BM = 32 TMW rows x 64
-// columns (two 32-column n-tiles), workgroup tile BM x 256. Per MFMA it moves
-// (TMW + 2) / (2 TMW) KB of operands through LDS instead of (TMW + 1) / TMW,
-// and every weight column is still dequantized by exactly one wave.
+// Four-wave variant: one wave per SIMD, each wave owning BM = 32 TMW rows x
+// 32 NTW columns (NTW 32-column n-tiles: 2 or 3), workgroup tile BM x 128 NTW.
+// Per MFMA it moves (TMW + NTW) / (NTW TMW) KB of operands through LDS instead
+// of (TMW + 1) / TMW, and every weight column is still dequantized by exactly
+// one wave; NTW = 3 (384 columns) cuts the LDS reads, A-tile stores and
+// barriers per MFMA by a further quarter to a third where its tiles fill the
+// CUs in as few rounds.
 //  * A half-block tiles sit in a ring of three LDS buffers: the tile of
 //    half-block kt + 1 is complete before the barrier that ends kt - 1, so the
 //    first slab of kt + 1 is read ahead while kt still computes.
@@ -285,20 +288,20 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
 //    end are clamped to the last half-block, so each wait count is static too.
 // Requires an even number of 128-blocks.
 // ---------------------------------------------------------------------------
-// Codes of one half-block for the wave's two n-tiles. Norms are kept
+// Codes of one half-block for the wave's NTW n-tiles. Norms are kept
 // zero-extended to 32 bits: 16-bit members next to vectors made the compiler
 // keep the slot in memory.
-template <bool NIB>
+template <bool NIB, int NTW>
 struct BSlot4 {
-  u32x4v lo[2];
-  u32x4v hi[NIB ? 1 : 2];  // int8 codes only: bytes at +64
-  uint32_t nrm[2];
+  u32x4v lo[NTW];
+  u32x4v hi[NIB ? 1 : NTW];  // int8 codes only: bytes at +64
+  uint32_t nrm[NTW];
 };
 
-template <bool NIB, int TMW>
+template <bool NIB, int TMW, int NTW>
 struct Frag4 {
   half8v a[TMW];
-  uint32_t raw[2][NIB ? 4 : 8];
+  uint32_t raw[NTW][NIB ? 4 : 8];
 };
 
 // A tiles of the four-wave kernel: 128-byte rows (32 pairs), 16-byte chunk c
@@ -310,16 +313,16 @@ struct Frag4 {
 constexpr int kARow4 = 128;
 __device__ __forceinline__ uint32_t a4_swz(int r) { return (uint32_t)((r >> 1) & 7); }
 
-template <bool NIB, int TMW, bool MASK>
-__device__ __forceinline__ void issue_frag4(Frag4<NIB, TMW>& f, uint32_t aaddr, int t,
-                                            const BSlot4<NIB>& bt, uint32_t lane4,
+template <bool NIB, int TMW, int NTW, bool MASK>
+__device__ __forceinline__ void issue_frag4(Frag4<NIB, TMW, NTW>& f, uint32_t aaddr, int t,
+                                            const BSlot4<NIB, NTW>& bt, uint32_t lane4,
                                             uint32_t code_mask) {
   // aaddr: this lane's row and swizzled chunk of slab t in m-tile 0
 #pragma unroll
   for (int i = 0; i < TMW; ++i)
     f.a[i] = __builtin_bit_cast(half8v, lds_ld128(aaddr + i * 32 * kARow4));
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < NTW; ++j) {
     uint32_t wl = bt.lo[j][t];
     if constexpr (MASK) wl &= code_mask;
     f.raw[j][0] = lds_ld32(tbl_addr<0>(wl, lane4));
@@ -337,11 +340,11 @@ __device__ __forceinline__ void issue_frag4(Frag4<NIB, TMW>& f, uint32_t aaddr, 
   }
 }
 
-template <bool NIB, int TMW>
-__device__ __forceinline__ void mma_frag4(float16v (&acc)[TMW][2], const Frag4<NIB, TMW>& f,
-                                          const BSlot4<NIB>& bt) {
+template <bool NIB, int TMW, int NTW>
+__device__ __forceinline__ void mma_frag4(float16v (&acc)[TMW][NTW], const Frag4<NIB, TMW, NTW>& f,
+                                          const BSlot4<NIB, NTW>& bt) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < NTW; ++j) {
     const _Float16 nh = __builtin_bit_cast(_Float16, (uint16_t)bt.nrm[j]);
     const half2v nrm2{nh, nh};
     half8v bf;
@@ -365,11 +368,11 @@ __device__ __forceinline__ void mma_frag4(float16v (&acc)[TMW][2], const Frag4<N
 // Output tile through LDS: the transposed accumulators (lane = row m, groups
 // of four consecutive columns) are written as 8- or 16-byte pieces into a
 // row-major staging tile, then copied to y in 16-byte coalesced stores.
-template <int TMW, int OM>
-__device__ __forceinline__ void store_tile4(const float16v (&acc)[TMW][2], void* __restrict__ y,
+template <int TMW, int NTW, int OM>
+__device__ __forceinline__ void store_tile4(const float16v (&acc)[TMW][NTW], void* __restrict__ y,
                                             int64_t ldy, const uint16_t* __restrict__ bias, int M,
                                             int N, int m0, int n0, int vec_ok, bool ybf) {
-  constexpr int BM = TMW * 32, BN = 256;
+  constexpr int BM = TMW * 32, BN = 128 * NTW;
   constexpr int ES = OM == OM_F16 ? 2 : 4;
   constexpr uint32_t OSTR = BN * ES + 16;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -378,11 +381,11 @@ __device__ __forceinline__ void store_tile4(const float16v (&acc)[TMW][2], void*
 #pragma unroll
   for (int i = 0; i < TMW; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NTW; ++j)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const uint32_t addr =
-            (uint32_t)(32 * i + l32) * OSTR + (uint32_t)(wave * 64 + 32 * j + 8 * g + 4 * h) * ES;
+        const uint32_t addr = (uint32_t)(32 * i + l32) * OSTR +
+                              (uint32_t)(wave * 32 * NTW + 32 * j + 8 * g + 4 * h) * ES;
         // element values first: a bit_cast applied to a vector element
         // lvalue reads element 0 of the vector with this compiler
         const float v0 = acc[i][j][4 * g], v1 = acc[i][j][4 * g + 1];
@@ -430,7 +433,7 @@ __device__ __forceinline__ void store_tile4(const float16v (&acc)[TMW][2], void*
   }
 }
 
-template <bool NIB, int TMW, bool MASK, int OM>
+template <bool NIB, int TMW, int NTW, bool MASK, int OM>
 __global__ __launch_bounds__(256) void gemm4_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
     const float* __restrict__ ct, int n_levels, uint32_t code_mask, int tbl_entries,
@@ -439,7 +442,7 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
     int ybf) {
   constexpr int NT = 256;
   constexpr int BM = TMW * 32;
-  constexpr int BN = 256;
+  constexpr int BN = 128 * NTW;
   constexpr int KA = BM * 8 / NT;
   constexpr uint32_t ABUF = BM * kARow4;
   static_assert(KA * NT == BM * 8, "A tile must split evenly over the threads");
@@ -480,11 +483,11 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
     a_src[i] = xp + (int64_t)m * xrow_u32 + (int64_t)kb0 * 64 + c * 4;
     a_dst[i] = (uint32_t)(r * kARow4 + (((uint32_t)c ^ a4_swz(r)) << 4));
   }
-  const uint8_t* b_row[2];
-  const uint16_t* n_row[2];
+  const uint8_t* b_row[NTW];
+  const uint16_t* n_row[NTW];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    int n = n0 + wave * 64 + j * 32 + l32;
+  for (int j = 0; j < NTW; ++j) {
+    int n = n0 + wave * 32 * NTW + j * 32 + l32;
     if (n >= N) n = N - 1;
     b_row[j] = codes + lay.codes_off(n) + 16 * h + (int64_t)kb0 * lay.c_blk;
     n_row[j] = norms + lay.norms_off(n) + (int64_t)kb0 * lay.n_blk;
@@ -495,11 +498,11 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
 
   const int nkt = 2 * nbz;  // half-blocks of this K range, a multiple of 4
   // loads past the last half-block re-read it (in bounds, never used)
-  auto ldb = [&](BSlot4<NIB>& sl, int kt) {
+  auto ldb = [&](BSlot4<NIB, NTW>& sl, int kt) {
     kt = kt < nkt ? kt : nkt - 1;
     const int bk = kt >> 1, half = kt & 1;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < NTW; ++j) {
       const uint8_t* pc = b_row[j] + bk * lay.c_blk + half * 32;
       sl.lo[j] = *reinterpret_cast<const u32x4v*>(pc);
       if constexpr (!NIB) sl.hi[j] = *reinterpret_cast<const u32x4v*>(pc + 64);
@@ -517,15 +520,15 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
     for (int i = 0; i < KA; ++i) lds_st128(buf + a_dst[i], rg[i]);
   };
 
-  float16v acc[TMW][2];
+  float16v acc[TMW][NTW];
 #pragma unroll
   for (int i = 0; i < TMW; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NTW; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  BSlot4<NIB> slot[4];
+  BSlot4<NIB, NTW> slot[4];
   u32x4v stg[2][KA];
   lda(stg[0], 0);
   lda(stg[1], 1);
@@ -539,8 +542,8 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
   lda(stg[1], 3);
   __syncthreads();
 
-  Frag4<NIB, TMW> f;
-  issue_frag4<NIB, TMW, MASK>(f, abuf + a_off[0], 0, slot[0], lane4, code_mask);
+  Frag4<NIB, TMW, NTW> f;
+  issue_frag4<NIB, TMW, NTW, MASK>(f, abuf + a_off[0], 0, slot[0], lane4, code_mask);
   uint32_t bcur = 0;  // ring offset (bytes) of half-block kt's A buffer
 
   auto half_step = [&](auto S_, int kt) {
@@ -551,12 +554,12 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      Frag4<NIB, TMW> fn;
-      if (t < 3) issue_frag4<NIB, TMW, MASK>(fn, abuf + bcur + a_off[t + 1], t + 1, slot[S], lane4, code_mask);
-      else issue_frag4<NIB, TMW, MASK>(fn, abuf + bnext + a_off[0], 0, slot[(S + 1) & 3], lane4, code_mask);
+      Frag4<NIB, TMW, NTW> fn;
+      if (t < 3) issue_frag4<NIB, TMW, NTW, MASK>(fn, abuf + bcur + a_off[t + 1], t + 1, slot[S], lane4, code_mask);
+      else issue_frag4<NIB, TMW, NTW, MASK>(fn, abuf + bnext + a_off[0], 0, slot[(S + 1) & 3], lane4, code_mask);
       // keep the next slab's reads ahead of this slab's MFMAs
       __builtin_amdgcn_sched_barrier(0);
-      mma_frag4<NIB, TMW>(acc, f, slot[S]);
+      mma_frag4<NIB, TMW, NTW>(acc, f, slot[S]);
       f = fn;
     }
     sta(abuf + bst, stg[S & 1]);  // A(kt + 2)
@@ -571,13 +574,13 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
     half_step(std::integral_constant<int, 3>{}, kt + 3);
   }
 
-  store_tile4<TMW, OM>(acc, y, ldy, bias, M, N, m0, n0, vec_ok, ybf != 0);
+  store_tile4<TMW, NTW, OM>(acc, y, ldy, bias, M, N, m0, n0, vec_ok, ybf != 0);
 }
 
-template <bool NIB, int TMW, bool MASK, int OM>
+template <bool NIB, int TMW, int NTW, bool MASK, int OM>
 static int launch_gemm4_t(const GemmArgs& a, hipStream_t st, int ksplit = 1) {
-  constexpr int BM = TMW * 32, BN = 256;
-  auto kern = gemm4_kernel<NIB, TMW, MASK, OM>;
+  constexpr int BM = TMW * 32, BN = 128 * NTW;
+  auto kern = gemm4_kernel<NIB, TMW, NTW, MASK, OM>;
   const int entries = table_entries(NIB, a.n_levels);
   constexpr size_t ES = OM == OM_F16 ? 2 : 4;
   const size_t lds_loop = (size_t)entries * 256 + 3 * (size_t)BM * kARow4;
@@ -658,6 +661,29 @@ static GemmShape pick_gemm_tile(int M, int N) {
   return best;
 }
 
+// n-tiles per wave of the four-wave kernel: the width whose tiles take the
+// fewest rounds x columns per CU (M = 2048 on 12288 columns: 768 tiles of 256
+// in three rounds or 512 of 384 in two, equal); ties go to the wider tile,
+// which reads less through LDS and stores fewer A tiles and passes fewer
+// barriers per MFMA. Only for nibble codes with 16-bit output: 384 fp32
+// columns would not fit the output staging in LDS, and the int8 variant
+// needs more registers than a wave has (it spilled).
+static int gemm4_ntw(bool nibble, int M, int N, int om) {
+  if (!nibble || om != OM_F16) return 2;
+  const int cus = num_cus();
+  int best = 2;
+  int64_t best_cost = -1;
+  for (int ntw = 2; ntw <= 3; ++ntw) {
+    const int64_t tiles = (int64_t)((M + 127) / 128) * ((N + 128 * ntw - 1) / (128 * ntw));
+    const int64_t cost = (tiles + cus - 1) / cus * ntw;
+    if (best_cost < 0 || cost <= best_cost) {
+      best = ntw;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
 static bool use_gemm4(int M, int N, int nb) {
   const int64_t tiles4 = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
   return (nb & 1) == 0 && tiles4 >= num_cus() && tiles4 <= 4 * (int64_t)num_cus();
@@ -713,7 +739,11 @@ template <bool NIB, int OM>
 static int launch_gemm_shape(const GemmArgs& a, hipStream_t st, void* ws, size_t ws_bytes) {
   if (use_gemm4(a.M, a.N, a.nb)) {
     const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
-    return mask ? launch_gemm4_t<NIB, 4, true, OM>(a, st) : launch_gemm4_t<NIB, 4, false, OM>(a, st);
+    if constexpr (NIB && OM == OM_F16) {
+      if (gemm4_ntw(NIB, a.M, a.N, OM) == 3)
+        return mask ? launch_gemm4_t<NIB, 4, 3, true, OM>(a, st) : launch_gemm4_t<NIB, 4, 3, false, OM>(a, st);
+    }
+    return mask ? launch_gemm4_t<NIB, 4, 2, true, OM>(a, st) : launch_gemm4_t<NIB, 4, 2, false, OM>(a, st);
   }
   // fp16 out (the linear entry points): split K when the tiles are few and
   // the workspace holds the partial sums; otherwise one launch
@@ -724,8 +754,8 @@ static int launch_gemm_shape(const GemmArgs& a, hipStream_t st, void* ws, size_t
     p.ldy = a.N;
     p.bias = nullptr;
     const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
-    const int rc = mask ? launch_gemm4_t<NIB, 4, true, OM_F32>(p, st, z4)
-                        : launch_gemm4_t<NIB, 4, false, OM_F32>(p, st, z4);
+    const int rc = mask ? launch_gemm4_t<NIB, 4, 2, true, OM_F32>(p, st, z4)
+                        : launch_gemm4_t<NIB, 4, 2, false, OM_F32>(p, st, z4);
     if (rc) return rc;
     return split_reduce(reinterpret_cast<const float*>(ws), z4, a.M, a.N, a.bias, a.y, a.ldy, st,
                         a.ybf != 0);
