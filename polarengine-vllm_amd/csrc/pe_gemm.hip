@@ -277,13 +277,16 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
 // one wave; NTW = 3 (384 columns) cuts the LDS reads, A-tile stores and
 // barriers per MFMA by a further quarter to a third where its tiles fill the
 // CUs in as few rounds.
-//  * A half-block tiles sit in a ring of three LDS buffers: the tile of
-//    half-block kt + 1 is complete before the barrier that ends kt - 1, so the
-//    first slab of kt + 1 is read ahead while kt still computes.
+//  * A half-block tiles sit in a ring of six LDS buffers (96 KB beside the
+//    64 KB table), stored four half-blocks ahead, with one barrier per two
+//    half-blocks: the tile of half-block kt + 1 is complete before the barrier
+//    that precedes kt, so the first slab of kt + 1 is read ahead while kt
+//    still computes.
 //  * Within a half-block every slab's operands (A fragments and codebook
 //    lookups) are issued one slab ahead of its MFMAs.
 //  * Codes ride a ring of four half-block slots (issued three half-blocks
-//    ahead), activations a ring of two register stages (two ahead); the loop
+//    ahead), activations a ring of two register stages (loaded six ahead,
+//    stored four ahead); the loop
 //    body covers four half-blocks so every ring index is static. Loads past the
 //    end are clamped to the last half-block, so each wait count is static too.
 // Requires an even number of 128-blocks.
@@ -311,6 +314,9 @@ struct Frag4 {
 // the eight rows of each parity need eight distinct chunks. The plain
 // c ^ (r & 7) repeats after eight rows and made every A read a 2-way conflict.
 constexpr int kARow4 = 128;
+// A half-block tiles in the four-wave kernel's LDS ring (16 KB each at 128
+// rows): A(kt + 4) is stored while A(kt) is read, one barrier per two tiles
+constexpr int kA4Ring = 6;
 __device__ __forceinline__ uint32_t a4_swz(int r) { return (uint32_t)((r >> 1) & 7); }
 
 template <bool NIB, int TMW, int NTW, bool MASK>
@@ -529,27 +535,32 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   BSlot4<NIB, NTW> slot[4];
-  u32x4v stg[2][KA];
+  u32x4v stg[2][KA], pre[2][KA];  // pre: prologue only
   lda(stg[0], 0);
   lda(stg[1], 1);
+  lda(pre[0], 2);
+  lda(pre[1], 3);
   ldb(slot[0], 0);
   ldb(slot[1], 1);
   ldb(slot[2], 2);
   __syncthreads();  // codebook table written
   sta(abuf, stg[0]);
   sta(abuf + ABUF, stg[1]);
-  lda(stg[0], 2);
-  lda(stg[1], 3);
+  sta(abuf + 2 * ABUF, pre[0]);
+  sta(abuf + 3 * ABUF, pre[1]);
+  lda(stg[0], 4);
+  lda(stg[1], 5);
   __syncthreads();
 
   Frag4<NIB, TMW, NTW> f;
   issue_frag4<NIB, TMW, NTW, MASK>(f, abuf + a_off[0], 0, slot[0], lane4, code_mask);
   uint32_t bcur = 0;  // ring offset (bytes) of half-block kt's A buffer
+  auto ring_next = [](uint32_t b) { return b == (kA4Ring - 1) * ABUF ? 0u : b + ABUF; };
 
   auto half_step = [&](auto S_, int kt) {
     constexpr int S = decltype(S_)::value;
-    const uint32_t bnext = bcur == 2 * ABUF ? 0u : bcur + ABUF;
-    const uint32_t bst = bnext == 2 * ABUF ? 0u : bnext + ABUF;
+    const uint32_t bnext = ring_next(bcur);
+    const uint32_t bst = ring_next(ring_next(ring_next(bnext)));  // where A(kt - 2) was
     ldb(slot[(S + 3) & 3], kt + 3);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -562,10 +573,13 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
       mma_frag4<NIB, TMW, NTW>(acc, f, slot[S]);
       f = fn;
     }
-    sta(abuf + bst, stg[S & 1]);  // A(kt + 2)
-    lda(stg[S & 1], kt + 4);
+    sta(abuf + bst, stg[S & 1]);  // A(kt + 4)
+    lda(stg[S & 1], kt + 6);
     bcur = bnext;
-    __syncthreads();
+    // one barrier per 128-block: between two of them the waves read A(kt),
+    // A(kt + 1) and the first slab of A(kt + 2) while A(kt + 4), A(kt + 5)
+    // go into the buffers of A(kt - 2), A(kt - 1), read before the last one
+    if constexpr (S & 1) __syncthreads();
   };
   for (int kt = 0; kt < nkt; kt += 4) {
     half_step(std::integral_constant<int, 0>{}, kt);
@@ -583,7 +597,7 @@ static int launch_gemm4_t(const GemmArgs& a, hipStream_t st, int ksplit = 1) {
   auto kern = gemm4_kernel<NIB, TMW, NTW, MASK, OM>;
   const int entries = table_entries(NIB, a.n_levels);
   constexpr size_t ES = OM == OM_F16 ? 2 : 4;
-  const size_t lds_loop = (size_t)entries * 256 + 3 * (size_t)BM * kARow4;
+  const size_t lds_loop = (size_t)entries * 256 + kA4Ring * (size_t)BM * kARow4;
   const size_t lds_out = (size_t)BM * (BN * ES + 16);
   const size_t lds = lds_loop > lds_out ? lds_loop : lds_out;
   if (lds > 160 * 1024) return PE_ERR_DIMS;
