@@ -700,7 +700,7 @@ static int gemm4_ntw(bool nibble, int M, int N, int om) {
 
 static bool use_gemm4(int M, int N, int nb) {
   const int64_t tiles4 = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
-  return (nb & 1) == 0 && tiles4 >= num_cus() && tiles4 <= 4 * (int64_t)num_cus();
+  return (nb & 1) == 0 && tiles4 >= num_cus() && tiles4 <= 16 * (int64_t)num_cus();
 }
 
 // K split of the four-wave kernel for M >= 256 whose 128 x 256 tiles are too
@@ -732,10 +732,11 @@ static int gemm_ksplit(int M, int N, int nb) {
   return z < 2 ? 1 : z;
 }
 
-// The four-wave kernel (128 x 256 tiles) is the faster one when its tiles fill
-// the CUs for one to four rounds (measured on M = 2048 prefill shapes: 6-18%
-// ahead); with fewer tiles the eight-wave kernel's narrower tiles spread
-// wider, and with many rounds its two waves per SIMD hide more latency.
+// The four-wave kernel (128 x 256 or 128 x 384 tiles) is the faster one when
+// its tiles fill the CUs for one to sixteen rounds (measured on the C3
+// prefill shapes: 6-18% ahead at M = 2048, 2.5-4% at M = 8192 on 12288
+// columns); with fewer tiles the eight-wave kernel's narrower tiles spread
+// wider.
 template <bool NIB, int OM>
 static int launch_gemm_eight(const GemmArgs& a, hipStream_t st, int ksplit) {
   const GemmShape g = pick_gemm_tile(a.M, a.N);
