@@ -698,6 +698,17 @@ static int gemm4_ntw(bool nibble, int M, int N, int om) {
   return best;
 }
 
+// 64-row four-wave tiles for 16-bit output when the 128-row ones are too few
+// for one round and the 64-row ones fill at least three quarters of it (M =
+// 256 on 12288 columns: 192 tiles): one launch without the K split's fp32
+// partial sums and reduction (Q4 12288 x 4096 at M = 256: 52.3-52.7 against
+// 56.6-57.0 us with the split), at the cost of half the MFMAs per codebook
+// lookup.
+static bool use_gemm4_short(int M, int N, int nb) {
+  const int64_t tiles = (int64_t)((M + 63) / 64) * ((N + 255) / 256);
+  return (nb & 1) == 0 && tiles * 4 >= 3 * (int64_t)num_cus() && tiles <= num_cus();
+}
+
 static bool use_gemm4(int M, int N, int nb) {
   const int64_t tiles4 = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
   return (nb & 1) == 0 && tiles4 >= num_cus() && tiles4 <= 16 * (int64_t)num_cus();
@@ -708,7 +719,7 @@ static bool use_gemm4(int M, int N, int nb) {
 // tiles): groups of at least four 128-blocks (an even count each), about one
 // workgroup per CU in all. 1 = no split.
 static int gemm4_ksplit(int M, int N, int nb) {
-  if (M < 256 || (nb & 1) || use_gemm4(M, N, nb)) return 1;
+  if (M < 256 || (nb & 1) || use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb)) return 1;
   const int64_t tiles4 = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
   int z = (int)(num_cus() / tiles4);
   if (z > nb / 4) z = nb / 4;
@@ -721,7 +732,7 @@ static int gemm4_ksplit(int M, int N, int nb) {
 // fp32 partial sums in the workspace, then the ordered reduction shared with
 // the decode path. 1 = no split (the four-wave kernel never splits).
 static int gemm_ksplit(int M, int N, int nb) {
-  if (use_gemm4(M, N, nb) || gemm4_ksplit(M, N, nb) > 1) return 1;
+  if (use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb) || gemm4_ksplit(M, N, nb) > 1) return 1;
   const GemmShape g = pick_gemm_tile(M, N);
   const int bm = 32 * g.tmw, bn = 32 * g.wn;
   const int64_t tiles = (int64_t)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
@@ -759,6 +770,12 @@ static int launch_gemm_shape(const GemmArgs& a, hipStream_t st, void* ws, size_t
         return mask ? launch_gemm4_t<NIB, 4, 3, true, OM>(a, st) : launch_gemm4_t<NIB, 4, 3, false, OM>(a, st);
     }
     return mask ? launch_gemm4_t<NIB, 4, 2, true, OM>(a, st) : launch_gemm4_t<NIB, 4, 2, false, OM>(a, st);
+  }
+  if constexpr (OM == OM_F16) {
+    if (use_gemm4_short(a.M, a.N, a.nb)) {
+      const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
+      return mask ? launch_gemm4_t<NIB, 2, 2, true, OM>(a, st) : launch_gemm4_t<NIB, 2, 2, false, OM>(a, st);
+    }
   }
   // fp16 out (the linear entry points): split K when the tiles are few and
   // the workspace holds the partial sums; otherwise one launch

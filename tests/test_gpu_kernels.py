@@ -491,10 +491,12 @@ def test_prefill_ksplit_row_sample(m, n, k, bits):
 # Shapes whose 128 x 256 tile count fills the CUs for one to four rounds take
 # the four-wave prefill kernel: f16 and f32 outputs, nibble and int8 codes,
 # masked small codebooks, bias, M and N tails, both weight layouts; the last
-# two (nibble codes, 16-bit out) take its 384-column tiles, N ragged.
+# two (nibble codes, 16-bit out) take its 384-column tiles, N ragged; the
+# M = 300 ones its 64-row tiles (one round without a K split), M and N ragged.
 FOUR_WAVE_CASES = [(2048, 4096, 4096, 4, "f16", False, True), (2000, 4200, 4096, 6, "f16", True, False),
                    (2048, 4096, 4096, 3, "f32", False, False), (2048, 4096, 2048, 8, "f32", False, False),
-                   (1950, 4352, 1024, 2, "f16", True, True), (2048, 12200, 2048, 3, "f16", False, False)]
+                   (1950, 4352, 1024, 2, "f16", True, True), (2048, 12200, 2048, 3, "f16", False, False),
+                   (300, 10000, 2048, 3, "f16", True, False), (300, 10000, 2048, 5, "f16", False, True)]
 
 
 @pytest.mark.parametrize("m,n,k,bits,out,with_bias,tiled", FOUR_WAVE_CASES)
