@@ -714,23 +714,32 @@ static bool use_gemm4(int M, int N, int nb) {
   return (nb & 1) == 0 && tiles4 >= num_cus() && tiles4 <= 16 * (int64_t)num_cus();
 }
 
-// K split of the four-wave kernel for M >= 256 whose 128 x 256 tiles are too
-// few for one round (M = 256..512 on the 4096 x 12288 down projection: 32-64
-// tiles): groups of at least four 128-blocks (an even count each), about one
+// K split of the four-wave kernel for M > 64 whose tiles are too few for one
+// round (M = 128..512 on the 4096 x 12288 down projection: 32-64 tiles):
+// groups of at least four 128-blocks (an even count each), about one
 // workgroup per CU in all. 1 = no split.
+// Tile rows of that split: 64 up to M = 256 (half the fp32 partial sums of
+// 128-row tiles at the same grid size; measured against the eight-wave
+// kernel's split at M = 128: 31.9 against 43.7 us on the 4096 x 12288 down
+// projection, 33.3 against 45.5 on Q4 12288 x 4096; M = 256 on the down
+// projection 47.1 against 48.5 with 128-row tiles), 128 above (M = 512: 79.1
+// against 82.4 us with 64-row ones).
+static int gemm4_split_rows(int M) { return M <= 256 ? 64 : 128; }
+
 static int gemm4_ksplit(int M, int N, int nb) {
-  if (M < 256 || (nb & 1) || use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb)) return 1;
-  const int64_t tiles4 = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
+  if (M <= 64 || (nb & 1) || use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb)) return 1;
+  const int rows = gemm4_split_rows(M);
+  const int64_t tiles4 = (int64_t)((M + rows - 1) / rows) * ((N + 255) / 256);
   int z = (int)(num_cus() / tiles4);
   if (z > nb / 4) z = nb / 4;
   return z < 2 ? 1 : z;
 }
 
-// K split of the eight-wave kernel when its tiles would leave more than half
-// the CUs idle (few output tiles over a long K: M = 128 on the 4096 x 12288
-// down projection has 32): gemm_ksplit groups of at least two 128-blocks,
-// fp32 partial sums in the workspace, then the ordered reduction shared with
-// the decode path. 1 = no split (the four-wave kernel never splits).
+// K split of the eight-wave kernel where the four-wave one takes none (M =
+// 33..64, an odd block count) and its tiles would leave more than half the
+// CUs idle (few output tiles over a long K): gemm_ksplit groups of at least
+// two 128-blocks, fp32 partial sums in the workspace, then the ordered
+// reduction shared with the decode path. 1 = no split.
 static int gemm_ksplit(int M, int N, int nb) {
   if (use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb) || gemm4_ksplit(M, N, nb) > 1) return 1;
   const GemmShape g = pick_gemm_tile(M, N);
@@ -786,8 +795,11 @@ static int launch_gemm_shape(const GemmArgs& a, hipStream_t st, void* ws, size_t
     p.ldy = a.N;
     p.bias = nullptr;
     const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
-    const int rc = mask ? launch_gemm4_t<NIB, 4, 2, true, OM_F32>(p, st, z4)
-                        : launch_gemm4_t<NIB, 4, 2, false, OM_F32>(p, st, z4);
+    const int rc = gemm4_split_rows(a.M) == 64
+                       ? (mask ? launch_gemm4_t<NIB, 2, 2, true, OM_F32>(p, st, z4)
+                               : launch_gemm4_t<NIB, 2, 2, false, OM_F32>(p, st, z4))
+                       : (mask ? launch_gemm4_t<NIB, 4, 2, true, OM_F32>(p, st, z4)
+                               : launch_gemm4_t<NIB, 4, 2, false, OM_F32>(p, st, z4));
     if (rc) return rc;
     return split_reduce(reinterpret_cast<const float*>(ws), z4, a.M, a.N, a.bias, a.y, a.ldy, st,
                         a.ybf != 0);
