@@ -714,8 +714,8 @@ static bool use_gemm4(int M, int N, int nb) {
   return (nb & 1) == 0 && tiles4 >= num_cus() && tiles4 <= 16 * (int64_t)num_cus();
 }
 
-// K split of the four-wave kernel for M > 64 whose tiles are too few for one
-// round (M = 128..512 on the 4096 x 12288 down projection: 32-64 tiles):
+// K split of the four-wave kernel for M > 32 whose tiles are too few for one
+// round (M = 33..512 on the 4096 x 12288 down projection: 16-64 tiles):
 // groups of at least four 128-blocks (an even count each), about one
 // workgroup per CU in all. 1 = no split.
 // Tile rows of that split: 64 up to M = 256 (half the fp32 partial sums of
@@ -727,7 +727,7 @@ static bool use_gemm4(int M, int N, int nb) {
 static int gemm4_split_rows(int M) { return M <= 256 ? 64 : 128; }
 
 static int gemm4_ksplit(int M, int N, int nb) {
-  if (M <= 64 || (nb & 1) || use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb)) return 1;
+  if (M <= 32 || (nb & 1) || use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb)) return 1;
   const int rows = gemm4_split_rows(M);
   const int64_t tiles4 = (int64_t)((M + rows - 1) / rows) * ((N + 255) / 256);
   int z = (int)(num_cus() / tiles4);
@@ -735,11 +735,12 @@ static int gemm4_ksplit(int M, int N, int nb) {
   return z < 2 ? 1 : z;
 }
 
-// K split of the eight-wave kernel where the four-wave one takes none (M =
-// 33..64, an odd block count) and its tiles would leave more than half the
-// CUs idle (few output tiles over a long K): gemm_ksplit groups of at least
-// two 128-blocks, fp32 partial sums in the workspace, then the ordered
-// reduction shared with the decode path. 1 = no split.
+// K split of the eight-wave kernel where the four-wave one takes none (an
+// odd block count, or too many 64-row tiles for a split) and its tiles would
+// leave more than half the CUs idle (few output tiles over a long K):
+// gemm_ksplit groups of at least two 128-blocks, fp32 partial sums in the
+// workspace, then the ordered reduction shared with the decode path. 1 = no
+// split.
 static int gemm_ksplit(int M, int N, int nb) {
   if (use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb) || gemm4_ksplit(M, N, nb) > 1) return 1;
   const GemmShape g = pick_gemm_tile(M, N);
@@ -824,12 +825,14 @@ int gemm(bool nibble, int omode, const GemmArgs& a, hipStream_t st, void* ws, si
 
 // Matmul on a pair-f16 x_tf, used by the linear entry points for M > 1: the
 // fp32 partial sums of the K split, if it applies.
-// M = 33..64 with fp16 out takes the GEMM when its K split applies (measured
-// 29-32 us against 57 us for the small-M kernel at M = 64 on the MLP shapes)
+// M = 33..64 with fp16 out takes the GEMM when a K split applies (the
+// four-wave kernel's with 64-row tiles: 25.0 us at M = 64 on Q4 12288 x 4096,
+// against 31.5 us for the eight-wave kernel's split and 57 us for the
+// small-M kernel)
 static bool mm_small(int64_t M, int N, int nb, int out_mode) {
   if (M <= 32) return true;
   if (M > kSmallMaxRows) return false;
-  return out_mode != OM_F16 || gemm_ksplit((int)M, N, nb) <= 1;
+  return out_mode != OM_F16 || (gemm4_ksplit((int)M, N, nb) <= 1 && gemm_ksplit((int)M, N, nb) <= 1);
 }
 
 size_t mm_xtf_workspace(bool nibble, int64_t M, int N, int nb) {

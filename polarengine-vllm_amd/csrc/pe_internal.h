@@ -104,7 +104,7 @@ int moe_grouped(bool nibble, int epilogue, const SmallArgs& a, int groups, hipSt
 
 // pe_gemv_mfma.hip: decode GEMV, 1 <= M <= kDecMaxRows (M > 16 through the K
 // split with two m-tiles; at M = 33..64 the prefill GEMM's K split measured
-// faster: 29-32 against 44 us at M = 64), fp16 out (+ fp16 bias)
+// faster: 25 against 44 us at M = 64), fp16 out (+ fp16 bias)
 constexpr int kDecMaxRows = 32;
 struct DecArgs {
   const uint8_t* codes;
