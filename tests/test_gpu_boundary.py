@@ -29,13 +29,17 @@ def _want_bf16(x32, codes, norms, ct, k, bias32=None):
 
 # every route of pe_linear_forward that a test-sized matrix reaches: decode
 # M = 1 (tiled and row-major, fused FWHT), decode with the K split (M = 16),
-# small-M matmul (M = 40), prefill with the K split (M = 300), the four-wave
-# prefill (M = 2048), and the M = 1 fallback past the decode kernel
-# (K = 53248). (The M = 1 GEMV on raw x is left only for row-major weights
-# past 2 GiB.)
+# small-M matmul (M = 40), prefill with the K split (M = 300; M = 128 and
+# M = 48 on the four-wave kernel's 64-row tiles), the four-wave prefill
+# (M = 2048; with 384-column tiles at N = 12200, ragged), its 64-row tiles
+# in one launch (M = 300, N = 10000), and the M = 1 fallback past the decode
+# kernel (K = 53248). (The M = 1 GEMV on raw x is left only for row-major
+# weights past 2 GiB.)
 BF16_ROUTES = [(1, 12288, 4096, 4, True), (16, 12288, 4096, 4, True), (1, 4096, 4096, 5, False),
                (40, 768, 2048, 3, True), (300, 4100, 8192, 4, True),
-               (2048, 4096, 4096, 6, True), (1, 4096, 53248, 4, True)]
+               (2048, 4096, 4096, 6, True), (1, 4096, 53248, 4, True),
+               (2048, 12200, 2048, 3, True), (300, 10000, 2048, 4, False),
+               (128, 4096, 12288, 4, True), (48, 12288, 4096, 3, True)]
 
 
 @pytest.mark.parametrize("m,n,k,bits,tiled", BF16_ROUTES)
