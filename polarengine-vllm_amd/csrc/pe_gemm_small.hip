@@ -274,6 +274,10 @@ static int launch_small_ep(const SmallArgs& a, hipStream_t st) {
 constexpr int kMoeWaves = 8;
 constexpr int kMoeThreads = 64 * kMoeWaves;
 constexpr int kMoeRows = 32;  // activation rows per pass (two 16-row m-tiles)
+// Rows per pass for experts with many rows (prefill): four m-tiles, so each
+// expert's weights are streamed half as often (at about 27 more VGPRs: one
+// workgroup per CU)
+constexpr int kMoeRowsWide = 64;
 // 16-row tiles per wave of the SE_F32 (w2) kernel with nibble codes; 2 keeps
 // two workgroups per CU (4 tiles: one, and slower)
 constexpr int kMoeF32Tiles = 2;
@@ -328,15 +332,17 @@ __device__ __forceinline__ int moe_tile_row(int x, int wave, int j) {
   else return x * (NT * 16 * kMoeWaves) + j * (16 * kMoeWaves) + wave * 16;
 }
 
-template <bool NIB, int EP, int D>
+template <bool NIB, int EP, int D, int MR>
 __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint32_t code_mask,
                                                                int tbl_entries, uint32_t abuf) {
   constexpr bool SWI = EP == SE_SWIGLU || EP == SE_SWIGLU_XTF;
+  constexpr int MTX = MR / 16;  // m-tiles per pass
+  constexpr int SR = MR / 32;   // staged rows per thread
   // tiles per wave: gate and up (SwiGLU); SE_F32 with nibble codes: two
   // 16-row tiles 128 rows apart, so the workgroup's table fill, staging and
   // prologue serve 256 weight rows
   constexpr int NT = SWI ? 2 : (NIB ? kMoeF32Tiles : 1);
-  constexpr uint32_t kStage = kMoeRows * 256;  // bytes per LDS stage
+  constexpr uint32_t kStage = MR * 256;  // bytes per LDS stage
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -373,29 +379,38 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
   else
     fill_codebook<TBL_F16>(0, a.ct, a.n_levels, tbl_entries, kMoeWaves);
 
-  // staging role of this thread: row sr, 16-byte chunk sc of the 256-byte block row
-  static_assert(kMoeThreads == 16 * kMoeRows, "one 16-byte chunk of one staged row per thread");
+  // staging role of this thread: rows sr + 32 k (k < SR), 16-byte chunk sc of
+  // the 256-byte block row
+  static_assert(kMoeThreads == 16 * 32, "one 16-byte chunk of 32 staged rows per thread pass");
   const int sr = tid >> 4, sc = tid & 15;
-  const uint32_t sdst = (uint32_t)sr * 256u + ((uint32_t)(sc ^ (sr & 15)) << 4);
+  uint32_t sdst[SR];
+#pragma unroll
+  for (int k = 0; k < SR; ++k)
+    sdst[k] = (uint32_t)(sr + 32 * k) * 256u + ((uint32_t)(sc ^ (sr & 15)) << 4);
   const int64_t xrow = (int64_t)a.nb * 64;  // uint32 per activation row
 
-  for (int mbase = 0; mbase < M; mbase += kMoeRows) {
+  for (int mbase = 0; mbase < M; mbase += MR) {
     const int mrem = M - mbase;
-    const int MT = mrem > 16 ? 2 : 1;
+    const int MT = mrem >= MR ? MTX : (mrem + 15) >> 4;
     // Rows past M re-read row M - 1 and blocks past the end re-read the last
     // block: every lane issues the same loads on every path, so the
     // compiler's vmcnt waits stay exact (a conditional load made it wait for
     // every outstanding load). Rows past M only feed outputs never stored.
-    int srow = row0 + (mbase + sr < M ? mbase + sr : M - 1);
-    if (a.a_rows) srow = a.a_rows[srow];
-    const uint32_t* ssrc = a.xp + (int64_t)srow * xrow + sc * 4;
-    auto lda = [&](int b) -> u32x4v {
-      b = b < a.nb ? b : a.nb - 1;
-      return *reinterpret_cast<const u32x4v*>(ssrc + (int64_t)b * 64);
-    };
-    float4v acc[2][NT];
+    const uint32_t* ssrc[SR];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int k = 0; k < SR; ++k) {
+      const int rr = sr + 32 * k;
+      int srow = row0 + (mbase + rr < M ? mbase + rr : M - 1);
+      if (a.a_rows) srow = a.a_rows[srow];
+      ssrc[k] = a.xp + (int64_t)srow * xrow + sc * 4;
+    }
+    auto lda = [&](int k, int b) -> u32x4v {
+      b = b < a.nb ? b : a.nb - 1;
+      return *reinterpret_cast<const u32x4v*>(ssrc[k] + (int64_t)b * 64);
+    };
+    float4v acc[MTX][NT];
+#pragma unroll
+    for (int i = 0; i < MTX; ++i)
 #pragma unroll
       for (int j = 0; j < NT; ++j) acc[i][j] = float4v{0.f, 0.f, 0.f, 0.f};
 
@@ -405,13 +420,18 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
       moe_load_w<NIB, NT>(ring[d], src, d, a.nb, a.lay);
       __builtin_amdgcn_sched_barrier(0);
     }
-    // activation FIFO: block k is loaded D blocks before it is staged and
-    // waits in sreg[k % D]
-    u32x4v sreg[D];
-    sreg[0] = lda(0);
-    lds_st128(abuf + sdst, sreg[0]);
+    // activation FIFO: block q is loaded D blocks before it is staged and
+    // waits in sreg[q % D]
+    u32x4v sreg[D][SR];
 #pragma unroll
-    for (int k = 1; k <= D; ++k) sreg[k % D] = lda(k);
+    for (int k = 0; k < SR; ++k) {
+      sreg[0][k] = lda(k, 0);
+      lds_st128(abuf + sdst[k], sreg[0][k]);
+    }
+#pragma unroll
+    for (int q = 1; q <= D; ++q)
+#pragma unroll
+      for (int k = 0; k < SR; ++k) sreg[q % D][k] = lda(k, q);
     __syncthreads();  // codebook table and stage 0 written
 
     // A row of this lane in m-tile i: activation row 16 i + l16 of the stage.
@@ -440,7 +460,7 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
             // reads and codebook lookups of slab t + 1 are issued before the
             // MFMAs of slab t
             constexpr int TV = NIB ? 4 : 8;  // lookups per (tile, slab)
-            auto issue = [&](auto t_, u32x4v (&af)[2], uint32_t (&tv)[NT][TV]) {
+            auto issue = [&](auto t_, u32x4v (&af)[MTX], uint32_t (&tv)[NT][TV]) {
               constexpr int t = decltype(t_)::value;
 #pragma unroll
               for (int i = 0; i < MTC; ++i) {
@@ -463,7 +483,7 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
                 }
               }
             };
-            auto mma = [&](const u32x4v (&af)[2], const uint32_t (&tv)[NT][TV]) {
+            auto mma = [&](const u32x4v (&af)[MTX], const uint32_t (&tv)[NT][TV]) {
 #pragma unroll
               for (int j = 0; j < NT; ++j) {
                 u32x4v bw;
@@ -480,7 +500,7 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
                                                                      acc[i][j], 0, 0, 0);
               }
             };
-            u32x4v af0[2], af1[2];
+            u32x4v af0[MTX], af1[MTX];
             uint32_t tv0[NT][TV], tv1[NT][TV];
             issue(std::integral_constant<int, 0>{}, af0, tv0);
             issue(std::integral_constant<int, 1>{}, af1, tv1);
@@ -497,26 +517,36 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
             moe_load_w<NIB, NT>(ring[d], src, b + D, a.nb, a.lay);
             // next stage: block b + 1 into the other buffer (its readers, block
             // b - 1, finished before the previous barrier); load block b + 1 + D
-            if (b + 1 < a.nb) lds_st128(abuf + (uint32_t)((b + 1) & 1) * kStage + sdst, sreg[(d + 1) % D]);
-            sreg[(d + 1) % D] = lda(b + 1 + D);
+#pragma unroll
+            for (int k = 0; k < SR; ++k) {
+              if (b + 1 < a.nb) lds_st128(abuf + (uint32_t)((b + 1) & 1) * kStage + sdst[k], sreg[(d + 1) % D][k]);
+              sreg[(d + 1) % D][k] = lda(k, b + 1 + D);
+            }
             __syncthreads();
           }
         }
       }
     };
-    if (MT == 2) kloop(std::integral_constant<int, 2>{});
-    else kloop(std::integral_constant<int, 1>{});
+    if constexpr (MTX == 4) {
+      if (MT == 4) kloop(std::integral_constant<int, 4>{});
+      else if (MT == 3) kloop(std::integral_constant<int, 3>{});
+      else if (MT == 2) kloop(std::integral_constant<int, 2>{});
+      else kloop(std::integral_constant<int, 1>{});
+    } else {
+      if (MT == 2) kloop(std::integral_constant<int, 2>{});
+      else kloop(std::integral_constant<int, 1>{});
+    }
 
     if constexpr (EP == SE_SWIGLU_XTF) {
       // The workgroup's 128 columns are one 128-block of h: silu(gate) * up
-      // as fp16 into an LDS tile [32 rows][128] (over the stage buffers; the
+      // as fp16 into an LDS tile [MR rows][128] (over the stage buffers; the
       // barrier above ended their reads), then one 16-lane group per row
       // transforms its block and writes pair f16 (x_tf[p], x_tf[p + 64]) at
       // dword p of row (row0 + m), block blockIdx.x. Columns >= N are zero
       // (the padding up to a whole block).
       const int n = nt * 16 + l16;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < MTX; ++i) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 16 * i + 4 * g + e;
@@ -527,21 +557,25 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
         }
       }
       __syncthreads();
-      const int r = tid >> 4, q = tid & 15;  // 32 groups of 16 lanes: one row each
-      float v[8];
-      {
-        const u32x4v w = lds_ld128(abuf + (uint32_t)r * 256u + (uint32_t)q * 16u);
+      const int q = tid & 15;  // 32 groups of 16 lanes: rows tid / 16 + 32 k
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          v[2 * k] = h2f((uint16_t)(w[k] & 0xffff));
-          v[2 * k + 1] = h2f((uint16_t)(w[k] >> 16));
+      for (int k = 0; k < SR; ++k) {
+        const int r = (tid >> 4) + 32 * k;
+        float v[8];
+        {
+          const u32x4v w = lds_ld128(abuf + (uint32_t)r * 256u + (uint32_t)q * 16u);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            v[2 * c] = h2f((uint16_t)(w[c] & 0xffff));
+            v[2 * c + 1] = h2f((uint16_t)(w[c] >> 16));
+          }
         }
+        fwht128_group16(v, q);
+        const int m = mbase + r;
+        const bool live = r < 16 * MT && m < M;
+        const int64_t prow = live ? (int64_t)(row0 + m) : 0;  // no address past the rows
+        store_pair_block(v, q, reinterpret_cast<uint32_t*>(a.y) + prow * (a.ldy / 2) + (int64_t)blockIdx.x * 64, live);
       }
-      fwht128_group16(v, q);
-      const int m = mbase + r;
-      const bool live = r < 16 * MT && m < M;
-      const int64_t prow = live ? (int64_t)(row0 + m) : 0;  // no address past the rows
-      store_pair_block(v, q, reinterpret_cast<uint32_t*>(a.y) + prow * (a.ldy / 2) + (int64_t)blockIdx.x * 64, live);
     } else {
     // epilogue from registers: D element (lane, e) of m-tile i is row
     // 16 i + 4 (lane / 16) + e, column moe_tile_row + lane % 16
@@ -550,7 +584,7 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
       const int n = moe_tile_row<SWI, NT>(blockIdx.x, wave, j) + l16;
       if (n < a.N) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < MTX; ++i) {
           if (i >= MT) continue;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -574,13 +608,13 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
   }
 }
 
-template <bool NIB, int EP>
+template <bool NIB, int EP, int MR>
 static int launch_moe_t(const SmallArgs& a, int groups, hipStream_t st) {
   constexpr int D = 2;  // 2 blocks in flight per wave: measured faster than 3 or 4
-  auto kern = moe_gemv_kernel<NIB, EP, D>;
+  auto kern = moe_gemv_kernel<NIB, EP, D, MR>;
   const int entries = table_entries(NIB, a.n_levels);
   const uint32_t abuf = (uint32_t)round_up((size_t)entries * 256, 256);
-  const size_t lds = abuf + 2 * (size_t)kMoeRows * 256;
+  const size_t lds = abuf + 2 * (size_t)MR * 256;
   if (lds > 160 * 1024) return PE_ERR_DIMS;
   static const bool attr_ok = [&] {
     return hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -595,17 +629,26 @@ static int launch_moe_t(const SmallArgs& a, int groups, hipStream_t st) {
   return launch_status();
 }
 
+// Rows per pass: 64 when the experts hold at least 64 rows on average (a.M:
+// the pairs over all experts), else 32 (two workgroups per CU).
+template <bool NIB, int EP>
+static int launch_moe_mr(const SmallArgs& a, int groups, hipStream_t st) {
+  if ((int64_t)a.M >= (int64_t)kMoeRowsWide * groups)
+    return launch_moe_t<NIB, EP, kMoeRowsWide>(a, groups, st);
+  return launch_moe_t<NIB, EP, kMoeRows>(a, groups, st);
+}
+
 int moe_grouped(bool nibble, int epilogue, const SmallArgs& a, int groups, hipStream_t st) {
   if (!a.group_off || a.nb <= 0 || a.N <= 0) return PE_ERR_DIMS;
   // one expert's codes and norms are addressed by 32-bit buffer offsets
   if (a.codes_stride >= ((int64_t)1 << 31) || a.norms_stride * 2 >= ((int64_t)1 << 31))
     return PE_ERR_DIMS;
   switch (epilogue) {
-    case SE_F32: return nibble ? launch_moe_t<true, SE_F32>(a, groups, st) : launch_moe_t<false, SE_F32>(a, groups, st);
-    case SE_SWIGLU: return nibble ? launch_moe_t<true, SE_SWIGLU>(a, groups, st) : launch_moe_t<false, SE_SWIGLU>(a, groups, st);
+    case SE_F32: return nibble ? launch_moe_mr<true, SE_F32>(a, groups, st) : launch_moe_mr<false, SE_F32>(a, groups, st);
+    case SE_SWIGLU: return nibble ? launch_moe_mr<true, SE_SWIGLU>(a, groups, st) : launch_moe_mr<false, SE_SWIGLU>(a, groups, st);
     case SE_SWIGLU_XTF:
       if (a.ldy % 128) return PE_ERR_DIMS;  // rows of whole 128-blocks
-      return nibble ? launch_moe_t<true, SE_SWIGLU_XTF>(a, groups, st) : launch_moe_t<false, SE_SWIGLU_XTF>(a, groups, st);
+      return nibble ? launch_moe_mr<true, SE_SWIGLU_XTF>(a, groups, st) : launch_moe_mr<false, SE_SWIGLU_XTF>(a, groups, st);
     default: return PE_ERR_DTYPE;
   }
 }

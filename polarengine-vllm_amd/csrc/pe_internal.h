@@ -86,7 +86,7 @@ struct SmallArgs {
   void* y;
   int64_t ldy;
   const uint16_t* bias;
-  int M;                     // rows (small-M matmul)
+  int M;                     // rows (small-M matmul); MoE: all pairs over the experts
   int N;                     // output columns (SwiGLU: I; the weights hold 2I rows)
   int nb;
   WLayout lay;               // per-expert layout (row-major for the MoE path)

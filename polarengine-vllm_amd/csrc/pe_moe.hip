@@ -525,15 +525,15 @@ static int moe_run(const void* x, int x_dtype, int64_t T, int H, int I, int E, i
   {
     SmallArgs a{reinterpret_cast<const uint8_t*>(W.w13_codes), W.w13_norms, W.ct13, W.n_levels13,
                 reinterpret_cast<const uint32_t*>(ws + L.xtf), sorted_token, offsets,
-                2 * (int64_t)I * row13, 2 * (int64_t)I * nb13, ws + L.htf, Ip, nullptr, 0, I,
-                nb13, wlayout(nib13, tiled13, nb13)};
+                2 * (int64_t)I * row13, 2 * (int64_t)I * nb13, ws + L.htf, Ip, nullptr, (int)P, I,
+                nb13, wlayout(nib13, tiled13, nb13)};  // M: all pairs (rows per pass)
     if (int rc = moe_grouped(nib13, SE_SWIGLU_XTF, a, E, st)) return rc;
   }
   // 3. down -> y2 [P, H] fp32
   {
     SmallArgs a{reinterpret_cast<const uint8_t*>(W.w2_codes), W.w2_norms, W.ct2, W.n_levels2,
                 reinterpret_cast<const uint32_t*>(ws + L.htf), nullptr, offsets,
-                (int64_t)H * row2, (int64_t)H * nb2, ws + L.y2, H, nullptr, 0, H, nb2,
+                (int64_t)H * row2, (int64_t)H * nb2, ws + L.y2, H, nullptr, (int)P, H, nb2,
                 wlayout(nib2, tiled2, nb2)};
     if (int rc = moe_grouped(nib2, SE_F32, a, E, st)) return rc;
   }

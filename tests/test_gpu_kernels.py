@@ -729,6 +729,10 @@ def _moe_layer(rng, e, hdim, inter, b13, b2, tile=True):
     (80, 4, 256, 256, 2, 4, 5),       # ~40 tokens per expert: several passes
     (3, 16, 512, 384, 1, 5, 6),       # most experts empty; int8 experts
     (40, 4, 384, 132, 3, 4, 3),       # 2I = 264 rows: w13 stays row-major
+    # at least 64 rows per expert on average: 64-row passes (four m-tiles)
+    (256, 4, 256, 256, 2, 3, 4),      # ~128 rows per expert, ragged
+    (300, 8, 384, 200, 3, 4, 6),      # I not a multiple of 128, int8 w2
+    (200, 2, 256, 384, 1, 5, 4),      # int8 w13, ~100 rows per expert
 ])
 def test_moe_forward_matches_oracle(t, e, hdim, inter, k, b13, b2, tile):
     _say(f"moe forward t={t} e={e} h={hdim} i={inter} k={k} q{b13}/q{b2} tile={tile}")
