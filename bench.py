@@ -168,8 +168,9 @@ def kv_extra(dev, n_vec=1 << 21, d=128, bits=3):
 def moe_extra(dev, t=128, e=64, h=2048, inter=1408, k=8, b13=3, b2=4):
     """Grouped quantized experts (routing, SwiGLU w13, w2, weighted combine)
     through PolarQuantMoEMethod.apply: 64 experts, top-8, H=2048, I=1408,
-    w13 Q3 and w2 Q4 nibbles, 128 tokens (1024 token-expert pairs). The
-    stored expert bytes over the call time, as HBM GB/s."""
+    w13 Q3 and w2 Q4 nibbles, 128 tokens (1024 token-expert pairs; C5) or
+    `t` tokens. The stored expert bytes over the call time, as HBM GB/s, and
+    the expert FLOPs over the call time."""
     from polarengine_vllm.moe_method import PolarQuantMoEMethod
     meth = PolarQuantMoEMethod(128, b13, b2)
     g = torch.Generator(device=dev).manual_seed(11)
@@ -194,9 +195,10 @@ def moe_extra(dev, t=128, e=64, h=2048, inter=1408, k=8, b13=3, b2=4):
     # gate the ~60 us call
     calls = [lambda ly=ly: meth.apply(ly, x, logits, k, True) for ly in layers]
     tm, _ = time_graph(calls, 4, 16, 64, dev)
-    return {"moe_t128_e64_top8": {"us_per_call": round(tm * 1e6, 1),
+    return {f"moe_t{t}_e{e}_top{k}": {"us_per_call": round(tm * 1e6, 1),
                                   "GB/s": round(wbytes * active / e / tm / 1e9, 1),
                                   "hbm_frac": round(wbytes * active / e / tm / 1e9 / HBM_PEAK_GBS, 4),
+                                  "TFLOP/s": round(2.0 * t * k * 3 * h * inter / tm / 1e12, 1),
                                   "expert_bytes": wbytes, "active_experts": active,
                                   "includes": "routing + x FWHT with expert bucketing + w13 SwiGLU (FWHT of h fused) + w2 + combine"}}
 
@@ -617,6 +619,8 @@ def main():
                              "note": "one weight copy, Infinity-Cache resident"}
     extra.update(kv_extra(dev))
     extra.update(moe_extra(dev))
+    # the same experts in the prefill regime (about 256 rows per expert)
+    extra.update(moe_extra(dev, t=2048))
     extra.update(e2e_extra(dev))
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
