@@ -365,7 +365,9 @@ def test_tile_weights_bit_exact(n, k, bits):
 TILED_CASES = [(1, 12288, 4096, 4), (1, 4096, 12288, 3), (1, 1000, 1408, 5), (4, 257, 384, 2),
                (16, 4096, 2048, 4), (16, 4096, 4096, 4), (33, 1000, 1408, 6), (256, 1536, 1024, 4),
                (300, 200, 640, 8), (1, 48, 256, 6), (24, 4096, 12288, 3), (32, 12288, 4096, 4),
-               (64, 12288, 4096, 4), (20, 1000, 1408, 5)]
+               (64, 12288, 4096, 4), (20, 1000, 1408, 5),
+               # M = 33..64 on the four-wave 64-row K split with int8 codes
+               (64, 6144, 4096, 5), (40, 4096, 4096, 6)]
 
 
 @pytest.mark.parametrize("m,n,k,bits", TILED_CASES)
