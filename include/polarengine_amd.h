@@ -94,6 +94,19 @@ int pe_fwht128(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t l
                void* y, int y_layout, void* stream);
 
 /*
+ * Normalised Walsh-Hadamard transform over the WHOLE last dimension of each
+ * row, n a power of two (1 <= n <= 32768): stages h = 1, 2, 4, ..., n/2 pair
+ * (a, b) -> (a + b, a - b), then y = result / sqrt(n). fp32 arithmetic, one
+ * rounding to y_dtype. Replaces fwht_butterfly (kernels/fwht.py:160-190) and
+ * the CUDA fwht_butterfly_kernel (kernels/cuda/fwht_cuda.cu:35-86). x has
+ * x_dtype (PE_DTYPE_F16/BF16/F32) and row stride ldx >= n (elements); y is
+ * [rows, n] of y_dtype, contiguous. x == y is allowed when ldx == n and the
+ * dtypes match. PE_ERR_DIMS for n not a power of two or above 32768.
+ */
+int pe_fwht_pow2(const void* x, int x_dtype, int64_t rows, int64_t n, int64_t ldx,
+                 void* y, int y_dtype, void* stream);
+
+/*
  * Reference native GEMV on int8 codes (bits 5..8, or unpacked 2..4):
  * out[n] = sum_b norms[n,b] * sum_k ct_scaled[codes[n,128b+k]] * x_tf[128b+k].
  * Replaces polar_gemv (kernels/polar_gemv.py:181-216; pybind

@@ -44,4 +44,4 @@ extern "C" const char* pe_status_string(int status) {
   }
 }
 
-extern "C" int pe_abi_version(void) { return 3; }
+extern "C" int pe_abi_version(void) { return 4; }

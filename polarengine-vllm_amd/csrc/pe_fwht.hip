@@ -8,6 +8,8 @@
 // 16/32-byte store per lane. HBM-bound: 2*2 bytes per element for f16 in and
 // pair-f16 out.
 
+#include <cmath>
+
 #include "pe_internal.h"
 
 namespace pe {
@@ -100,9 +102,90 @@ int repack_pair(const float* x, int64_t rows, int64_t cols, void* y, hipStream_t
   return launch_status();
 }
 
+// ---------------------------------------------------------------------------
+// Whole-row FWHT of any power-of-two length n <= 2^15: the reference's
+// fwht_butterfly (kernels/fwht.py:160-190), stages h = 1, 2, 4, ..., n/2
+// pairing (a, b) -> (a + b, a - b) over the whole last dimension, then a
+// division by sqrt(n). The rows of one workgroup sit in LDS as fp32 (n or, for
+// short rows, 2048 elements: several rows), every stage is one pass of the
+// 256 lanes over the pairs, and the result is rounded once to the output type.
+// ---------------------------------------------------------------------------
+constexpr int kPow2MaxLog = 15;
+constexpr int kPow2WgElems = 2048;  // elements per workgroup for rows shorter than this
+
+__device__ __forceinline__ float load_elem(const void* p, int64_t i, int dt) {
+  if (dt == PE_DTYPE_F32) return reinterpret_cast<const float*>(p)[i];
+  const uint16_t b = reinterpret_cast<const uint16_t*>(p)[i];
+  return dt == PE_DTYPE_BF16 ? bf2f(b) : h2f(b);
+}
+
+__global__ __launch_bounds__(256) void fwht_pow2_kernel(const void* x, int xdt, void* y, int ydt,
+                                                        int64_t rows, int logn, int64_t ldx,
+                                                        float sqrt_n) {
+  extern __shared__ float s[];
+  const int n = 1 << logn;
+  const int rpw = n >= kPow2WgElems ? 1 : kPow2WgElems >> logn;  // rows per workgroup
+  const int64_t r0 = (int64_t)blockIdx.x * rpw;
+  const int nr = (int)(rows - r0 < rpw ? rows - r0 : rpw);
+  const int elems = nr << logn;
+  for (int i = threadIdx.x; i < elems; i += blockDim.x) {
+    const int rr = i >> logn, c = i & (n - 1);
+    s[i] = load_elem(x, (r0 + rr) * ldx + c, xdt);
+  }
+  __syncthreads();
+  for (int lh = 0; lh < logn; ++lh) {
+    const int h = 1 << lh;
+    for (int p = threadIdx.x; p < (elems >> 1); p += blockDim.x) {
+      const int i = ((p >> lh) << (lh + 1)) | (p & (h - 1));
+      const float a = s[i], b = s[i + h];
+      s[i] = a + b;
+      s[i + h] = a - b;
+    }
+    __syncthreads();
+  }
+  const int64_t base = r0 << logn;  // output rows are contiguous
+  for (int i = threadIdx.x; i < elems; i += blockDim.x) {
+    const float v = s[i] / sqrt_n;
+    if (ydt == PE_DTYPE_F32) reinterpret_cast<float*>(y)[base + i] = v;
+    else if (ydt == PE_DTYPE_BF16) reinterpret_cast<uint16_t*>(y)[base + i] = f2bf_bits(v);
+    else reinterpret_cast<uint16_t*>(y)[base + i] = f2h_bits(v);
+  }
+}
+
+int fwht_pow2(const void* x, int x_dtype, int64_t rows, int64_t n, int64_t ldx, void* y,
+              int y_dtype, hipStream_t st) {
+  if (!x || !y) return PE_ERR_NULL;
+  if (x_dtype < PE_DTYPE_F16 || x_dtype > PE_DTYPE_F32 || y_dtype < PE_DTYPE_F16 ||
+      y_dtype > PE_DTYPE_F32)
+    return PE_ERR_DTYPE;
+  if (rows < 0 || n < 1 || (n & (n - 1)) || n > (int64_t(1) << kPow2MaxLog) || ldx < n)
+    return PE_ERR_DIMS;
+  if (rows == 0) return PE_OK;
+  int logn = 0;
+  while ((int64_t(1) << logn) < n) ++logn;
+  const int rpw = n >= kPow2WgElems ? 1 : kPow2WgElems >> logn;
+  const int64_t grid = (rows + rpw - 1) / rpw;
+  if (grid > INT32_MAX) return PE_ERR_DIMS;
+  const size_t lds = (size_t)(n >= kPow2WgElems ? n : kPow2WgElems) * sizeof(float);
+  static const bool attr_ok = [] {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(fwht_pow2_kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+  }();
+  (void)attr_ok;
+  const float sqrt_n = (float)std::sqrt((double)n);
+  fwht_pow2_kernel<<<dim3((unsigned)grid), dim3(256), lds, st>>>(x, x_dtype, y, y_dtype, rows, logn,
+                                                                 ldx, sqrt_n);
+  return launch_status();
+}
+
 }  // namespace pe
 
 extern "C" int pe_fwht128(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t ldx,
                           void* y, int y_layout, void* stream) {
   return pe::fwht128(x, x_dtype, rows, cols, ldx, y, y_layout, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int pe_fwht_pow2(const void* x, int x_dtype, int64_t rows, int64_t n, int64_t ldx,
+                            void* y, int y_dtype, void* stream) {
+  return pe::fwht_pow2(x, x_dtype, rows, n, ldx, y, y_dtype, reinterpret_cast<hipStream_t>(stream));
 }

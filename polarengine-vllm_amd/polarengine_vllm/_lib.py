@@ -35,6 +35,7 @@ _SIGNATURES = {
     "pe_status_string": (ctypes.c_char_p, [_c_int]),
     "pe_abi_version": (_c_int, []),
     "pe_fwht128": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_int, _vp]),
+    "pe_fwht_pow2": (_c_int, [_vp, _c_int, _c_i64, _c_i64, _c_i64, _vp, _c_int, _vp]),
     "pe_polar_gemv": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
     "pe_polar_gemv_packed": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
     "pe_polar_matmul_workspace_size": (_c_sz, [_c_i64, _c_int]),
@@ -139,17 +140,35 @@ def act_dtype(t: torch.Tensor) -> int:
 
 
 _WS_CACHE: dict = {}
+# Every buffer workspace() ever handed out, per key. A superseded buffer is
+# never released: kernels receive workspaces as raw pointers, so a HIP graph
+# captured before a growth keeps writing the old address on every replay, and
+# its completion counters (which must stay zero between calls) must not be
+# memory that the caching allocator has handed to someone else.
+_WS_RETIRED: dict = {}
+
+
+def _ws_key(device: torch.device):
+    if device.type != "cuda":
+        return (device, 0)
+    return (device, torch.cuda.current_stream(device).cuda_stream)
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """Per-device, per-stream growable workspace (uint8), reused across calls.
     Zero-filled when allocated: the library keeps completion counters in its
-    first 4 KB, which must start at zero and which every call leaves zero."""
+    first 4 KB, which must start at zero and which every call leaves zero.
+    Growth allocates a larger buffer and keeps the old one alive for the life
+    of the process (see _WS_RETIRED)."""
     if nbytes <= 0:
         return None
-    key = (device, torch.cuda.current_stream(device).cuda_stream)
+    key = _ws_key(device)
     buf = _WS_CACHE.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        if buf is not None:
+            _WS_RETIRED.setdefault(key, []).append(buf)
+        # geometric growth: the retired buffers never add up to more than the live one
+        size = max(nbytes, 1 << 20, 2 * buf.numel() if buf is not None else 0)
+        buf = torch.zeros(size, dtype=torch.uint8, device=device)
         _WS_CACHE[key] = buf
     return buf

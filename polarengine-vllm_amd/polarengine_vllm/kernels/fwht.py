@@ -3,12 +3,15 @@
 ``fwht_matmul`` keeps the reference's name and contract (each contiguous
 ``block_size`` block of the last dimension multiplied by the normalised
 Hadamard matrix) but runs the gfx950 butterfly kernel ``pe_fwht128`` instead
-of an fp32 GEMM against H. GPU tensors only; block_size 128.
+of an fp32 GEMM against H; block_size 128. ``fwht_butterfly`` transforms the
+whole last dimension (any power of two up to 32768) with ``pe_fwht_pow2``.
+GPU tensors only.
 """
 
 from __future__ import annotations
 
 import math
+import weakref
 from typing import Optional
 
 import torch
@@ -88,47 +91,110 @@ def fwht_pairs(x: torch.Tensor, block_size: int = 128) -> torch.Tensor:
     return out
 
 
+def fwht_butterfly(x: torch.Tensor) -> torch.Tensor:
+    """Normalised Walsh-Hadamard transform over the whole last dimension.
+
+    Reference: kernels/fwht.py:160-190 (``fwht_butterfly``): stages
+    h = 1, 2, 4, ..., n/2 pair (a, b) -> (a + b, a - b), then divide by
+    sqrt(n); the last dimension must be a power of two (AssertionError
+    otherwise). Runs ``pe_fwht_pow2`` (n <= 32768): fp32 arithmetic, one
+    rounding to x's dtype. Unlike the reference, which butterflies in x's own
+    precision and leaves x overwritten with the unnormalised stages, x is not
+    modified. GPU tensors only.
+    """
+    n = x.shape[-1]
+    assert n >= 1 and (n & (n - 1)) == 0, f"last dim must be power of 2, got {n}"
+    dev = _lib.require_device(x)
+    dt = {torch.float16: _lib.PE_DTYPE_F16, torch.bfloat16: _lib.PE_DTYPE_BF16,
+          torch.float32: _lib.PE_DTYPE_F32}.get(x.dtype)
+    if dt is None:
+        raise TypeError(f"unsupported dtype {x.dtype}")
+    xc = x.contiguous()
+    out = torch.empty_like(xc)
+    rows = xc.numel() // n
+    if rows:
+        _lib.check(_lib.lib().pe_fwht_pow2(xc.data_ptr(), dt, rows, n, n, out.data_ptr(), dt,
+                                           _lib.stream_ptr(dev)), "pe_fwht_pow2")
+    return out.view(x.shape)
+
+
 class FWHTCache:
     """Single-entry cache of an FWHT result, shared by Q/K/V projections.
 
     Same interface as the reference (kernels/fwht.py:115-153): ``get``
     returns the cached transform when ``x`` is the tensor that was ``put``,
-    ``clear`` empties it. The entry keeps a reference to ``x`` and records
-    its version counter and geometry, so a different tensor that later
-    reuses the same storage address, or an in-place update of ``x`` through
-    torch, misses instead of returning a stale transform.
+    ``clear`` empties it.
+
+    The entry is keyed on the tensor object itself (held weakly: the entry,
+    and with it the transform, is dropped as soon as ``x`` is freed), its
+    geometry and, for tensors that track versions, its version counter, so an
+    in-place update of ``x`` through torch misses instead of returning a stale
+    transform.
+
+    Inference tensors (``torch.inference_mode()``, which vLLM runs every
+    forward under) track no version. For them the cache holds an entry only
+    inside a *scope*: ``install_fwht_cache_hooks`` (linear_method) opens one
+    around every forward of a module that owns PolarQuant linears and clears
+    the cache on entry and exit, so an entry only ever serves sibling
+    projections inside one parent forward. Outside a scope an inference
+    tensor is never cached (each projection transforms its own input), since
+    a hidden-state tensor that is updated in place between layers would
+    otherwise be served the previous layer's transform.
 
     A write that bypasses torch (a kernel handed ``x.data_ptr()``) does not
-    bump the version. This package's own wrappers record such writes into
-    caller tensors (``increment_version``); for anything else the cache must
-    be scoped: ``install_fwht_cache_hooks`` (linear_method) clears it at the
-    start of every forward of a module that owns PolarQuant linears, so an
-    entry only ever serves sibling projections inside one parent forward.
+    bump the version either. This package's own wrappers record such writes
+    into caller tensors (``increment_version``); anything else must use the
+    scope hooks.
     """
 
     def __init__(self):
-        self._x: Optional[torch.Tensor] = None
+        self._ref = None
         self._key = None
         self._result: Optional[torch.Tensor] = None
+        self._scope = 0
 
     @staticmethod
     def _make_key(x: torch.Tensor, in_f: int):
-        return (x.data_ptr(), in_f, tuple(x.shape), tuple(x.stride()), x.dtype, x._version)
+        ver = None if x.is_inference() else x._version
+        return (x.data_ptr(), in_f, tuple(x.shape), tuple(x.stride()), x.dtype, ver)
+
+    def _cacheable(self, x: torch.Tensor) -> bool:
+        return self._scope > 0 or not x.is_inference()
 
     def get(self, x: torch.Tensor, in_f: int) -> Optional[torch.Tensor]:
-        if self._x is not None and self._key == self._make_key(x, in_f):
-            return self._result
-        return None
+        if self._ref is None or self._ref() is not x or not self._cacheable(x):
+            return None
+        if self._key != self._make_key(x, in_f):
+            return None
+        return self._result
 
     def put(self, x: torch.Tensor, in_f: int, result: torch.Tensor) -> None:
-        self._x = x
+        if not self._cacheable(x):
+            self.clear()
+            return
+        self.clear()
+        self._ref = weakref.ref(x, self._on_free)
         self._key = self._make_key(x, in_f)
         self._result = result
 
+    def _on_free(self, ref) -> None:
+        if self._ref is ref:
+            self.clear()
+
     def clear(self) -> None:
-        self._x = None
+        self._ref = None
         self._key = None
         self._result = None
+
+    def enter_scope(self) -> None:
+        """Start a parent module's forward: empty, and serve inference tensors."""
+        self.clear()
+        self._scope += 1
+
+    def exit_scope(self) -> None:
+        """End a parent module's forward: empty, and drop the transform."""
+        self.clear()
+        self._scope = max(0, self._scope - 1)
 
 
 # Process-wide cache used by the linear method, so separate q/k/v (or

@@ -85,7 +85,9 @@ def patch_model_attention(model: torch.nn.Module, config: PolarKVConfig) -> Pola
     ``past_key_values``, where ``PolarKVAttentionWrapper`` itself serves)
     has its attention blocks, the modules owning a q_proj or qkv_proj, tagged
     with ``_polar_kv_layer_idx`` / ``_polar_kv_cache`` in the same order, as
-    the reference's hook does (kv_cache/attention.py:128-155)."""
+    the reference's hook does (kv_cache/attention.py:128-155). Patching a
+    model again re-points every backend at the new cache (its original
+    forward is kept, so wrappers never stack)."""
     cache = PolarKVCache(config)
     wrapper = PolarKVAttentionWrapper(cache)
     backends = [m for m in model.modules() if _backend_forward(m)]
@@ -93,7 +95,11 @@ def patch_model_attention(model: torch.nn.Module, config: PolarKVConfig) -> Pola
                            if hasattr(m, "q_proj") or hasattr(m, "qkv_proj")]
     for idx, module in enumerate(targets[:config.num_layers]):
         if backends:
-            module.forward = wrapper.wrap_attention_forward(module.forward, idx)
+            # a backend patched before is re-pointed at the new cache: its
+            # original forward is wrapped again, never the earlier wrapper
+            orig = getattr(module, "_polar_kv_orig_forward", None) or module.forward
+            module._polar_kv_orig_forward = orig
+            module.forward = wrapper.wrap_attention_forward(orig, idx)
         module._polar_kv_layer_idx = idx
         module._polar_kv_cache = cache
     return cache

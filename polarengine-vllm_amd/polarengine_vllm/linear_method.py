@@ -26,7 +26,7 @@ from __future__ import annotations
 
 import logging
 import math
-from typing import Any, Dict, Optional
+from typing import Any, Dict, List, Optional
 
 import numpy as np
 import torch
@@ -103,6 +103,7 @@ class PolarQuantLinearMethod:
         layer.ct_scaled = layer.ct_scaled.to(device=device, dtype=torch.float32).contiguous()
         # host copy of the codebook: the decode kernel takes it by value
         layer.ct_host = np.ascontiguousarray(layer.ct_scaled.cpu().numpy(), dtype=np.float32)
+        layer.ct_host_list = [float(v) for v in layer.ct_host]  # the same, for the custom op
         if layer.norms.dtype != torch.float16:
             layer.norms = layer.norms.to(torch.float16)
         layer.norms = layer.norms.contiguous()
@@ -130,56 +131,97 @@ class PolarQuantLinearMethod:
         fp16 and bf16 activations give a result of the same dtype; any other
         float dtype is transformed from its own precision and gives fp16, the
         reference's output dtype (linear_method.py:184-221 casts x.float()
-        and returns .half())."""
-        orig_shape = x.shape
+        and returns .half()). Under torch.compile the call is the custom op
+        ``polarengine::linear_apply`` (same kernels, no FWHT cache), so a
+        compiled model forward traces through it."""
         packed = bool(getattr(layer, "packed", False))
         codes = layer.codes_packed if packed else layer.codes
-        dev = _lib.require_device(x, codes)
-        if not x.is_floating_point():
-            raise TypeError(f"PolarEngine linear takes floating-point activations, got {x.dtype}")
-        out_dtype = x.dtype if x.dtype in (torch.float16, torch.bfloat16) else torch.float16
-        x2 = x.reshape(-1, layer.in_f)
-        m = x2.shape[0]
-        y = torch.empty(m, layer.out_f, dtype=out_dtype, device=dev)
-        if m == 0:
-            return y.view(*orig_shape[:-1], layer.out_f)
-        b = None
-        if bias is not None:
-            b = bias.to(device=dev, dtype=out_dtype).contiguous()
-        L = _lib.lib()
-        st = _lib.stream_ptr(dev)
-        n_levels = layer.ct_scaled.numel()
-        kp = layer.in_f_padded
-        ct_host = getattr(layer, "ct_host", None)
-        ct_host = None if ct_host is None else ct_host.ctypes.data
         fmt = (_lib.PE_PACK_NIBBLE if packed else 0) | (
             _lib.PE_LAYOUT_TILE16 if getattr(layer, "tiled", False) else 0)
-        out_code = _lib.act_dtype(y)
+        if torch.compiler.is_compiling():
+            ct_list = getattr(layer, "ct_host_list", None) or []
+            return torch.ops.polarengine.linear_apply(
+                x, codes, layer.norms, layer.ct_scaled, bias, layer.bits, fmt, layer.in_f,
+                layer.in_f_padded, layer.out_f, ct_list)
+        ct_host = getattr(layer, "ct_host", None)
+        return _linear_forward(x, codes, layer.norms, layer.ct_scaled, ct_host, bias, layer.bits,
+                               fmt, layer.in_f, layer.in_f_padded, layer.out_f, self._fwht_cache)
 
-        if m > _FUSED_FWHT_MAX_M or x.dtype != out_dtype:
-            x_tf = self._fwht_cache.get(x, layer.in_f)
-            if x_tf is None:
-                xp = x2 if kp == layer.in_f else F.pad(x2, (0, kp - layer.in_f))
-                x_tf = fwht_pairs(xp)
-                self._fwht_cache.put(x, layer.in_f, x_tf)
-            ws_bytes = L.pe_linear_xtf_workspace_size(m, kp, layer.out_f, layer.bits, fmt)
-            ws = _lib.workspace(dev, ws_bytes)
-            rc = L.pe_linear_forward_xtf(
-                x_tf.data_ptr(), m, kp, codes.data_ptr(), layer.bits, fmt,
-                layer.norms.data_ptr(), layer.ct_scaled.data_ptr(), ct_host, n_levels, _lib.ptr(b),
-                out_code, y.data_ptr(), layer.out_f, _lib.ptr(ws), ws_bytes, st)
-            _lib.check(rc, "pe_linear_forward_xtf")
-        else:
-            xc = x2 if kp == layer.in_f else F.pad(x2, (0, kp - layer.in_f))
-            xc = xc.contiguous()
-            ws_bytes = L.pe_linear_workspace_size(m, kp, layer.out_f, layer.bits, fmt)
-            ws = _lib.workspace(dev, ws_bytes)
-            rc = L.pe_linear_forward(
-                xc.data_ptr(), out_code, m, kp, kp, codes.data_ptr(), layer.bits,
-                fmt, layer.norms.data_ptr(), layer.ct_scaled.data_ptr(), ct_host, n_levels,
-                _lib.ptr(b), y.data_ptr(), layer.out_f, _lib.ptr(ws), ws_bytes, st)
-            _lib.check(rc, "pe_linear_forward")
-        return y.view(*orig_shape[:-1], layer.out_f)
+
+def _linear_forward(x: torch.Tensor, codes: torch.Tensor, norms: torch.Tensor,
+                    ct_scaled: torch.Tensor, ct_host: Optional[np.ndarray],
+                    bias: Optional[torch.Tensor], bits: int, fmt: int, in_f: int, kp: int,
+                    out_f: int, cache: Optional[FWHTCache]) -> torch.Tensor:
+    """The forward of PolarQuantLinearMethod.apply on explicit buffers:
+
+    * M <= 32 with a 16-bit x: ``pe_linear_forward`` (FWHT fused into the
+      decode GEMV);
+    * otherwise ``fwht_pairs`` (through ``cache`` when given) and
+      ``pe_linear_forward_xtf``."""
+    orig_shape = x.shape
+    dev = _lib.require_device(x, codes)
+    if not x.is_floating_point():
+        raise TypeError(f"PolarEngine linear takes floating-point activations, got {x.dtype}")
+    out_dtype = x.dtype if x.dtype in (torch.float16, torch.bfloat16) else torch.float16
+    x2 = x.reshape(-1, in_f)
+    m = x2.shape[0]
+    y = torch.empty(m, out_f, dtype=out_dtype, device=dev)
+    if m == 0:
+        return y.view(*orig_shape[:-1], out_f)
+    b = None
+    if bias is not None:
+        b = bias.to(device=dev, dtype=out_dtype).contiguous()
+    L = _lib.lib()
+    st = _lib.stream_ptr(dev)
+    n_levels = ct_scaled.numel()
+    ct_ptr = None if ct_host is None else ct_host.ctypes.data
+    out_code = _lib.act_dtype(y)
+
+    if m > _FUSED_FWHT_MAX_M or x.dtype != out_dtype:
+        x_tf = cache.get(x, in_f) if cache is not None else None
+        if x_tf is None:
+            xp = x2 if kp == in_f else F.pad(x2, (0, kp - in_f))
+            x_tf = fwht_pairs(xp)
+            if cache is not None:
+                cache.put(x, in_f, x_tf)
+        ws_bytes = L.pe_linear_xtf_workspace_size(m, kp, out_f, bits, fmt)
+        ws = _lib.workspace(dev, ws_bytes)
+        rc = L.pe_linear_forward_xtf(
+            x_tf.data_ptr(), m, kp, codes.data_ptr(), bits, fmt, norms.data_ptr(),
+            ct_scaled.data_ptr(), ct_ptr, n_levels, _lib.ptr(b), out_code, y.data_ptr(), out_f,
+            _lib.ptr(ws), ws_bytes, st)
+        _lib.check(rc, "pe_linear_forward_xtf")
+    else:
+        xc = x2 if kp == in_f else F.pad(x2, (0, kp - in_f))
+        xc = xc.contiguous()
+        ws_bytes = L.pe_linear_workspace_size(m, kp, out_f, bits, fmt)
+        ws = _lib.workspace(dev, ws_bytes)
+        rc = L.pe_linear_forward(
+            xc.data_ptr(), out_code, m, kp, kp, codes.data_ptr(), bits, fmt, norms.data_ptr(),
+            ct_scaled.data_ptr(), ct_ptr, n_levels, _lib.ptr(b), y.data_ptr(), out_f,
+            _lib.ptr(ws), ws_bytes, st)
+        _lib.check(rc, "pe_linear_forward")
+    return y.view(*orig_shape[:-1], out_f)
+
+
+# The linear forward as a torch custom op, for traced / compiled models
+# (torch.compile cannot trace the raw-pointer ctypes call). The fake
+# implementation gives the output's shape and dtype.
+@torch.library.custom_op("polarengine::linear_apply", mutates_args=())
+def _linear_apply_op(x: torch.Tensor, codes: torch.Tensor, norms: torch.Tensor,
+                     ct_scaled: torch.Tensor, bias: Optional[torch.Tensor], bits: int, fmt: int,
+                     in_f: int, in_f_padded: int, out_f: int,
+                     ct_host: List[float]) -> torch.Tensor:
+    host = np.asarray(ct_host, dtype=np.float32) if ct_host else None
+    return _linear_forward(x, codes, norms, ct_scaled, host, bias, bits, fmt, in_f, in_f_padded,
+                           out_f, None)
+
+
+@_linear_apply_op.register_fake
+def _linear_apply_fake(x, codes, norms, ct_scaled, bias, bits, fmt, in_f, in_f_padded, out_f,
+                       ct_host):
+    out_dtype = x.dtype if x.dtype in (torch.float16, torch.bfloat16) else torch.float16
+    return x.new_empty((*x.shape[:-1], out_f), dtype=out_dtype)
 
 
 def create_fwht_clear_hook(linear_method: PolarQuantLinearMethod):
@@ -192,26 +234,35 @@ def create_fwht_clear_hook(linear_method: PolarQuantLinearMethod):
 
 
 def install_fwht_cache_hooks(model: torch.nn.Module, cache: Optional[FWHTCache] = None) -> int:
-    """Register the cache-clearing pre-hook on every module that has a
+    """Scope the FWHT cache to every forward of each module that has a
     PolarQuant linear as a direct child (e.g. a decoder layer's attention and
-    MLP blocks), and return how many were registered.
+    MLP blocks): a forward pre-hook empties the cache and opens a scope, a
+    forward hook (also run when the forward raises) empties it and closes the
+    scope. Returns how many modules were hooked.
 
     Sibling projections called inside one such forward (q/k/v on the same
-    hidden state, gate/up) still share one transform; a new forward of the
-    parent always starts empty, so a hidden-state buffer rewritten outside
-    torch between forwards can never be served a stale transform. The
-    reference defines the hook but registers it nowhere."""
+    hidden state, gate/up) share one transform, also for inference tensors,
+    which the cache serves only inside a scope; a new forward of the parent
+    always starts empty, so a hidden-state buffer rewritten outside torch
+    between forwards can never be served a stale transform, and the
+    transform is released when the parent's forward returns. The reference
+    defines the clearing hook (linear_method.py:265-288) but registers it
+    nowhere."""
     cache = GLOBAL_FWHT_CACHE if cache is None else cache
 
-    def hook(module: torch.nn.Module, args):
-        cache.clear()
+    def pre_hook(module: torch.nn.Module, args):
+        cache.enter_scope()
+
+    def post_hook(module: torch.nn.Module, args, output):
+        cache.exit_scope()
 
     n = 0
     for parent in model.modules():
         if any(isinstance(getattr(child, "quant_method", None), PolarQuantLinearMethod)
                for child in parent.children()):
             if not getattr(parent, "_polar_fwht_hook", False):
-                parent.register_forward_pre_hook(hook)
+                parent.register_forward_pre_hook(pre_hook)
+                parent.register_forward_hook(post_hook, always_call=True)
                 parent._polar_fwht_hook = True
                 n += 1
     return n

@@ -22,7 +22,7 @@ runtime layout (one 16-row x 128-block tile of codes is one contiguous read).
 from __future__ import annotations
 
 import math
-from typing import Optional
+from typing import List, Optional
 
 import torch
 
@@ -153,63 +153,110 @@ class PolarQuantMoEMethod:
               topk_group: Optional[int] = None, num_expert_group: Optional[int] = None,
               custom_routing_function=None, scoring_func: str = "softmax",
               e_score_correction_bias: Optional[torch.Tensor] = None, **kwargs) -> torch.Tensor:
-        """Routed quantized SwiGLU experts: [T, H] fp16 or bf16 -> [T, H] of the same dtype."""
-        dev = _lib.require_device(x, layer.w13_codes)
-        x_code = _lib.act_dtype(x)
-        xs = x.reshape(-1, layer.hidden_size).contiguous()
-        t = xs.shape[0]
-        out = torch.empty_like(xs)
-        L = _lib.lib()
-        e, h, i = layer.num_experts, layer.hidden_size, layer.intermediate_size
-        weights = (layer.w13_codes.data_ptr(), self.bits13,
-                   _layout(layer.w13_packed, layer.w13_tiled), layer.w13_norms.data_ptr(),
-                   layer.w13_ct_scaled.data_ptr(), 1 << self.bits13,
-                   layer.w2_codes.data_ptr(), self.bits2, _layout(layer.w2_packed, layer.w2_tiled),
-                   layer.w2_norms.data_ptr(), layer.w2_ct_scaled.data_ptr(), 1 << self.bits2)
+        """Routed quantized SwiGLU experts: [T, H] fp16 or bf16 -> [T, H] of the
+        same dtype. Under torch.compile the call is the custom op
+        ``polarengine::moe_routed`` (or ``polarengine::moe_given`` after a
+        custom routing function), so a compiled model forward traces through it."""
+        _lib.require_device(x, layer.w13_codes)
+        _lib.act_dtype(x)
+        e = layer.num_experts
+        wts = (layer.w13_codes, layer.w13_norms, layer.w13_ct_scaled, layer.w2_codes,
+               layer.w2_norms, layer.w2_ct_scaled)
+        meta = [self.bits13, _layout(layer.w13_packed, layer.w13_tiled), self.bits2,
+                _layout(layer.w2_packed, layer.w2_tiled), e, layer.hidden_size,
+                layer.intermediate_size]
+        compiling = torch.compiler.is_compiling()
         if custom_routing_function is None:
             # routing and experts in one call (the routing shares the first launch)
+            t = x.numel() // layer.hidden_size
             lg, bias, scoring, n_group, t_group = self._routing_args(
                 router_logits.reshape(t, -1), e, scoring_func, e_score_correction_bias,
                 use_grouped_topk, num_expert_group, topk_group)
-            if t == 0:
-                return out.view(x.shape)
-            wsb = L.pe_moe_workspace_size(t, top_k, e, h, i)
-            ws = _lib.workspace(dev, wsb)
-            rc = L.pe_moe_forward_routed(
-                xs.data_ptr(), x_code, t, h, i, e, top_k, lg.data_ptr(), int(bool(renormalize)),
-                scoring, _lib.ptr(bias), n_group, t_group, *weights, out.data_ptr(), _lib.ptr(ws),
-                wsb, _lib.stream_ptr(dev))
-            _lib.check(rc, "pe_moe_forward_routed")
-            return out.view(x.shape)
+            route = [top_k, int(bool(renormalize)), scoring, n_group, t_group]
+            if compiling:
+                return torch.ops.polarengine.moe_routed(x, lg, bias, *wts, route, meta)
+            return _moe_routed(x, lg, bias, *wts, route, meta)
+        xs = x.reshape(-1, layer.hidden_size)
         w, ids = custom_routing_function(hidden_states=xs, gating_output=router_logits,
                                          topk=top_k, renormalize=renormalize)
         w = w.to(torch.float32).contiguous()
         ids = ids.to(torch.int32).contiguous()
-        if t == 0:
-            return out.view(x.shape)
-        wsb = L.pe_moe_workspace_size(t, top_k, e, h, i)
-        ws = _lib.workspace(dev, wsb)
-        rc = L.pe_moe_forward(xs.data_ptr(), x_code, t, h, i, e, top_k, w.data_ptr(),
-                              ids.data_ptr(), *weights, out.data_ptr(), _lib.ptr(ws), wsb,
-                              _lib.stream_ptr(dev))
-        _lib.check(rc, "pe_moe_forward")
-        return out.view(x.shape)
-        L = _lib.lib()
-        e, h, i = layer.num_experts, layer.hidden_size, layer.intermediate_size
-        wsb = L.pe_moe_workspace_size(t, top_k, e, h, i)
-        ws = _lib.workspace(dev, wsb)
-        rc = L.pe_moe_forward(
-            xs.data_ptr(), x_code, t, h, i, e, top_k, w.data_ptr(), ids.data_ptr(),
-            layer.w13_codes.data_ptr(), self.bits13, _layout(layer.w13_packed, layer.w13_tiled),
-            layer.w13_norms.data_ptr(), layer.w13_ct_scaled.data_ptr(), 1 << self.bits13,
-            layer.w2_codes.data_ptr(), self.bits2, _layout(layer.w2_packed, layer.w2_tiled),
-            layer.w2_norms.data_ptr(), layer.w2_ct_scaled.data_ptr(), 1 << self.bits2,
-            out.data_ptr(), _lib.ptr(ws), wsb, _lib.stream_ptr(dev))
-        _lib.check(rc, "pe_moe_forward")
-        return out.view(x.shape)
+        if compiling:
+            return torch.ops.polarengine.moe_given(x, w, ids, *wts, meta)
+        return _moe_given(x, w, ids, *wts, meta)
 
     def get_fused_moe_quant_config(self):
         return None
+
+
+def _moe_weights(w13c, w13n, w13ct, w2c, w2n, w2ct, meta):
+    b13, lay13, b2, lay2 = meta[:4]
+    return (w13c.data_ptr(), b13, lay13, w13n.data_ptr(), w13ct.data_ptr(), 1 << b13,
+            w2c.data_ptr(), b2, lay2, w2n.data_ptr(), w2ct.data_ptr(), 1 << b2)
+
+
+def _moe_routed(x: torch.Tensor, lg: torch.Tensor, bias: Optional[torch.Tensor],
+                w13c: torch.Tensor, w13n: torch.Tensor, w13ct: torch.Tensor, w2c: torch.Tensor,
+                w2n: torch.Tensor, w2ct: torch.Tensor, route: List[int],
+                meta: List[int]) -> torch.Tensor:
+    """pe_moe_forward_routed: routing (route = top_k, renormalize, scoring,
+    n_group, topk_group) and the experts (meta = bits13, layout13, bits2,
+    layout2, E, H, I) in one call."""
+    dev = x.device
+    e, h, i = meta[4:]
+    top_k, renorm, scoring, n_group, t_group = route
+    xs = x.reshape(-1, h).contiguous()
+    t = xs.shape[0]
+    out = torch.empty_like(xs)
+    if t == 0:
+        return out.view(x.shape)
+    L = _lib.lib()
+    wsb = L.pe_moe_workspace_size(t, top_k, e, h, i)
+    ws = _lib.workspace(dev, wsb)
+    rc = L.pe_moe_forward_routed(
+        xs.data_ptr(), _lib.act_dtype(xs), t, h, i, e, top_k, lg.data_ptr(), renorm, scoring,
+        _lib.ptr(bias), n_group, t_group, *_moe_weights(w13c, w13n, w13ct, w2c, w2n, w2ct, meta),
+        out.data_ptr(), _lib.ptr(ws), wsb, _lib.stream_ptr(dev))
+    _lib.check(rc, "pe_moe_forward_routed")
+    return out.view(x.shape)
+
+
+def _moe_given(x: torch.Tensor, w: torch.Tensor, ids: torch.Tensor, w13c: torch.Tensor,
+               w13n: torch.Tensor, w13ct: torch.Tensor, w2c: torch.Tensor, w2n: torch.Tensor,
+               w2ct: torch.Tensor, meta: List[int]) -> torch.Tensor:
+    """pe_moe_forward: the experts on given routing (fp32 weights, int32 ids [T, k])."""
+    dev = x.device
+    e, h, i = meta[4:]
+    xs = x.reshape(-1, h).contiguous()
+    t = xs.shape[0]
+    out = torch.empty_like(xs)
+    if t == 0:
+        return out.view(x.shape)
+    top_k = ids.shape[-1]
+    L = _lib.lib()
+    wsb = L.pe_moe_workspace_size(t, top_k, e, h, i)
+    ws = _lib.workspace(dev, wsb)
+    rc = L.pe_moe_forward(xs.data_ptr(), _lib.act_dtype(xs), t, h, i, e, top_k, w.data_ptr(),
+                          ids.data_ptr(), *_moe_weights(w13c, w13n, w13ct, w2c, w2n, w2ct, meta),
+                          out.data_ptr(), _lib.ptr(ws), wsb, _lib.stream_ptr(dev))
+    _lib.check(rc, "pe_moe_forward")
+    return out.view(x.shape)
+
+
+# The two MoE calls as torch custom ops, for traced / compiled models; the
+# fake implementations give the output's shape and dtype (x's).
+torch.library.custom_op("polarengine::moe_routed", _moe_routed, mutates_args=())
+torch.library.custom_op("polarengine::moe_given", _moe_given, mutates_args=())
+
+
+@torch.library.register_fake("polarengine::moe_routed")
+def _moe_routed_fake(x, lg, bias, w13c, w13n, w13ct, w2c, w2n, w2ct, route, meta):
+    return torch.empty_like(x)
+
+
+@torch.library.register_fake("polarengine::moe_given")
+def _moe_given_fake(x, w, ids, w13c, w13n, w13ct, w2c, w2n, w2ct, meta):
+    return torch.empty_like(x)
 
 
 class PolarPassthroughMoEMethod:

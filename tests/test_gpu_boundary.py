@@ -301,10 +301,25 @@ def test_fwht_cache_scoped_by_hooks_against_raw_writes():
     parent = _qkv_parent()
     assert install_fwht_cache_hooks(parent) == 1
     assert install_fwht_cache_hooks(parent) == 0  # idempotent
+    import polarengine_vllm.linear_method as LM
     x = to_dev(O.seeded_normal((64, 512), 1.0, 690))
     GLOBAL_FWHT_CACHE.clear()
-    parent(x)
-    assert GLOBAL_FWHT_CACHE.get(x, 512) is not None  # shared by q/k/v
+    calls = []
+    real = LM.fwht_pairs
+
+    def counting(t, *a, **k):
+        calls.append(t.shape)
+        return real(t, *a, **k)
+
+    LM.fwht_pairs = counting
+    try:
+        parent(x)
+        with torch.inference_mode():  # inference tensors share inside the scope too
+            parent(x.clone())
+    finally:
+        LM.fwht_pairs = real
+    assert len(calls) == 2  # one transform per parent forward, shared by q/k/v
+    assert GLOBAL_FWHT_CACHE.get(x, 512) is None  # released when the forward ended
     ver = x._version
     x2 = O.seeded_normal((64, 512), 1.0, 691)
     _raw_overwrite(x, to_dev(x2))
@@ -316,6 +331,28 @@ def test_fwht_cache_scoped_by_hooks_against_raw_writes():
         check_close(y.float().cpu().numpy(),
                     O.linear_apply(xnow, c, nrm, ct, 512).astype(np.float32), "after raw write")
     GLOBAL_FWHT_CACHE.clear()
+
+
+def test_apply_under_inference_mode_without_hooks():
+    """apply() at M = 64 (the materialised-transform range) on inference
+    tensors with no scope hooks installed: no version counter is touched,
+    nothing is cached, and each projection is right."""
+    from polarengine_vllm.kernels.fwht import GLOBAL_FWHT_CACHE
+    say("apply under inference_mode, no hooks")
+    parent = _qkv_parent(seed=720)
+    GLOBAL_FWHT_CACHE.clear()
+    with torch.inference_mode():
+        x = to_dev(O.seeded_normal((64, 512), 1.0, 721))
+        outs = parent(x)
+        assert GLOBAL_FWHT_CACHE._result is None
+        x.add_(1.0)  # in place between forwards: must not be served a stale transform
+        outs2 = parent(x)
+    for ys, xv in ((outs, O.seeded_normal((64, 512), 1.0, 721)), (outs2, None)):
+        xnow = x.cpu().numpy() if xv is None else xv
+        for y, lin in zip(ys, (parent.q, parent.k, parent.v)):
+            c, nrm, ct = lin.o
+            check_close(y.float().cpu().numpy(),
+                        O.linear_apply(xnow, c, nrm, ct, 512).astype(np.float32), "inference")
 
 
 def test_fwht_matmul_out_write_invalidates_cache():
@@ -367,3 +404,57 @@ def test_polar_gemv_splitk_names(bits):
     with pytest.raises(ValueError):
         polar_gemv_splitk(dcodes, to_dev(x_tf), to_dev(norms), to_dev(ct), n, k, k // 128,
                           split_k=0)
+
+
+@pytest.mark.parametrize("m", [1, 64])
+def test_apply_compiles_fullgraph(m):
+    """torch.compile(fullgraph=True) of a module whose forward calls
+    PolarQuantLinearMethod.apply traces through the polarengine::linear_apply
+    custom op and equals the eager forward bit for bit (aot_eager: no code
+    generation, the op runs the same kernels)."""
+    from polarengine_vllm.kernels.fwht import GLOBAL_FWHT_CACHE
+    say(f"torch.compile fullgraph linear m={m}")
+    parent = _qkv_parent(seed=730)
+    x = to_dev(O.seeded_normal((m, 512), 1.0, 731))
+    GLOBAL_FWHT_CACHE.clear()
+    eager = parent(x)
+    torch._dynamo.reset()
+    comp = torch.compile(parent, fullgraph=True, backend="aot_eager")
+    got = comp(x)
+    torch.cuda.synchronize()
+    for a, b in zip(got, eager):
+        assert a.dtype == b.dtype and a.shape == b.shape
+        assert torch.equal(a, b)
+    GLOBAL_FWHT_CACHE.clear()
+
+
+def test_moe_apply_compiles_fullgraph():
+    """The same for PolarQuantMoEMethod.apply (polarengine::moe_routed and,
+    after a traced custom routing function, polarengine::moe_given)."""
+    from test_gpu_kernels import _moe_layer
+    say("torch.compile fullgraph moe")
+    rng = np.random.default_rng(740)
+    meth, layer, _ = _moe_layer(rng, 16, 512, 384, 3, 4, True)
+
+    class Block(torch.nn.Module):
+        def __init__(self, given):
+            super().__init__()
+            self.given = given
+
+        def forward(self, x, logits):
+            if self.given:
+                def route(hidden_states, gating_output, topk, renormalize):
+                    w, ids = torch.topk(torch.softmax(gating_output.float(), -1), topk, -1)
+                    return w / w.sum(-1, keepdim=True), ids
+                return meth.apply(layer, x, logits, 4, True, custom_routing_function=route)
+            return meth.apply(layer, x, logits, 4, True)
+
+    x = to_dev(O.seeded_normal((48, 512), 1.0, 741))
+    logits = to_dev(O.seeded_normal((48, 16), 1.0, 742, np.float32))
+    for given in (False, True):
+        blk = Block(given)
+        eager = blk(x, logits)
+        torch._dynamo.reset()
+        got = torch.compile(blk, fullgraph=True, backend="aot_eager")(x, logits)
+        torch.cuda.synchronize()
+        assert torch.equal(got, eager), f"given={given}"

@@ -751,3 +751,39 @@ def test_moe_forward_matches_oracle(t, e, hdim, inter, k, b13, b2, tile):
     check_close(y.float().cpu().numpy(), want, f"moe t={t} e={e}")
     y2 = meth.apply(layer, to_dev(x), to_dev(logits), k, True)
     assert torch.equal(y, y2), "moe forward not deterministic"
+
+
+# ---------------------------------------------------------------------------
+# fwht_butterfly: whole-row transform of any power-of-two length
+# (reference kernels/fwht.py:160-190)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+def test_fwht_butterfly_matches_oracle(dtype):
+    """pe_fwht_pow2 against the oracle's float64 butterfly for n = 1 .. 32768:
+    fp32 within 2e-6 of max |y| (fp32 stages), fp16 / bf16 within one
+    rounding of the output type (4e-3 / 8e-3 of max |y|); self-inverse."""
+    from polarengine_vllm.kernels.fwht import fwht_butterfly
+    tdt = getattr(torch, dtype)
+    tol = {"float32": 2e-6, "float16": 4e-3, "bfloat16": 8e-3}[dtype]
+    rng = np.random.default_rng(5)
+    for logn in range(0, 16):
+        n = 1 << logn
+        for rows in (1, 3, 37):
+            if rows * n > (1 << 21):
+                continue
+            _say(f"fwht_butterfly n={n} rows={rows} {dtype}")
+            x = rng.standard_normal((rows, n)).astype(np.float32)
+            xd = torch.from_numpy(x).to(tdt).to(DEV)
+            y = fwht_butterfly(xd)
+            assert y.dtype == tdt and y.shape == xd.shape
+            want = O.fwht_butterfly(xd.float().cpu().numpy())
+            err = np.abs(y.float().cpu().numpy() - want).max() / max(np.abs(want).max(), 1e-30)
+            assert err <= tol, f"n={n} rows={rows}: normwise err {err:.3e}"
+            if dtype == "float32":
+                back = fwht_butterfly(y).cpu().numpy()
+                assert np.abs(back - x).max() <= 4e-6 * max(np.abs(x).max(), 1.0)
+    # the 128 case agrees with the blockwise kernel (fwht_matmul) to fp32 rounding
+    x = torch.from_numpy(rng.standard_normal((64, 128)).astype(np.float32)).to(DEV)
+    from polarengine_vllm.kernels.fwht import fwht_matmul
+    assert torch.allclose(fwht_butterfly(x), fwht_matmul(x), atol=1e-5)

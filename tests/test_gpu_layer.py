@@ -17,8 +17,7 @@ import pytest
 import torch
 
 import polar_oracle as O
-from gpu_helpers import (DEV, check_close, dev_tiled, linear_call, rand_layer, say,
-                         stratified_rows, to_dev)
+from gpu_helpers import DEV, check_close, dev_tiled, linear_call, rand_layer, say, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -28,14 +27,30 @@ C4_SPECS = [("q_proj", HID, NQ * HD, 5), ("k_proj", HID, NKV * HD, 5), ("v_proj"
             ("down_proj", INTER, HID, 4)]
 
 
-class PolarLinear(torch.nn.Module):
-    """A vLLM-style linear module: forward = quant_method.apply(self, x)."""
+# the checkpoint's polar_config.json for this layer (the reference fixture's
+# bit assignment, tests/conftest.py:60-131): methods come from
+# PolarQuantConfig.get_quant_method, as vLLM builds them
+C4_POLAR_CONFIG = {
+    "format": "polar_engine_v4", "quantization": "polarengine", "block_size": 128,
+    "bit_assignment": {"q_proj": 5, "k_proj": 5, "v_proj": 5, "o_proj": 6, "gate_proj": 3,
+                       "up_proj": 3, "down_proj": 4, "embed": 5, "lm_head": 6},
+    "layers": {},
+}
 
-    def __init__(self, in_f, out_f, bits, seed):
+
+class PolarLinear(torch.nn.Module):
+    """A vLLM-style linear module: forward = quant_method.apply(self, x), the
+    method resolved from the polar config by the module's prefix."""
+
+    def __init__(self, in_f, out_f, bits, seed, prefix):
         super().__init__()
+        from polarengine_vllm.config import PolarQuantConfig
         from polarengine_vllm.linear_method import PolarQuantLinearMethod
         from polarengine_vllm.quantizer import PolarQuantizer
-        self.quant_method = PolarQuantLinearMethod(128, bits)
+        cfg = PolarQuantConfig.from_config(C4_POLAR_CONFIG)
+        self.quant_method = cfg.get_quant_method(self, prefix)
+        assert isinstance(self.quant_method, PolarQuantLinearMethod)
+        assert self.quant_method.bits == bits, (prefix, self.quant_method.bits, bits)
         self.quant_method.create_weights(self, in_f, [out_f], in_f, out_f, torch.float16)
         self.to(DEV)
         w = torch.from_numpy(O.seeded_normal((out_f, in_f), 0.02, seed)).to(DEV)
@@ -57,7 +72,8 @@ class PolarLinear(torch.nn.Module):
 class Attn(torch.nn.Module):
     def __init__(self, seed):
         super().__init__()
-        mods = {n: PolarLinear(i, o, b, seed + k) for k, (n, i, o, b) in enumerate(C4_SPECS[:4])}
+        mods = {n: PolarLinear(i, o, b, seed + k, f"model.layers.0.self_attn.{n}")
+                for k, (n, i, o, b) in enumerate(C4_SPECS[:4])}
         for n, m in mods.items():
             setattr(self, n, m)
 
@@ -78,7 +94,7 @@ class Mlp(torch.nn.Module):
     def __init__(self, seed):
         super().__init__()
         for k, (n, i, o, b) in enumerate(C4_SPECS[4:]):
-            setattr(self, n, PolarLinear(i, o, b, seed + 4 + k))
+            setattr(self, n, PolarLinear(i, o, b, seed + 4 + k, f"model.layers.0.mlp.{n}"))
 
     def forward(self, x):
         g, u = self.gate_proj(x), self.up_proj(x)
@@ -153,6 +169,36 @@ def test_decoder_layer_c4(c4_layer, m, monkeypatch):
     assert c4_layer.self_attn.k_proj.seen[0] is q_in and c4_layer.self_attn.v_proj.seen[0] is q_in
 
 
+@pytest.mark.parametrize("m", [1, 64, 512])
+def test_decoder_layer_c4_inference_mode(c4_layer, m, monkeypatch):
+    """The C4 layer under torch.inference_mode() (how vLLM runs every
+    forward): inference tensors carry no version counter, the FWHT cache
+    still shares one transform per input inside each hooked block, and the
+    output equals the same forward outside inference mode bit for bit."""
+    import polarengine_vllm.linear_method as lm
+    say(f"C4 decoder layer under inference_mode m={m}")
+    calls = []
+    real = lm.fwht_pairs
+
+    def counting(x, *a, **k):
+        calls.append(x.shape)
+        return real(x, *a, **k)
+
+    monkeypatch.setattr(lm, "fwht_pairs", counting)
+    h = torch.from_numpy(O.seeded_normal((m, HID), 1.0, 990 + m)).to(DEV)
+    want = c4_layer(h)
+    n_plain = len(calls)
+    with torch.inference_mode():
+        hi = h.clone()
+        got = c4_layer(hi)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert len(calls) - n_plain == (0 if m <= 32 else 4)
+    for mod in c4_layer.modules():
+        if hasattr(mod, "seen"):
+            mod.seen.clear()
+
+
 # ---------------------------------------------------------------------------
 # C2: decode MLP shapes at M = 4 and 16 (tiled runtime layout, with bias)
 # ---------------------------------------------------------------------------
@@ -176,7 +222,7 @@ def test_c2_decode_mlp_shapes(m, n, k, bits):
 
 # ---------------------------------------------------------------------------
 # C3: prefill shapes; whole outputs against the dense dequantize-then-matmul
-# route (one fp32 sgemm), M = 8192 on a stratified row sample
+# route (one fp32 sgemm), M = 8192 included
 # ---------------------------------------------------------------------------
 
 @pytest.mark.parametrize("m,n,k,bits", [(256, 4096, 12288, 3), (256, 12288, 4096, 4),
@@ -193,10 +239,7 @@ def test_c3_prefill_whole_output(m, n, k, bits):
     fmt = _lib.PE_PACK_NIBBLE | _lib.PE_LAYOUT_TILE16
     y = linear_call(to_dev(x), dcodes, dnorms, ct, bits, fmt, n, to_dev(bias))
     w = O.dequant_weight(codes, norms, ct)
-    if m <= 2048:
-        rows = np.arange(m)
-    else:
-        rows = stratified_rows(m, seed=m + n, per_tile=2)
+    rows = np.arange(m)  # every row, M = 8192 included
     want = O.dequant_matmul(x[rows], w, bias)
     got = y[torch.from_numpy(rows).to(DEV)].float().cpu().numpy()
     check_close(got, want.astype(np.float32), f"C3 m={m} {n}x{k} q{bits} ({len(rows)} rows)")

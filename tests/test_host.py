@@ -189,6 +189,111 @@ def test_fwht_cache_semantics():
     assert cache.get(x, 128) is None
 
 
+def test_fwht_cache_inference_tensors_need_a_scope():
+    """Inference tensors (vLLM runs every forward under inference_mode) have
+    no version counter: put/get must not touch it, and outside a scope the
+    cache never serves them (a hidden state updated in place between layers
+    would otherwise get the previous layer's transform)."""
+    cache = FWHTCache()
+    r = torch.randn(4, 128)
+    with torch.inference_mode():
+        x = torch.randn(4, 128)
+        cache.put(x, 128, r)          # must not raise
+        assert cache.get(x, 128) is None
+        cache.enter_scope()
+        cache.put(x, 128, r)
+        assert cache.get(x, 128) is r
+        cache.exit_scope()            # the scope's end drops the transform
+        assert cache.get(x, 128) is None
+
+
+def test_fwht_cache_entry_dies_with_its_tensor():
+    """The cache holds x weakly: once x is freed the entry and its transform
+    go, and a new tensor at the same address misses."""
+    import gc
+    import weakref
+    cache = FWHTCache()
+    x, r = torch.randn(8, 128), torch.randn(8, 128)
+    cache.put(x, 128, r)
+    rref = weakref.ref(r)
+    del r, x
+    gc.collect()
+    assert cache._result is None and rref() is None
+    y = torch.randn(8, 128)
+    assert cache.get(y, 128) is None
+
+
+def test_fwht_cache_scope_hooks_share_inside_one_forward():
+    """install_fwht_cache_hooks: siblings inside one parent forward share the
+    transform under inference_mode; the parent's forward end releases it."""
+    from polarengine_vllm.linear_method import PolarQuantLinearMethod, install_fwht_cache_hooks
+    from polarengine_vllm.kernels.fwht import GLOBAL_FWHT_CACHE
+    method = PolarQuantLinearMethod(128, 4)
+    seen = []
+
+    class Proj(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.quant_method = method
+
+        def forward(self, t):
+            hit = GLOBAL_FWHT_CACHE.get(t, 128)
+            if hit is None:
+                GLOBAL_FWHT_CACHE.put(t, 128, t * 2)
+            seen.append(hit is not None)
+            return t
+
+    class Block(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.q, self.k, self.v = Proj(), Proj(), Proj()
+
+        def forward(self, t):
+            return self.q(t) + self.k(t) + self.v(t)
+
+    blk = Block()
+    assert install_fwht_cache_hooks(blk) == 1
+    assert install_fwht_cache_hooks(blk) == 0  # idempotent
+    with torch.inference_mode():
+        h = torch.randn(2, 128)
+        blk(h)
+        assert seen == [False, True, True]
+        assert GLOBAL_FWHT_CACHE.get(h, 128) is None and GLOBAL_FWHT_CACHE._result is None
+        h.add_(1.0)   # in place, untracked: the next forward starts empty anyway
+        blk(h)
+        assert seen[3:] == [False, True, True]
+
+
+def test_workspace_growth_keeps_old_buffers():
+    """A workspace that grows keeps every earlier buffer alive: a graph
+    captured earlier still writes through their raw pointers."""
+    from polarengine_vllm import _lib
+    dev = torch.device("cpu")
+    key = _lib._ws_key(dev)
+    _lib._WS_CACHE.pop(key, None)
+    _lib._WS_RETIRED.pop(key, None)
+    a = _lib.workspace(dev, 100)
+    assert a.numel() >= 100 and int(a.sum()) == 0
+    assert _lib.workspace(dev, 50) is a
+    b = _lib.workspace(dev, a.numel() + 1)
+    assert b is not a and b.numel() >= 2 * a.numel()
+    assert _lib._WS_RETIRED[key] == [a]
+    c = _lib.workspace(dev, b.numel() + 1)
+    assert _lib._WS_RETIRED[key] == [a, b] and c.numel() >= 2 * b.numel()
+    _lib._WS_CACHE.pop(key, None)
+    _lib._WS_RETIRED.pop(key, None)
+
+
+def test_fwht_butterfly_is_gpu_only_and_checks_length():
+    """fwht_butterfly (reference kernels/fwht.py:160-190) asserts a
+    power-of-two last dimension and has no CPU path."""
+    from polarengine_vllm.kernels.fwht import fwht_butterfly
+    with pytest.raises(AssertionError):
+        fwht_butterfly(torch.randn(2, 96))
+    with pytest.raises(RuntimeError, match="GPU only"):
+        fwht_butterfly(torch.randn(2, 64))
+
+
 def test_fwht_clear_hook_as_forward_pre_hook():
     """create_fwht_clear_hook (reference linear_method.py:265-288): a forward
     pre-hook that empties the method's cache before the module runs."""
@@ -208,3 +313,29 @@ def test_fwht_clear_hook_as_forward_pre_hook():
     blk(x)
     assert seen == [None]  # cleared before the forward ran
     method._fwht_cache.clear()
+
+
+def test_custom_ops_registered_with_fake_shapes():
+    """The linear and MoE forwards are torch custom ops whose fake
+    implementations give the output's shape and dtype without running a
+    kernel (what torch.compile traces)."""
+    import polarengine_vllm.linear_method  # noqa: F401  (registers the ops)
+    import polarengine_vllm.moe_method  # noqa: F401
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        x = torch.empty(3, 5, 256, dtype=torch.bfloat16)
+        codes = torch.empty(96, 128, dtype=torch.uint8)
+        y = torch.ops.polarengine.linear_apply(x, codes, torch.empty(96, 2, dtype=torch.float16),
+                                               torch.empty(16), None, 4, 3, 256, 256, 96, [])
+        assert y.shape == (3, 5, 96) and y.dtype == torch.bfloat16
+        y32 = torch.ops.polarengine.linear_apply(x.float(), codes, torch.empty(96, 2), torch.empty(16),
+                                                 None, 4, 3, 256, 256, 96, [])
+        assert y32.dtype == torch.float16
+        xm = torch.empty(7, 256, dtype=torch.float16)
+        w = [torch.empty(1)] * 6
+        out = torch.ops.polarengine.moe_routed(xm, torch.empty(7, 8), None, *w, [2, 1, 0, 0, 0],
+                                               [3, 1, 4, 1, 8, 256, 128])
+        assert out.shape == xm.shape and out.dtype == xm.dtype
+        out = torch.ops.polarengine.moe_given(xm, torch.empty(7, 2), torch.empty(7, 2, dtype=torch.int32),
+                                              *w, [3, 1, 4, 1, 8, 256, 128])
+        assert out.shape == xm.shape

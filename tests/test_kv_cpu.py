@@ -119,6 +119,17 @@ def test_presets_and_patch_model_attention():
         assert blk.attn._polar_kv_layer_idx == i and blk.attn._polar_kv_cache is vcache
         assert blk.attn.forward.__name__ == "wrapped_forward"
         assert not hasattr(blk, "_polar_kv_layer_idx")  # the backends were found, not the blocks
+    # patching again re-points the backends at the new cache: the original
+    # forward is wrapped once more, never the earlier wrapper
+    orig = [blk.attn._polar_kv_orig_forward for blk in vmodel]
+    vcache2 = patch_model_attention(vmodel, PolarKVConfig(num_layers=3))
+    for i, blk in enumerate(vmodel):
+        assert blk.attn._polar_kv_cache is vcache2
+        assert blk.attn._polar_kv_orig_forward is orig[i]
+        inner = blk.attn.forward.__closure__
+        cells = [c.cell_contents for c in inner]
+        assert orig[i] in cells and not any(getattr(c, "__name__", "") == "wrapped_forward"
+                                            for c in cells if callable(c))
 
 
 def _count_codes(r, ct):
