@@ -93,12 +93,18 @@ class Linear:
             _lib.check(rc, "pe_linear_forward")
 
 
-def time_steps(calls, steps, warmup, dev, repeats=1):
+def time_steps(calls, steps, warmup, dev, repeats=1, steady=False):
     """Exactly `steps` calls per timed sample (cycling through `calls`),
     captured in one HIP graph and replayed on the current stream; `warmup`
     untimed eager calls (at least one per call object) and one untimed replay
     first. Each sample is bracketed by synchronize, with HIP events on the
-    replay stream. Returns (median seconds per call, per-sample list)."""
+    replay stream. Cold samples: synchronize, start event, replay, end event
+    (the replay's launch latency falls inside the sample). Steady samples
+    (steady=True): synchronize, an untimed replay, start event, the timed
+    replay, end event -- the timed replay is queued while the untimed one
+    runs, as in a serving loop, so the sample holds the calls alone; it still
+    holds exactly `steps` calls. Returns (median seconds per call, per-sample
+    list)."""
     s = torch.cuda.Stream(device=dev)
     s.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(s):
@@ -116,6 +122,8 @@ def time_steps(calls, steps, warmup, dev, repeats=1):
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     for _ in range(repeats):
         torch.cuda.synchronize(dev)
+        if steady:
+            g.replay()
         e0.record()
         g.replay()
         e1.record()
@@ -353,16 +361,7 @@ def prefill_extra(dev):
                      "GB/s": round(algo_bytes(256, nn, kk, bb) / t / 1e9, 1),
                      "includes": "FWHT-128 of x (pair f16) + MFMA GEMM (K split where the tiles are few)"}
         del lay
-    flops = 2.0 * 2048 * 12288 * 4096
-    for name, (nn, kk, bb, seed) in (("prefill_m2048", (12288, 4096, 4, 300)),
-                                     ("prefill_down_q3_m2048", (4096, 12288, 3, 301))):
-        pf = Linear(nn, kk, bb, 2048, dev, seed=seed)
-        t_pf = time_eager(pf, 3, 20, dev)
-        out[name] = {"us_per_call": round(t_pf * 1e6, 1),
-                     "TFLOP/s": round(flops / t_pf / 1e12, 1),
-                     "mfma_frac": round(flops / t_pf / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
-                     "includes": "FWHT-128 of x (pair f16) + MFMA GEMM"}
-        del pf
+    out.update(prefill_m2048_extra(dev))
     # chunked-prefill sizes on the down projection (few output tiles: K split)
     for mm in (128, 512):
         lay = [Linear(4096, 12288, 4, mm, dev, seed=310 + i) for i in range(4)]
@@ -373,6 +372,160 @@ def prefill_extra(dev):
                                          "GB/s": round(algo_bytes(mm, 4096, 12288, 4) / t / 1e9, 1)}
         del lay
     return out
+
+
+PREFILL_TRACE_JSON = os.path.join(ROOT, "profiles", "trace_gemm4_prefill_m2048.json")
+PREFILL_PMC_JSON = os.path.join(ROOT, "profiles", "pmc_gemm4_prefill_m2048.json")
+
+
+def _time_each(fn, calls, dev):
+    """Per-call times of `calls` back-to-back calls (HIP events around each
+    call, one synchronize at the end): the first calls run at full clock,
+    later ones at the clock the card holds under sustained load."""
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(calls + 1)]
+    torch.cuda.synchronize(dev)
+    ev[0].record()
+    for i in range(calls):
+        fn()
+        ev[i + 1].record()
+    torch.cuda.synchronize(dev)
+    return [ev[i].elapsed_time(ev[i + 1]) * 1e-3 for i in range(calls)]
+
+
+def prefill_m2048_extra(dev, trace_only=False):
+    """The metric's second half: the prefill linear at M=2048 (FWHT-128 of x
+    into pair f16, then the MFMA GEMM) on Q4 12288x4096 and the Q3 4096x12288
+    down projection. us_per_call: 3 warm-up and 20 back-to-back calls
+    (sustained: the card lowers its clock under MFMA load); full_clock_us:
+    the fastest of 20 back-to-back calls timed one by one (the first calls
+    run before the clock drops). The dense fp16 GEMM
+    of the same shape (torch.matmul: hipBLASLt) is timed the same two ways
+    beside it. roofline: the GEMM kernel alone, its duration the larger of
+    the committed rocprofv3 trace mean and the event-timed call minus the
+    traced FWHT (profiles/), 2*M*N*K flops over it against 2.5 PFLOP/s
+    dense fp16; mfma_busy from the committed counter pass."""
+    out = {}
+    flops = 2.0 * 2048 * 12288 * 4096
+    trace = pmc = None
+    if os.path.exists(PREFILL_TRACE_JSON):
+        with open(PREFILL_TRACE_JSON) as f:
+            trace = json.load(f)
+    if os.path.exists(PREFILL_PMC_JSON):
+        with open(PREFILL_PMC_JSON) as f:
+            pmc = json.load(f)
+    for name, (nn, kk, bb, seed) in (("prefill_m2048", (12288, 4096, 4, 300)),
+                                     ("prefill_down_q3_m2048", (4096, 12288, 3, 301))):
+        pf = Linear(nn, kk, bb, 2048, dev, seed=seed)
+        t_pf = time_eager(pf, 3, 20, dev)
+        if trace_only:
+            out[name] = {"us_per_call": round(t_pf * 1e6, 1)}
+            del pf
+            continue
+        t_full = float(np.min(_time_each(pf, 20, dev)))
+        ent = {"us_per_call": round(t_pf * 1e6, 1),
+               "TFLOP/s": round(flops / t_pf / 1e12, 1),
+               "mfma_frac": round(flops / t_pf / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+               "full_clock_us": round(t_full * 1e6, 1),
+               "full_clock_TFLOP/s": round(flops / t_full / 1e12, 1),
+               "includes": "FWHT-128 of x (pair f16) + MFMA GEMM"}
+        # dense fp16 reference of the same product (not this library)
+        a = torch.randn(2048, kk, device=dev, dtype=torch.float16)
+        b = torch.randn(nn, kk, device=dev, dtype=torch.float16)
+        c = torch.empty(2048, nn, device=dev, dtype=torch.float16)
+        dense = lambda: torch.matmul(a, b.t(), out=c)  # noqa: E731
+        t_d = time_eager(dense, 3, 20, dev)
+        t_df = float(np.min(_time_each(dense, 20, dev)))
+        ent["dense_fp16_reference"] = {"us_per_call": round(t_d * 1e6, 1),
+                                       "full_clock_us": round(t_df * 1e6, 1),
+                                       "what": "torch.matmul fp16 (hipBLASLt), same shape, "
+                                               "timed the same two ways"}
+        del a, b, c
+        tr = (trace or {}).get(name)
+        if tr:
+            gemm_us = max(tr["gemm_avg_us"], t_pf * 1e6 - tr["fwht_avg_us"])
+            ach = flops / (gemm_us * 1e-6) / 1e12
+            ent["roofline"] = {"bound": "mfma", "kernel": tr["gemm_kernel"],
+                               "kernel_us": round(gemm_us, 2),
+                               "kernel_us_source": "trace mean" if gemm_us == tr["gemm_avg_us"]
+                               else "HIP events minus traced FWHT",
+                               "achieved": round(ach, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                               "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK_TFLOPS, 4),
+                               "fwht_us": tr["fwht_avg_us"], "trace": tr}
+            if pmc and pmc.get(name):
+                ent["roofline"]["mfma_busy"] = pmc[name]
+        out[name] = ent
+        del pf
+    return out
+
+
+def fwht_extra(dev):
+    """FWHT-128 of the prefill activation into the GEMM's pair-f16 layout,
+    M=2048 at K=4096 and K=12288, as HBM GB/s of 2*M*K*2 bytes (fp16 in,
+    pair f16 out), over 8 rotating inputs from a HIP graph."""
+    out = {}
+    for kk in (4096, 12288):
+        xs = [torch.randn(2048, kk, device=dev, dtype=torch.float16) for _ in range(8)]
+        ys = [torch.empty(2048, kk // 2, device=dev, dtype=torch.int32) for _ in range(8)]
+        L = _lib.lib()
+
+        def mk(x, y):
+            def f():
+                rc = L.pe_fwht128(x.data_ptr(), 0, 2048, kk, kk, y.data_ptr(), _lib.PE_XTF_PAIR_F16,
+                                  _lib.stream_ptr(dev))
+                if rc:
+                    _lib.check(rc, "pe_fwht128")
+            return f
+        t, n = time_graph([mk(x, y) for x, y in zip(xs, ys)], 1, 16, 256, dev)
+        b = 2 * 2048 * kk * 2
+        out[f"fwht_m2048_k{kk}"] = {"us_per_call": round(t * 1e6, 2), "bytes": b,
+                                    "GB/s": round(b / t / 1e9, 1),
+                                    "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4)}
+        del xs, ys
+    return out
+
+
+def hbm_extra(dev, steps=20, repeats=10):
+    """The part's measured HBM ceiling, timed like the headline: a plain
+    streaming read of the headline's 26 MB (pe_stream_read, 16 rotating
+    buffers = 416 MB, graph replays of `steps` calls, cold and steady
+    samples) and a 1 GiB copy (pe_copy: 2 GiB of traffic per call)."""
+    L = _lib.lib()
+    nbytes = algo_bytes(1, 12288, 4096, 4) // 16 * 16
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).random_(0, 255) for _ in range(N_COPIES)]
+    sink = torch.empty(L.pe_stream_read_sink_bytes(nbytes), dtype=torch.uint8, device=dev)
+
+    def mk(b):
+        def f():
+            rc = L.pe_stream_read(b.data_ptr(), nbytes, sink.data_ptr(), 0x9E3779B9,
+                                  _lib.stream_ptr(dev))
+            if rc:
+                _lib.check(rc, "pe_stream_read")
+        return f
+    calls = [mk(b) for b in bufs]
+    t_cold, _ = time_steps(calls, steps, 32, dev, repeats=repeats)
+    t_st, _ = time_steps(calls, steps, 32, dev, repeats=repeats, steady=True)
+    del bufs
+    cb = 1 << 30
+    src = torch.empty(cb, dtype=torch.uint8, device=dev).random_(0, 255)
+    dst = torch.empty_like(src)
+
+    def cp():
+        rc = L.pe_copy(dst.data_ptr(), src.data_ptr(), cb, _lib.stream_ptr(dev))
+        if rc:
+            _lib.check(rc, "pe_copy")
+    t_cp = time_eager(cp, 3, 20, dev)
+    assert torch.equal(src[:1 << 20], dst[:1 << 20])
+    del src, dst
+    return {"hbm_read_26MB": {"us_per_call": round(t_st * 1e6, 3), "bytes": nbytes,
+                              "GB/s": round(nbytes / t_st / 1e9, 1),
+                              "hbm_frac": round(nbytes / t_st / 1e9 / HBM_PEAK_GBS, 4),
+                              "cold_us_per_call": round(t_cold * 1e6, 3),
+                              "cold_GB/s": round(nbytes / t_cold / 1e9, 1),
+                              "what": "pe_stream_read of the headline's byte count, 16 rotating "
+                                      "buffers, steady and cold graph samples like the headline"},
+            "hbm_copy_1GiB": {"us_per_call": round(t_cp * 1e6, 1), "bytes_moved": 2 * cb,
+                              "GB/s": round(2 * cb / t_cp / 1e9, 1),
+                              "hbm_frac": round(2 * cb / t_cp / 1e9 / HBM_PEAK_GBS, 4)}}
 
 
 class DecoderLayerLinears:
@@ -553,6 +706,63 @@ def summarize_trace(trace_csv, kernel_substr="gemv_mfma_kernel"):
             if spans else 0}
 
 
+def summarize_prefill(trace_csv, pmc_csv=None):
+    """The M=2048 prefill dispatches of `bench.py --only-extra prefill2048`
+    (per shape: 3 warm-up and 20 timed calls, each an fwht128_kernel then the
+    GEMM; Q4 12288x4096 first, then Q3 4096x12288): per shape the GEMM's and
+    the transform's mean / median / min duration over the 20 timed calls;
+    with the counter pass, per-dispatch means of every counter over the same
+    calls and the MFMA figures derived from them."""
+    import csv
+    names = ("prefill_m2048", "prefill_down_q3_m2048")
+    rows = []
+    for r in csv.DictReader(open(trace_csv)):
+        kn = r["Kernel_Name"]
+        if "fwht128_kernel" in kn or "gemm" in kn:
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), kn))
+    rows.sort()
+    if len(rows) != 92:
+        raise SystemExit(f"{trace_csv}: {len(rows)} transform / GEMM dispatches, expected 92")
+    out = {}
+    for i, name in enumerate(names):
+        half = rows[46 * i:46 * (i + 1)]
+        fw = [(e - b) * 1e-3 for b, e, k in half if "fwht128" in k][3:]
+        gm = [(e - b) * 1e-3 for b, e, k in half if "gemm" in k][3:]
+        gk = [k for _, _, k in half if "gemm" in k][0]
+        out[name] = {"gemm_kernel": gk.split("(")[0], "gemm_avg_us": round(float(np.mean(gm)), 2),
+                     "gemm_median_us": round(float(np.median(gm)), 2),
+                     "gemm_min_us": round(float(np.min(gm)), 2),
+                     "fwht_avg_us": round(float(np.mean(fw)), 2),
+                     "fwht_median_us": round(float(np.median(fw)), 2), "timed_calls": len(gm)}
+    if pmc_csv:
+        disp = {}
+        for r in csv.DictReader(open(pmc_csv)):
+            if "gemm" not in r["Kernel_Name"]:
+                continue
+            d = disp.setdefault(int(r["Dispatch_Id"]), {"kernel": r["Kernel_Name"].split("(")[0]})
+            d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        ids = sorted(disp)
+        if len(ids) != 46:
+            raise SystemExit(f"{pmc_csv}: {len(ids)} GEMM dispatches, expected 46")
+        pm = {}
+        for i, name in enumerate(names):
+            sel = [disp[d] for d in ids[23 * i + 3:23 * (i + 1)]]
+            keys = [k for k in sel[0] if k != "kernel"]
+            mean = {k: float(np.mean([x[k] for x in sel])) for k in keys}
+            ent = {"kernel": sel[0]["kernel"], "counters_mean": {k: round(v) for k, v in mean.items()}}
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in mean and "SQ_BUSY_CU_CYCLES" in mean:
+                ent["mfma_busy_of_cu_busy"] = round(
+                    mean["SQ_VALU_MFMA_BUSY_CYCLES"] / (4.0 * mean["SQ_BUSY_CU_CYCLES"]), 4)
+            if "SQ_INSTS_MFMA" in mean:
+                ent["mfma_flops"] = mean["SQ_INSTS_MFMA"] * 32768.0  # 32x32x16 f16: 2*32*32*16
+            if "GRBM_GUI_ACTIVE" in mean and "SQ_VALU_MFMA_BUSY_CYCLES" in mean:
+                ent["mfma_busy_of_elapsed"] = round(
+                    mean["SQ_VALU_MFMA_BUSY_CYCLES"] / (4.0 * 256 * mean["GRBM_GUI_ACTIVE"] / 8.0), 4)
+            pm[name] = ent
+        return out, pm
+    return out, None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -567,19 +777,32 @@ def main():
     ap.add_argument("--headline-only", action="store_true",
                     help="time only the headline call (for a rocprofv3 kernel trace whose "
                          "dispatches are exactly the headline's)")
-    ap.add_argument("--only-extra", choices=("moe", "prefill", "kv", "layer", "decode", "e2e"),
+    ap.add_argument("--only-extra", choices=("moe", "prefill", "prefill2048", "kv", "layer",
+                                             "decode", "e2e", "fwht", "hbm"),
                     help="time only one of the extra workloads and print its JSON (for a "
                          "rocprofv3 kernel trace of that path alone)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print the traffic JSON from the two pmc passes and exit")
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
                     help="print the headline kernel's trace summary JSON and exit")
+    ap.add_argument("--summarize-prefill", nargs="+", metavar="CSV",
+                    help="KERNEL_TRACE_CSV [PMC_CSV] of --only-extra prefill2048: write "
+                         "profiles/trace_gemm4_prefill_m2048.json (and pmc_...json) and exit")
     args = ap.parse_args()
     if args.summarize_pmc:
         print(json.dumps(summarize_pmc(*args.summarize_pmc), indent=1))
         return
     if args.summarize_trace:
         print(json.dumps(summarize_trace(args.summarize_trace), indent=1))
+        return
+    if args.summarize_prefill:
+        tr, pm = summarize_prefill(*args.summarize_prefill[:2])
+        with open(PREFILL_TRACE_JSON, "w") as f:
+            json.dump(tr, f, indent=1)
+        if pm:
+            with open(PREFILL_PMC_JSON, "w") as f:
+                json.dump(pm, f, indent=1)
+        print(json.dumps({"trace": tr, "pmc": pm}, indent=1))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build's hot path is a single-GPU kernel "
@@ -593,25 +816,33 @@ def main():
         return
     if args.only_extra:
         fn = {"moe": moe_extra, "prefill": prefill_extra, "kv": kv_extra,
-              "layer": decoder_layer_extra, "decode": decode_extra, "e2e": e2e_extra}[args.only_extra]
+              "prefill2048": lambda d: prefill_m2048_extra(d, trace_only=True),
+              "layer": decoder_layer_extra, "decode": decode_extra, "e2e": e2e_extra,
+              "fwht": fwht_extra, "hbm": hbm_extra}[args.only_extra]
         print(json.dumps(fn(dev)))
         return
 
     n, k, bits, m = 12288, 4096, 4, 1
     x = torch.randn(m, k, device=dev, dtype=torch.float16)
     layers = [Linear(n, k, bits, m, dev, seed=100 + i, x=x) for i in range(N_COPIES)]
-    t_call, samples = time_steps(layers, args.steps, args.warmup, dev, repeats=args.repeats)
+    t_call, samples = time_steps(layers, args.steps, args.warmup, dev, repeats=args.repeats,
+                                 steady=True)
+    t_cold, samples_cold = time_steps(layers, args.steps, args.warmup, dev, repeats=args.repeats)
     B = algo_bytes(m, n, k, bits)
     if args.headline_only:
         print(json.dumps({"workload": "headline only", "us_per_call": round(t_call * 1e6, 3),
                           "GB/s": round(B / t_call / 1e9, 1), "steps": args.steps,
                           "repeats": args.repeats,
-                          "samples_us": [round(v * 1e6, 3) for v in samples]}))
+                          "samples_us": [round(v * 1e6, 3) for v in samples],
+                          "cold_us_per_call": round(t_cold * 1e6, 3),
+                          "cold_samples_us": [round(v * 1e6, 3) for v in samples_cold]}))
         return
     t_hot, _ = time_graph(layers[:1], 1, args.warmup, 1024, dev)
     del layers
 
     extra = decode_extra(dev)
+    extra.update(hbm_extra(dev, args.steps, args.repeats))
+    extra.update(fwht_extra(dev))
     extra.update(prefill_extra(dev))
     extra.update(decoder_layer_extra(dev))
     extra["cache_hot_m1"] = {"us_per_call": round(t_hot * 1e6, 2),
@@ -656,10 +887,16 @@ def main():
         "config": {"workload": "decode linear Q4 12288x4096 M=1 (FWHT fused + nibble GEMV), "
                                f"{N_COPIES} rotating weight copies",
                    "M": m, "N": n, "K": k, "bits": bits, "algorithmic_bytes": B},
-        "timing": {"method": f"{args.repeats} samples of exactly {args.steps} calls (one HIP "
-                             "graph replay each, HIP events on the replay stream); median",
+        "timing": {"method": f"{args.repeats} steady samples of exactly {args.steps} calls (one "
+                             "HIP graph replay each, queued behind an untimed replay of the same "
+                             "graph so the timed one holds the calls alone; HIP events on the "
+                             "replay stream); median",
                    "samples": args.repeats,
-                   "min_us": round(min(samples) * 1e6, 3), "max_us": round(max(samples) * 1e6, 3)},
+                   "min_us": round(min(samples) * 1e6, 3), "max_us": round(max(samples) * 1e6, 3),
+                   "cold_us_per_call": round(t_cold * 1e6, 3),
+                   "cold_GB/s": round(B / t_cold / 1e9, 1),
+                   "cold_method": "the same samples without the untimed replay in front: the "
+                                  "replay's launch latency falls inside the sample"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic,

@@ -73,6 +73,13 @@ _SIGNATURES = {
                                        _vp, _vp, _c_sz, _vp]),
 }
 
+# measurement helpers (include/polarengine_amd_bench.h)
+_SIGNATURES.update({
+    "pe_stream_read_sink_bytes": (_c_sz, [_c_i64]),
+    "pe_stream_read": (_c_int, [_vp, _c_i64, _vp, ctypes.c_uint32, _vp]),
+    "pe_copy": (_c_int, [_vp, _vp, _c_i64, _vp]),
+})
+
 _lib: Optional[ctypes.CDLL] = None
 
 
