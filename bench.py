@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -344,7 +345,7 @@ def prefill_extra(dev):
         for name, (nn, kk, bb, seed) in ((f"prefill_m{mm}", (12288, 4096, 4, 320)),
                                          (f"prefill_down_q3_m{mm}", (4096, 12288, 3, 321))):
             pf = Linear(nn, kk, bb, mm, dev, seed=seed)
-            t_pf = time_eager(pf, 2, reps, dev)
+            t_pf, _, _ = time_settled(pf, dev, steps=reps)
             fl = 2.0 * mm * nn * kk
             out[name] = {"us_per_call": round(t_pf * 1e6, 1),
                          "TFLOP/s": round(fl / t_pf / 1e12, 1),
@@ -392,17 +393,31 @@ def _time_each(fn, calls, dev):
     return [ev[i].elapsed_time(ev[i + 1]) * 1e-3 for i in range(calls)]
 
 
+def time_settled(fn, dev, steps=20, settle_s=0.08):
+    """Back-to-back calls timed one by one after warm-up calls worth about
+    settle_s of GPU time. Under a sustained MFMA load the card's clock dips
+    for a few tens of milliseconds (the M=2048 GEMM goes from 214 to ~270 us
+    per call around calls 10-20, and back to ~212 us after ~80 calls); the
+    timed calls come after that. Returns (mean seconds per call, per-call
+    seconds, warm-up calls)."""
+    t0 = time_eager(fn, 1, 3, dev)
+    n = int(math.ceil(settle_s / max(t0, 1e-6)))
+    for _ in range(n):
+        fn()
+    ts = _time_each(fn, steps, dev)
+    return float(np.mean(ts)), ts, n
+
+
 def prefill_m2048_extra(dev, trace_only=False):
     """The metric's second half: the prefill linear at M=2048 (FWHT-128 of x
     into pair f16, then the MFMA GEMM) on Q4 12288x4096 and the Q3 4096x12288
-    down projection. us_per_call: 3 warm-up and 20 back-to-back calls
-    (sustained: the card lowers its clock under MFMA load); full_clock_us:
-    the fastest of 20 back-to-back calls timed one by one (the first calls
-    run before the clock drops). The dense fp16 GEMM
-    of the same shape (torch.matmul: hipBLASLt) is timed the same two ways
-    beside it. roofline: the GEMM kernel alone, its duration the larger of
-    the committed rocprofv3 trace mean and the event-timed call minus the
-    traced FWHT (profiles/), 2*M*N*K flops over it against 2.5 PFLOP/s
+    down projection. us_per_call: the mean of 20 back-to-back calls timed
+    one by one once the clock has settled under the sustained load
+    (time_settled); min_us / max_us: their spread. The dense fp16 GEMM of
+    the same shape (torch.matmul: hipBLASLt) is timed the same way beside it.
+    roofline: the GEMM kernel alone, its duration the larger of the committed
+    rocprofv3 trace mean (same settled calls) and the event-timed call minus
+    the traced FWHT (profiles/), 2*M*N*K flops over it against 2.5 PFLOP/s
     dense fp16; mfma_busy from the committed counter pass."""
     out = {}
     flops = 2.0 * 2048 * 12288 * 4096
@@ -416,29 +431,28 @@ def prefill_m2048_extra(dev, trace_only=False):
     for name, (nn, kk, bb, seed) in (("prefill_m2048", (12288, 4096, 4, 300)),
                                      ("prefill_down_q3_m2048", (4096, 12288, 3, 301))):
         pf = Linear(nn, kk, bb, 2048, dev, seed=seed)
-        t_pf = time_eager(pf, 3, 20, dev)
+        t_pf, ts, nwarm = time_settled(pf, dev)
         if trace_only:
-            out[name] = {"us_per_call": round(t_pf * 1e6, 1)}
+            out[name] = {"us_per_call": round(t_pf * 1e6, 1), "warmup_calls": nwarm}
             del pf
             continue
-        t_full = float(np.min(_time_each(pf, 20, dev)))
         ent = {"us_per_call": round(t_pf * 1e6, 1),
                "TFLOP/s": round(flops / t_pf / 1e12, 1),
                "mfma_frac": round(flops / t_pf / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
-               "full_clock_us": round(t_full * 1e6, 1),
-               "full_clock_TFLOP/s": round(flops / t_full / 1e12, 1),
+               "min_us": round(min(ts) * 1e6, 1), "max_us": round(max(ts) * 1e6, 1),
+               "warmup_calls": nwarm,
                "includes": "FWHT-128 of x (pair f16) + MFMA GEMM"}
         # dense fp16 reference of the same product (not this library)
         a = torch.randn(2048, kk, device=dev, dtype=torch.float16)
         b = torch.randn(nn, kk, device=dev, dtype=torch.float16)
         c = torch.empty(2048, nn, device=dev, dtype=torch.float16)
         dense = lambda: torch.matmul(a, b.t(), out=c)  # noqa: E731
-        t_d = time_eager(dense, 3, 20, dev)
-        t_df = float(np.min(_time_each(dense, 20, dev)))
+        t_d, ts_d, _ = time_settled(dense, dev)
         ent["dense_fp16_reference"] = {"us_per_call": round(t_d * 1e6, 1),
-                                       "full_clock_us": round(t_df * 1e6, 1),
+                                       "min_us": round(min(ts_d) * 1e6, 1),
+                                       "max_us": round(max(ts_d) * 1e6, 1),
                                        "what": "torch.matmul fp16 (hipBLASLt), same shape, "
-                                               "timed the same two ways"}
+                                               "timed the same way"}
         del a, b, c
         tr = (trace or {}).get(name)
         if tr:
@@ -706,34 +720,41 @@ def summarize_trace(trace_csv, kernel_substr="gemv_mfma_kernel"):
             if spans else 0}
 
 
-def summarize_prefill(trace_csv, pmc_csv=None):
+def summarize_prefill(trace_csv, pmc_csv=None, timed=20):
     """The M=2048 prefill dispatches of `bench.py --only-extra prefill2048`
-    (per shape: 3 warm-up and 20 timed calls, each an fwht128_kernel then the
-    GEMM; Q4 12288x4096 first, then Q3 4096x12288): per shape the GEMM's and
-    the transform's mean / median / min duration over the 20 timed calls;
+    (per shape: warm-up calls until the clock settles, then `timed` calls,
+    each an fwht128_kernel then the GEMM; Q4 12288x4096 first, then Q3
+    4096x12288; the two GEMMs are different kernel instantiations and the two
+    transforms different grid sizes): per shape the GEMM's and the
+    transform's mean / median / min duration over the last `timed` calls;
     with the counter pass, per-dispatch means of every counter over the same
     calls and the MFMA figures derived from them."""
     import csv
     names = ("prefill_m2048", "prefill_down_q3_m2048")
-    rows = []
+    gemm, fw = {}, {}
     for r in csv.DictReader(open(trace_csv)):
         kn = r["Kernel_Name"]
-        if "fwht128_kernel" in kn or "gemm" in kn:
-            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), kn))
-    rows.sort()
-    if len(rows) != 92:
-        raise SystemExit(f"{trace_csv}: {len(rows)} transform / GEMM dispatches, expected 92")
+        d = (int(r["Start_Timestamp"]), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3)
+        if "gemm" in kn:
+            gemm.setdefault(kn.split("(")[0], []).append(d)
+        elif "fwht128_kernel" in kn:
+            fw.setdefault(r.get("Grid_Size_X", r.get("Grid_Size")), []).append(d)
+    if len(gemm) != 2 or len(fw) != 2:
+        raise SystemExit(f"{trace_csv}: expected two GEMM kernels and two transform sizes, got "
+                         f"{list(gemm)} / {list(fw)}")
+    gk = sorted(gemm, key=lambda k: min(gemm[k])[0])   # in call order
+    fk = sorted(fw, key=lambda k: min(fw[k])[0])
     out = {}
-    for i, name in enumerate(names):
-        half = rows[46 * i:46 * (i + 1)]
-        fw = [(e - b) * 1e-3 for b, e, k in half if "fwht128" in k][3:]
-        gm = [(e - b) * 1e-3 for b, e, k in half if "gemm" in k][3:]
-        gk = [k for _, _, k in half if "gemm" in k][0]
-        out[name] = {"gemm_kernel": gk.split("(")[0], "gemm_avg_us": round(float(np.mean(gm)), 2),
+    for name, g, f in zip(names, gk, fk):
+        gm = [x for _, x in sorted(gemm[g])][-timed:]
+        fwv = [x for _, x in sorted(fw[f])][-timed:]
+        out[name] = {"gemm_kernel": g.replace("void ", ""), "gemm_avg_us": round(float(np.mean(gm)), 2),
                      "gemm_median_us": round(float(np.median(gm)), 2),
                      "gemm_min_us": round(float(np.min(gm)), 2),
-                     "fwht_avg_us": round(float(np.mean(fw)), 2),
-                     "fwht_median_us": round(float(np.median(fw)), 2), "timed_calls": len(gm)}
+                     "gemm_max_us": round(float(np.max(gm)), 2),
+                     "fwht_avg_us": round(float(np.mean(fwv)), 2),
+                     "fwht_median_us": round(float(np.median(fwv)), 2), "timed_calls": len(gm),
+                     "dispatches": len(gemm[g])}
     if pmc_csv:
         disp = {}
         for r in csv.DictReader(open(pmc_csv)):
@@ -741,15 +762,14 @@ def summarize_prefill(trace_csv, pmc_csv=None):
                 continue
             d = disp.setdefault(int(r["Dispatch_Id"]), {"kernel": r["Kernel_Name"].split("(")[0]})
             d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
-        ids = sorted(disp)
-        if len(ids) != 46:
-            raise SystemExit(f"{pmc_csv}: {len(ids)} GEMM dispatches, expected 46")
         pm = {}
-        for i, name in enumerate(names):
-            sel = [disp[d] for d in ids[23 * i + 3:23 * (i + 1)]]
+        for name, g in zip(names, gk):
+            sel = [disp[i] for i in sorted(disp) if disp[i]["kernel"] == g][-timed:]
+            if not sel:
+                raise SystemExit(f"{pmc_csv}: no dispatches of {g}")
             keys = [k for k in sel[0] if k != "kernel"]
             mean = {k: float(np.mean([x[k] for x in sel])) for k in keys}
-            ent = {"kernel": sel[0]["kernel"], "counters_mean": {k: round(v) for k, v in mean.items()}}
+            ent = {"kernel": g.replace("void ", ""), "counters_mean": {k: round(v) for k, v in mean.items()}}
             if "SQ_VALU_MFMA_BUSY_CYCLES" in mean and "SQ_BUSY_CU_CYCLES" in mean:
                 ent["mfma_busy_of_cu_busy"] = round(
                     mean["SQ_VALU_MFMA_BUSY_CYCLES"] / (4.0 * mean["SQ_BUSY_CU_CYCLES"]), 4)
