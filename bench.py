@@ -94,7 +94,7 @@ class Linear:
             _lib.check(rc, "pe_linear_forward")
 
 
-def time_steps(calls, steps, warmup, dev, repeats=1, steady=False):
+def time_steps(calls, steps, warmup, dev, repeats=1, steady=False, settle_s=0.0):
     """Exactly `steps` calls per timed sample (cycling through `calls`),
     captured in one HIP graph and replayed on the current stream; `warmup`
     untimed eager calls (at least one per call object) and one untimed replay
@@ -104,8 +104,10 @@ def time_steps(calls, steps, warmup, dev, repeats=1, steady=False):
     (steady=True): synchronize, an untimed replay, start event, the timed
     replay, end event -- the timed replay is queued while the untimed one
     runs, as in a serving loop, so the sample holds the calls alone; it still
-    holds exactly `steps` calls. Returns (median seconds per call, per-sample
-    list)."""
+    holds exactly `steps` calls. settle_s > 0 (the extras, not the headline):
+    before the samples, untimed replays worth about that much GPU time, so
+    that the clock has settled under the load. Returns (median seconds per
+    call, per-sample list)."""
     s = torch.cuda.Stream(device=dev)
     s.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(s):
@@ -117,8 +119,14 @@ def time_steps(calls, steps, warmup, dev, repeats=1, steady=False):
     with torch.cuda.graph(g, stream=s):
         for i in range(steps):
             calls[i % len(calls)]()
+    t_first = time.perf_counter()
     g.replay()
     torch.cuda.synchronize(dev)
+    if settle_s > 0:
+        per_replay = max(time.perf_counter() - t_first, 1e-6)
+        for _ in range(int(math.ceil(settle_s / per_replay))):
+            g.replay()
+        torch.cuda.synchronize(dev)
     samples = []
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     for _ in range(repeats):
@@ -135,9 +143,10 @@ def time_steps(calls, steps, warmup, dev, repeats=1, steady=False):
 
 def time_graph(calls, reps_per_graph, warmup, steps, dev):
     """Extras: about `steps` calls per sample in whole rounds over `calls`,
+    replayed until the clock has settled (about 80 ms of GPU time), then the
     median of five samples. Returns (seconds per call, calls per sample)."""
     n = max(len(calls), (steps // len(calls)) * len(calls))
-    t, _ = time_steps(calls, n, warmup, dev, repeats=5)
+    t, _ = time_steps(calls, n, warmup, dev, repeats=5, settle_s=0.08)
     return t, n
 
 
@@ -163,8 +172,8 @@ def kv_extra(dev, n_vec=1 << 21, d=128, bits=3):
     x = torch.randn(n_vec, d, device=dev, dtype=torch.bfloat16)
     packed, norms = qz.quantize(x)
     out = torch.empty_like(x)
-    t_q = time_eager(lambda: qz.quantize(x), 3, 20, dev)
-    t_d = time_eager(lambda: qz.dequantize(packed, norms, (n_vec, d), out=out), 3, 20, dev)
+    t_q, _, _ = time_settled(lambda: qz.quantize(x), dev)
+    t_d, _, _ = time_settled(lambda: qz.dequantize(packed, norms, (n_vec, d), out=out), dev)
     b = n_vec * (d * 2 + d * bits // 8 + 2)  # bf16 vectors + codes + bf16 norms
     res = {}
     for name, t in (("kv_quantize", t_q), ("kv_dequantize", t_d)):
