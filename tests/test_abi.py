@@ -65,6 +65,16 @@ def test_argument_errors_without_gpu_work():
     # unknown weight-format flag
     assert L.pe_linear_forward(16, 0, 1, 128, 128, 16, 4, 4, 16, 16, None, 16, None, 16, 8,
                                None, 0, None) == 3
+    # whole-row FWHT: n not a power of two, above 32768, bad dtype
+    assert L.pe_fwht_pow2(16, 2, 1, 96, 96, 16, 2, None) == 2
+    assert L.pe_fwht_pow2(16, 2, 1, 65536, 65536, 16, 2, None) == 2
+    assert L.pe_fwht_pow2(16, 7, 1, 64, 64, 16, 2, None) == 5
+    # measurement helpers: sizes that are not whole 16-byte units, misaligned, NULL
+    assert L.pe_stream_read(16, 100, 16, 0, None) == 2
+    assert L.pe_copy(16, 32, 100, None) == 2
+    assert L.pe_copy(16, 40, 128, None) == 4
+    assert L.pe_copy(None, 32, 128, None) == 1
+    assert L.pe_stream_read_sink_bytes(8192) == 1024 and L.pe_stream_read_sink_bytes(8193) == 2048
 
 
 def test_no_cpu_fallback():

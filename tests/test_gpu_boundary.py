@@ -458,3 +458,31 @@ def test_moe_apply_compiles_fullgraph():
         got = torch.compile(blk, fullgraph=True, backend="aot_eager")(x, logits)
         torch.cuda.synchronize()
         assert torch.equal(got, eager), f"given={given}"
+
+
+def test_measurement_helpers():
+    """pe_copy copies exactly (whole 16-byte units, a ragged tail of the last
+    workgroup); pe_stream_read folds every word it reads: on zero data the
+    fold is 0, so magic 0 makes every lane write its sink word and any other
+    magic none."""
+    from polarengine_vllm import _lib
+    say("measurement helpers")
+    L = _lib.lib()
+    st = _lib.stream_ptr(torch.device(DEV))
+    for nbytes in (16, 16384, (1 << 20) + 48):
+        src = torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device=DEV)
+        dst = torch.zeros_like(src)
+        _lib.check(L.pe_copy(dst.data_ptr(), src.data_ptr(), nbytes, st), "pe_copy")
+        torch.cuda.synchronize()
+        assert torch.equal(dst, src), nbytes
+        zero = torch.zeros(nbytes, dtype=torch.uint8, device=DEV)
+        sink = torch.full((L.pe_stream_read_sink_bytes(nbytes) // 4,), 7, dtype=torch.int32,
+                          device=DEV)
+        _lib.check(L.pe_stream_read(zero.data_ptr(), nbytes, sink.data_ptr(), 0x9E3779B9, st),
+                   "pe_stream_read")
+        torch.cuda.synchronize()
+        assert bool((sink == 7).all())
+        _lib.check(L.pe_stream_read(zero.data_ptr(), nbytes, sink.data_ptr(), 0, st),
+                   "pe_stream_read")
+        torch.cuda.synchronize()
+        assert bool((sink == 0).all())
