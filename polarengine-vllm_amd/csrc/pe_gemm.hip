@@ -175,8 +175,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
   const int tm = wid % tiles_m, tn = wid / tiles_m;
   const int m0 = tm * BM, n0 = tn * BN;
 
-  if constexpr (NIB) fill_codebook<TBL_NIB_H2>(0, ct, n_levels, tbl_entries, NT / 64);
-  else fill_codebook<TBL_F16>(0, ct, n_levels, tbl_entries, NT / 64);
+  // codebook values now, the table once the first A and B loads are issued
+  float cbr[4];
+  codebook_regs(cbr, ct, n_levels);
 
   // K range of this workgroup: gridDim.z groups split the 128-blocks; with
   // more than one, each writes fp32 partial sums to its slab [M][ldy] of y
@@ -226,6 +227,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
   load_atile<KA>(ar, a_src, 0);
   load_btile<NIB, TNW>(b0, b_row, n_row, 0, lay.c_blk, lay.n_blk);
   load_btile<NIB, TNW>(b1, b_row, n_row, 1, lay.c_blk, lay.n_blk);
+  if constexpr (NIB) fill_codebook_from<TBL_NIB_H2>(0, cbr, tbl_entries, NT / 64);
+  else fill_codebook_from<TBL_F16>(0, cbr, tbl_entries, NT / 64);
   store_atile<KA>(abuf, ar, a_dst);
   load_atile<KA>(ar, a_src, 1);
   __syncthreads();
@@ -466,8 +469,10 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
   const int tm = wid % tiles_m, tn = wid / tiles_m;
   const int m0 = tm * BM, n0 = tn * BN;
 
-  if constexpr (NIB) fill_codebook<TBL_NIB_H2>(0, ct, n_levels, tbl_entries, NT / 64);
-  else fill_codebook<TBL_F16>(0, ct, n_levels, tbl_entries, NT / 64);
+  // codebook values now, the table once the first A and B loads are issued
+  // (the values' round trip overlaps theirs)
+  float cbr[4];
+  codebook_regs(cbr, ct, n_levels);
   const uint32_t abuf = (uint32_t)tbl_entries * 256u;
 
   // K range of this workgroup, in pairs of 128-blocks (the loop takes four
@@ -543,6 +548,8 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
   ldb(slot[0], 0);
   ldb(slot[1], 1);
   ldb(slot[2], 2);
+  if constexpr (NIB) fill_codebook_from<TBL_NIB_H2>(0, cbr, tbl_entries, NT / 64);
+  else fill_codebook_from<TBL_F16>(0, cbr, tbl_entries, NT / 64);
   __syncthreads();  // codebook table written
   sta(abuf, stg[0]);
   sta(abuf + ABUF, stg[1]);

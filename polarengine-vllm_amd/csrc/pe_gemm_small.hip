@@ -374,10 +374,44 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
     src.voff_norms[j] = (uint32_t)(a.lay.norms_off(n) * 2);
   }
 
-  if constexpr (NIB)
-    fill_codebook<TBL_NIB_H2>(0, a.ct, a.n_levels, tbl_entries, kMoeWaves);
-  else
-    fill_codebook<TBL_F16>(0, a.ct, a.n_levels, tbl_entries, kMoeWaves);
+  // codebook table from wave-uniform loads of ct (scalar loads: they do not
+  // queue behind the vector loads); entry (hi << 4) | lo = half2(ct[lo],
+  // ct[hi]) for nibbles (wave w writes hi = w, w + 8), fp16(ct[e]) for int8
+  // (wave w writes entries 16 w .. 16 w + 15 and 16 (w + 8) ..); every lane
+  // its own copy. Entries past n_levels are never read (codes are masked).
+  (void)tbl_entries;
+  {
+    const float* __restrict__ ctp = a.ct;
+    const int nl = a.n_levels, last = nl - 1;
+    if constexpr (NIB) {
+      uint32_t h[16];
+#pragma unroll
+      for (int lo = 0; lo < 16; ++lo) h[lo] = f2h_bits(ctp[lo < nl ? lo : last]);
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int hi = wave + kMoeWaves * hh;
+        if (hi < nl) {
+          uint32_t chi = h[0];
+#pragma unroll
+          for (int k = 1; k < 16; ++k) chi = hi == k ? h[k] : chi;
+          const uint32_t base = ((uint32_t)hi << 12) | lane4;
+#pragma unroll
+          for (int lo = 0; lo < 16; ++lo)
+            if (lo < nl) lds_st32(base + ((uint32_t)lo << 8), h[lo] | (chi << 16));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int chunk = wave + kMoeWaves * hh;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const int e = chunk * 16 + k;
+          if (e < nl) lds_st32(((uint32_t)e << 8) | lane4, f2h_bits(ctp[e]));
+        }
+      }
+    }
+  }
 
   // staging role of this thread: rows sr + 32 k (k < SR), 16-byte chunk sc of
   // the 256-byte block row
@@ -414,24 +448,27 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(SmallArgs a, uint
 #pragma unroll
       for (int j = 0; j < NT; ++j) acc[i][j] = float4v{0.f, 0.f, 0.f, 0.f};
 
+    // activation FIFO: block q is loaded D blocks before it is staged and
+    // waits in sreg[q % D]. Blocks 0 .. D - 1 are loaded before the weight
+    // ring, so that staging block 0 waits for its own rows only (loads
+    // complete in issue order); block D after block 0 is staged.
+    u32x4v sreg[D][SR];
+#pragma unroll
+    for (int q = 0; q < D; ++q)
+#pragma unroll
+      for (int k = 0; k < SR; ++k) sreg[q][k] = lda(k, q);
+    __builtin_amdgcn_sched_barrier(0);
     MoeBlk<NT> ring[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       moe_load_w<NIB, NT>(ring[d], src, d, a.nb, a.lay);
       __builtin_amdgcn_sched_barrier(0);
     }
-    // activation FIFO: block q is loaded D blocks before it is staged and
-    // waits in sreg[q % D]
-    u32x4v sreg[D][SR];
 #pragma unroll
     for (int k = 0; k < SR; ++k) {
-      sreg[0][k] = lda(k, 0);
       lds_st128(abuf + sdst[k], sreg[0][k]);
+      sreg[0][k] = lda(k, D);
     }
-#pragma unroll
-    for (int q = 1; q <= D; ++q)
-#pragma unroll
-      for (int k = 0; k < SR; ++k) sreg[q % D][k] = lda(k, q);
     __syncthreads();  // codebook table and stage 0 written
 
     // A row of this lane in m-tile i: activation row 16 i + l16 of the stage.

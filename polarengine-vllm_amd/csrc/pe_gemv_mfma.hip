@@ -13,8 +13,9 @@
 //
 //  * one workgroup of NW = TN x KS waves per CU-sized share of rows: TN
 //    n-tiles of 16 weight rows (TN chosen so the grid covers the CUs once),
-//    KS contiguous K-slices of 128-blocks per tile; the slices combine
-//    through LDS at the end;
+//    KS K-slices of 128-blocks per tile, interleaved (slice s takes blocks
+//    s, s + KS, ..: the KS waves of a tile read neighbouring blocks at each
+//    step); the slices combine through LDS at the end;
 //  * the prologue never waits behind the weight stream: each wave first
 //    issues its activation loads and takes the codebook (kernel arguments,
 //    or scalar loads of ct that do not queue behind the vector weight
@@ -204,7 +205,7 @@ __device__ __forceinline__ void dec_xform_mfma(const u32x4v (&xq)[8], uint32_t s
 // x: raw fp16 activations [M, K] (XRAW) or pair-f16 x_tf [M][nb][64] (else),
 // row stride ldx fp16 elements. The workgroup covers TN 16-row tiles with
 // NW = TN * KS waves: wave w works on tile w % TN over the K-slice w / TN
-// (contiguous 128-blocks), streaming it D blocks deep. XC: activation
+// (blocks w / TN, w / TN + KS, ..), streaming it D blocks deep. XC: activation
 // registers per lane. SPLIT: the K blocks are divided into gridDim.y groups,
 // blockIdx.y's group only (its activations alone in LDS); each workgroup
 // writes fp32 partial sums part[blockIdx.y][M][N], and the last of the
@@ -235,9 +236,9 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
   // K blocks of this workgroup: [kb0, kb0 + nbr)
   const int kb0 = SPLIT ? (int)((int64_t)nb * blockIdx.y / gridDim.y) : 0;
   const int nbr = SPLIT ? (int)((int64_t)nb * (blockIdx.y + 1) / gridDim.y) - kb0 : nb;
-  const int b_begin = kb0 + (int)((int64_t)nbr * ks / KS);
-  const int b_end = kb0 + (int)((int64_t)nbr * (ks + 1) / KS);
-  const int nbw = b_end - b_begin;  // blocks of this wave (uniform)
+  // interleaved slices: block i of this wave is kb0 + ks + KS i
+  const int b_begin = kb0 + ks;
+  const int nbw = nbr > ks ? (nbr - ks + KS - 1) / KS : 0;  // blocks of this wave (uniform)
 
   // weight row of this lane (clamped; clamped rows are never stored)
   DecSrc src;
@@ -324,7 +325,7 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
   DecBlk<NIB, 1> ring[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) {
-    dec_load<NIB, 1>(ring[d], src, b_begin + d, d < nbw, c_blk, n_blk2);
+    dec_load<NIB, 1>(ring[d], src, b_begin + KS * d, d < nbw, c_blk, n_blk2);
     __builtin_amdgcn_sched_barrier(0);
   }
 
@@ -441,8 +442,8 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
   for (int i = 0; i < nbw; i += D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      if (i + d < nbw) do_block(ring[d], b_begin + i + d);
-      dec_load<NIB, 1>(ring[d], src, b_begin + i + d + D, i + d + D < nbw, c_blk, n_blk2);
+      if (i + d < nbw) do_block(ring[d], b_begin + KS * (i + d));
+      dec_load<NIB, 1>(ring[d], src, b_begin + KS * (i + d + D), i + d + D < nbw, c_blk, n_blk2);
       __builtin_amdgcn_sched_barrier(0);
     }
   }

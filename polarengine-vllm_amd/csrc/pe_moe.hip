@@ -258,11 +258,17 @@ __device__ void moe_align_block(const FrontArgs& a) {
     }
   };
   constexpr int64_t kChunk = (int64_t)kFrontThreads * kAlignBatch;
+  // one chunk (P <= 2048: T * top_k of a decode batch): the ids stay in
+  // registers for the scatter pass, one memory round trip fewer
+  const bool one = P <= kChunk;
+  int e1[kAlignBatch];
   for (int e = tid; e < E; e += kFrontThreads) cnt[e] = 0;
   __syncthreads();
   for (int64_t p0 = 0; p0 < P; p0 += kChunk) {
     int e[kAlignBatch];
     load_ids(p0, e);
+#pragma unroll
+    for (int u = 0; u < kAlignBatch; ++u) e1[u] = e[u];
 #pragma unroll
     for (int u = 0; u < kAlignBatch; ++u)
       if (p0 + tid + (int64_t)kFrontThreads * u < P && e[u] >= 0 && e[u] < E) atomicAdd(&cnt[e[u]], 1);
@@ -289,7 +295,12 @@ __device__ void moe_align_block(const FrontArgs& a) {
   for (int e = tid; e <= E; e += kFrontThreads) a.offsets[e] = base[e];
   for (int64_t p0 = 0; p0 < P; p0 += kChunk) {
     int e[kAlignBatch];
-    load_ids(p0, e);
+    if (one) {  // uniform
+#pragma unroll
+      for (int u = 0; u < kAlignBatch; ++u) e[u] = e1[u];
+    } else {
+      load_ids(p0, e);
+    }
 #pragma unroll
     for (int u = 0; u < kAlignBatch; ++u) {
       const int64_t p = p0 + tid + (int64_t)kFrontThreads * u;
