@@ -178,11 +178,11 @@ constexpr int kSplitBatch = 16;
 // FWHT-128 of the wave's 32 items on the matrix cores, stored as pair f16
 // into each item's 256-byte LDS slot: pair p = 32 mp + 8 q + 4 h + r holds
 // positions p (m-block mp) and p + 64 (m-block mp + 2), so each lane writes
-// four 16-byte runs per m-block pair. Every lane takes part; only live lanes
-// store.
+// four 16-byte runs per m-block pair (16-byte chunk c of the slot stored at
+// chunk c ^ sw). Every lane takes part; only live lanes store.
 template <bool BF>
 __device__ __forceinline__ void dec_xform_mfma(const u32x4v (&xq)[8], uint32_t slot, bool live,
-                                               int lane) {
+                                               int lane, uint32_t sw) {
   const H128Signs sg = h128_signs<BF ? 0x3F803F80u : 0x3C003C00u>(lane);
   const uint32_t h = (uint32_t)lane >> 5;
 #pragma unroll
@@ -196,7 +196,7 @@ __device__ __forceinline__ void dec_xform_mfma(const u32x4v (&xq)[8], uint32_t s
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           w[r] = pack_h2(a0[4 * q + r] * kInvSqrt128, a1[4 * q + r] * kInvSqrt128);
-        lds_st128(slot + 4u * (32u * mp + 8u * q + 4u * h), w);
+        lds_st128(slot + 16u * ((8u * mp + 2u * q + h) ^ sw), w);
       }
     }
   }
@@ -215,7 +215,7 @@ __device__ __forceinline__ void dec_xform_mfma(const u32x4v (&xq)[8], uint32_t s
 // matrix cores, 32 (row, block) items per wave (dec_xform_mfma), instead of
 // one item per 16-lane group on the VALU.
 template <bool NIB, int TN, int KS, bool XRAW, bool MASK, int XC, int D, bool CTV, bool SPLIT,
-          int MTD = 1, bool XMF = false>
+          int MTD = 1, bool XMF = false, bool SWZ = false>
 __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
     const float* __restrict__ ct, int n_levels, uint32_t code_mask,
@@ -268,8 +268,11 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
   // LDS bytes per activation row: 256 per block plus 16, so that the 16 rows
   // one ds_read_b128 phase reads (lanes l16 = rows) start in 16 different
   // bank groups; without the pad every row began in the same bank (row sizes
-  // are multiples of 256 B) and M > 1 reads conflicted 16 ways
-  const uint32_t xrow_b = (uint32_t)nbr * 256u + 16u;
+  // are multiples of 256 B) and M > 1 reads conflicted 16 ways. SWZ (where
+  // the padded rows do not fit, e.g. M = 4 at K = 12288 beside the 64 KB
+  // table): no pad, 16-byte chunk c of row m stored at chunk c ^ (m & 15) of
+  // its block, which spreads a phase's rows over the banks the same way.
+  const uint32_t xrow_b = (uint32_t)nbr * 256u + (SWZ ? 0u : 16u);
   const int gi = wave * 4 + g;
   int it_m, it_b;
   {
@@ -338,8 +341,9 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
   if constexpr (XM) {
     if (32 * wave < nitems) {  // uniform
       const uint32_t slot = xs_addr + (uint32_t)q_m * xrow_b + (uint32_t)q_b * 256u;
-      if (xbf) dec_xform_mfma<true>(xq, slot, q_live, lane);
-      else dec_xform_mfma<false>(xq, slot, q_live, lane);
+      const uint32_t sw = SWZ ? (uint32_t)q_m & 15u : 0u;
+      if (xbf) dec_xform_mfma<true>(xq, slot, q_live, lane, sw);
+      else dec_xform_mfma<false>(xq, slot, q_live, lane, sw);
     }
   } else {
     int m = it_m, b = it_b;
@@ -379,9 +383,9 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
             w = u32x4v{pack_h2(o[4], v[4]), pack_h2(o[5], v[5]), pack_h2(o[6], v[6]),
                        pack_h2(o[7], v[7])};
           }
-          lds_st128(blk + p0 * 4u, w);
+          lds_st128(blk + 16u * ((p0 >> 2) ^ (SWZ ? (uint32_t)m & 15u : 0u)), w);
         } else {
-          lds_st128(blk + (uint32_t)l16 * 16u, xr[i]);
+          lds_st128(blk + 16u * ((uint32_t)l16 ^ (SWZ ? (uint32_t)m & 15u : 0u)), xr[i]);
         }
       }
       b += 4 * NW;
@@ -404,18 +408,22 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
   // M-1; they only feed D rows >= M, which are never stored
   // (item (m, b) of the group sits at m * xrow_b + (b - kb0) * 256: the base
   // wraps below zero and comes back with b >= kb0)
-  uint32_t arow[MTD];
+  uint32_t arow[MTD], achk[MTD][4];  // SWZ: byte offset of chunk 4 g + t in the row's blocks
 #pragma unroll
   for (int i = 0; i < MTD; ++i) {
     const int r = 16 * i + l16;
-    arow[i] = xs_addr + (uint32_t)(r < M ? r : M - 1) * xrow_b - (uint32_t)kb0 * 256u + 64u * g;
+    const uint32_t rr = (uint32_t)(r < M ? r : M - 1);
+    arow[i] = xs_addr + rr * xrow_b - (uint32_t)kb0 * 256u + (SWZ ? 0u : 64u * g);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      achk[i][t] = SWZ ? 16u * ((4u * (uint32_t)g + t) ^ (rr & 15u)) : 16u * t;
   }
   auto do_block = [&](const DecBlk<NIB, 1>& k, int b) {
     u32x4v af[MTD][4];
 #pragma unroll
     for (int i = 0; i < MTD; ++i)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) af[i][t] = lds_ld128(arow[i] + (uint32_t)b * 256u + 16u * t);
+      for (int t = 0; t < 4; ++t) af[i][t] = lds_ld128(arow[i] + (uint32_t)b * 256u + achk[i][t]);
     half8v bf[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -623,23 +631,26 @@ static int dec_xc(int M, int nb, int nw) { return (M * nb + 4 * nw - 1) / (4 * n
 // 16-row m-tiles per MFMA pass: 1 (M <= 16) or 2 (M <= 32 = kDecMaxRows)
 static int dec_mtd(int M) { return M <= 16 ? 1 : 2; }
 
-static size_t dec_lds(bool nibble, int M, int nb, int n_levels, int nw) {
-  size_t lds = (size_t)table_entries(nibble, n_levels) * 256 + (size_t)M * (nb * 256 + 16);
+// LDS bytes: the table and M activation rows of nb blocks, 16 bytes of pad per
+// row unless the rows are swizzled (pad = false, the smaller layout, which
+// the fit checks assume; the launch pads where that fits)
+static size_t dec_lds(bool nibble, int M, int nb, int n_levels, int nw, bool pad = false) {
+  size_t lds = (size_t)table_entries(nibble, n_levels) * 256 + (size_t)M * (nb * 256 + (pad ? 16 : 0));
   const size_t red = (size_t)nw * dec_mtd(M) * 64 * 16 + 16;  // + the K split's last-group flag
   return lds < red ? red : lds;
 }
 
-template <bool NIB, int TN, bool XRAW, bool MASK, int XC, bool CTV, bool SPLIT = false, int MTD = 1,
-          bool XMF = false>
-static int launch_dec(const DecArgs& a, hipStream_t st, int groups = 1) {
+template <bool NIB, int TN, bool XRAW, bool MASK, int XC, bool CTV, bool SPLIT, int MTD, bool XMF,
+          bool SWZ>
+static int launch_dec_k(const DecArgs& a, hipStream_t st, int groups) {
   constexpr int KS = dec_ks<TN>(), NW = TN * KS;
   // blocks in flight per wave (nibble 1 KB, int8 2 KB each); deeper rings
   // measured slower (3 -> 8: 7.6 -> 8.8 us on Q4 12288 x 4096)
   constexpr int D = NIB ? 3 : 2;
-  auto kern = gemv_mfma_kernel<NIB, TN, KS, XRAW, MASK, XC, D, CTV, SPLIT, MTD, XMF>;
+  auto kern = gemv_mfma_kernel<NIB, TN, KS, XRAW, MASK, XC, D, CTV, SPLIT, MTD, XMF, SWZ>;
   if (dec_mtd(a.M) != MTD) return PE_ERR_DIMS;
   const int nbg = (a.nb + groups - 1) / groups;  // most blocks of one group
-  const size_t lds = dec_lds(NIB, a.M, nbg, a.n_levels, NW);
+  const size_t lds = dec_lds(NIB, a.M, nbg, a.n_levels, NW, !SWZ);
   // XMF: 32 items per wave (the same capacity as XC = 8: 8 per 16-lane group)
   if (lds > 160 * 1024 || dec_xc(a.M, nbg, NW) > (XMF ? 8 : XC)) return PE_ERR_DIMS;
   static const bool attr_ok = [&] {
@@ -666,6 +677,21 @@ static int launch_dec(const DecArgs& a, hipStream_t st, int groups = 1) {
       a.N, a.nb, xs_addr, a.lay, ctv, (a.xbf ? 1 : 0) | (a.ybf ? 2 : 0),
       SPLIT ? reinterpret_cast<float*>(a.ws) : nullptr, SPLIT ? a.cnt : nullptr);
   return launch_status();
+}
+
+// Padded activation rows where they fit; swizzled ones otherwise (only the
+// forms holding up to 8 items per 16-lane group can need it: 384 items of
+// 256 B beside a 64 KB table fill the LDS exactly)
+template <bool NIB, int TN, bool XRAW, bool MASK, int XC, bool CTV, bool SPLIT = false, int MTD = 1,
+          bool XMF = false>
+static int launch_dec(const DecArgs& a, hipStream_t st, int groups = 1) {
+  if constexpr (XC == 8 || XMF) {
+    constexpr int NW = TN * dec_ks<TN>();
+    const int nbg = (a.nb + groups - 1) / groups;
+    if (dec_lds(NIB, a.M, nbg, a.n_levels, NW, true) > 160 * 1024)
+      return launch_dec_k<NIB, TN, XRAW, MASK, XC, CTV, SPLIT, MTD, XMF, true>(a, st, groups);
+  }
+  return launch_dec_k<NIB, TN, XRAW, MASK, XC, CTV, SPLIT, MTD, XMF, false>(a, st, groups);
 }
 
 // activation registers per lane from which the transform moves to the

@@ -136,6 +136,8 @@ XTF_CASES = [
     (16, 200, 4096, "decode GEMV (K split over workgroups for the larger tables)"),
     (24, 64, 2048, "decode GEMV, two m-tiles, K split"),
     (32, 160, 1024, "decode GEMV, two m-tiles, K split"),
+    (4, 96, 12288, "decode GEMV, 384 items beside a 64 KB table: swizzled rows"),
+    (12, 80, 4096, "decode GEMV, 384 items beside a 64 KB table: swizzled rows"),
     (40, 200, 384, "small-M MFMA kernel (odd block count: no GEMM K split)"),
     (48, 4096, 256, "small-M MFMA kernel (two blocks: no K split)"),
     (64, 4096, 1024, "four-wave GEMM, 64-row tiles, K split + ordered reduction"),
@@ -205,8 +207,11 @@ def _hadamard_row_inputs(m, kp, ks):
     return x
 
 
+# (4, 96, 12288) and (12, 80, 4096): 384 items, which beside a 64 KB table
+# (4-bit and int8 codes) fill the LDS only without the per-row pad, so the
+# activation rows are swizzled instead
 RAW_CASES = [(1, 80, 1024), (1, 4096, 4096), (4, 96, 2048), (16, 200, 4096), (24, 64, 2048),
-             (32, 160, 1024)]
+             (32, 160, 1024), (4, 96, 12288), (12, 80, 4096)]
 
 
 @pytest.mark.parametrize("tiled", [True, False], ids=["tile16", "rowmajor"])
