@@ -169,9 +169,10 @@ class PolarQuantMoEMethod:
         if custom_routing_function is None:
             # routing and experts in one call (the routing shares the first launch)
             t = x.numel() // layer.hidden_size
+            # (the logits' own width, not -1: with zero tokens -1 is ambiguous)
             lg, bias, scoring, n_group, t_group = self._routing_args(
-                router_logits.reshape(t, -1), e, scoring_func, e_score_correction_bias,
-                use_grouped_topk, num_expert_group, topk_group)
+                router_logits.reshape(t, router_logits.shape[-1]), e, scoring_func,
+                e_score_correction_bias, use_grouped_topk, num_expert_group, topk_group)
             route = [top_k, int(bool(renormalize)), scoring, n_group, t_group]
             if compiling:
                 return torch.ops.polarengine.moe_routed(x, lg, bias, *wts, route, meta)

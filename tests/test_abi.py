@@ -75,6 +75,12 @@ def test_argument_errors_without_gpu_work():
     assert L.pe_copy(16, 40, 128, None) == 4
     assert L.pe_copy(None, 32, 128, None) == 1
     assert L.pe_stream_read_sink_bytes(8192) == 1024 and L.pe_stream_read_sink_bytes(8193) == 2048
+    # zero rows: valid arguments, nothing to do, nothing touched (the pointers
+    # below are aligned placeholders, never dereferenced)
+    assert L.pe_linear_forward(16, 0, 0, 128, 128, 16, 4, 1, 16, 16, None, 16, None, 16, 8,
+                               None, 0, None) == 0
+    assert L.pe_linear_forward_xtf(16, 0, 128, 16, 4, 1, 16, 16, None, 16, None, 0, 16, 8,
+                                   None, 0, None) == 0
 
 
 def test_no_cpu_fallback():

@@ -486,3 +486,64 @@ def test_measurement_helpers():
                    "pe_stream_read")
         torch.cuda.synchronize()
         assert bool((sink == 0).all())
+
+
+# ---------------------------------------------------------------------------
+# empty batches: a serving engine can hand a layer zero tokens
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("shape", [(0, 512), (3, 0, 512)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_apply_empty_batch(shape, dtype):
+    """apply on zero rows returns an empty result of the right shape and
+    dtype, launches nothing, and the layer still computes right afterwards."""
+    from polarengine_vllm.linear_method import PolarQuantLinearMethod
+    say(f"empty batch apply {shape} {dtype}")
+    n, k, bits = 256, 512, 4
+    codes, norms, ct = rand_layer(np.random.default_rng(640), n, k, bits)
+    layer = torch.nn.Module()
+    meth = PolarQuantLinearMethod(128, bits)
+    meth.create_weights(layer, k, [n], k, n, dtype)
+    layer.to(DEV)
+    layer.codes.copy_(to_dev(codes))
+    layer.norms.copy_(to_dev(norms))
+    meth.process_weights_after_loading(layer)
+    y0 = meth.apply(layer, torch.empty(shape, dtype=dtype, device=DEV), None)
+    torch.cuda.synchronize()
+    assert y0.shape == shape[:-1] + (n,) and y0.dtype == dtype
+    x = O.seeded_normal((2, k), 1.0, 641, np.float32)
+    xd = to_dev(x, dtype)
+    y = meth.apply(layer, xd, None)
+    want = O.linear_apply(xd.float().cpu().numpy(), codes, norms, ct, k)
+    check_close(y.float().cpu().numpy(), want.astype(np.float32), "after an empty batch")
+    meth._fwht_cache.clear()
+
+
+@pytest.mark.parametrize("routed", [True, False], ids=["logits", "given_ids"])
+def test_moe_apply_empty_batch(routed):
+    """The MoE method on zero tokens: an empty result, nothing launched, and
+    the next call is unaffected (the routing counters are left as they were)."""
+    from test_gpu_kernels import _moe_layer
+    say(f"empty batch moe routed={routed}")
+    meth, layer, (w13, w2) = _moe_layer(np.random.default_rng(642), 16, 512, 384, 3, 4)
+
+    def call(x, logits):
+        if routed:
+            return meth.apply(layer, x, logits, 4, True)
+
+        def fixed(hidden_states, gating_output, topk, renormalize):
+            w, ids = O.moe_route(gating_output.float().cpu().numpy(), topk, renormalize)
+            return to_dev(w), to_dev(ids.astype(np.int32))
+        return meth.apply(layer, x, logits, 4, True, custom_routing_function=fixed)
+
+    y0 = call(torch.empty(0, 512, dtype=torch.float16, device=DEV),
+              torch.empty(0, 16, dtype=torch.float32, device=DEV))
+    torch.cuda.synchronize()
+    assert y0.shape == (0, 512) and y0.dtype == torch.float16
+    x = O.seeded_normal((9, 512), 1.0, 643, np.float32)
+    logits = O.seeded_normal((9, 16), 1.0, 644, np.float32)
+    xd = to_dev(x, torch.float16)
+    y = call(xd, to_dev(logits))
+    w_ref, ids_ref = O.moe_route(logits, 4, True)
+    want = O.moe_forward(xd.float().cpu().numpy(), w_ref, ids_ref, w13, w2).astype(np.float32)
+    check_close(y.float().cpu().numpy(), want, f"moe after an empty batch routed={routed}")
