@@ -547,3 +547,30 @@ def test_moe_apply_empty_batch(routed):
     w_ref, ids_ref = O.moe_route(logits, 4, True)
     want = O.moe_forward(xd.float().cpu().numpy(), w_ref, ids_ref, w13, w2).astype(np.float32)
     check_close(y.float().cpu().numpy(), want, f"moe after an empty batch routed={routed}")
+
+
+@pytest.mark.parametrize("m", [4, 64])
+def test_apply_strided_input(m):
+    """A column slice of a wider tensor (row stride above in_f, as a split of
+    a fused projection's output is) gives the same result as its copy."""
+    from polarengine_vllm.linear_method import PolarQuantLinearMethod
+    say(f"strided input apply m={m}")
+    n, k, bits = 384, 512, 4
+    codes, norms, ct = rand_layer(np.random.default_rng(650 + m), n, k, bits)
+    layer = torch.nn.Module()
+    meth = PolarQuantLinearMethod(128, bits)
+    meth.create_weights(layer, k, [n], k, n, torch.float16)
+    layer.to(DEV)
+    layer.codes.copy_(to_dev(codes))
+    layer.norms.copy_(to_dev(norms))
+    meth.process_weights_after_loading(layer)
+    big = to_dev(O.seeded_normal((m, k + 192), 1.0, 651 + m, np.float32), torch.float16)
+    x = big[:, 64:64 + k]
+    assert not x.is_contiguous()
+    y = meth.apply(layer, x, None)
+    y_copy = meth.apply(layer, x.contiguous(), None)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_copy)
+    want = O.linear_apply(x.float().cpu().numpy(), codes, norms, ct, k)
+    check_close(y.float().cpu().numpy(), want.astype(np.float32), f"strided m={m}")
+    meth._fwht_cache.clear()
