@@ -573,6 +573,9 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       Frag4<NIB, TMW, NTW> fn;
+      // this slab's operands (issued one slab ago) are in: wait for them
+      // before the next slab's reads go out
+      __builtin_amdgcn_s_waitcnt(0xc07f);
       if (t < 3) issue_frag4<NIB, TMW, NTW, MASK>(fn, abuf + bcur + a_off[t + 1], t + 1, slot[S], lane4, code_mask);
       else issue_frag4<NIB, TMW, NTW, MASK>(fn, abuf + bnext + a_off[0], 0, slot[(S + 1) & 3], lane4, code_mask);
       // keep the next slab's reads ahead of this slab's MFMAs
