@@ -482,8 +482,15 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
   const int nbz = 2 * (int)((int64_t)(nb / 2) * (blockIdx.z + 1) / gridDim.z) - kb0;
   y = reinterpret_cast<char*>(y) + (int64_t)blockIdx.z * M * ldy * (OM == OM_F16 ? 2 : 4);
 
+  // Loads through buffer resources based at this workgroup's first row of x
+  // and first column of the weights: per-lane offsets in VGPRs, the K
+  // position in the scalar offset (no 64-bit address arithmetic in the K
+  // loop). Every extent is below 2 GiB (host check).
   const int64_t xrow_u32 = (int64_t)nb * 64;
-  const uint32_t* a_src[KA];
+  const int mlast = (m0 + BM <= M ? m0 + BM : M) - 1;
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(xp + (int64_t)m0 * xrow_u32), (short)0, (int)((mlast - m0 + 1) * xrow_u32 * 4), 0x00020000);
+  uint32_t a_voff[KA];
   uint32_t a_dst[KA];
 #pragma unroll
   for (int i = 0; i < KA; ++i) {
@@ -491,17 +498,24 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
     const int r = q >> 3, c = q & 7;
     int m = m0 + r;
     if (m >= M) m = M - 1;  // clamped rows feed discarded outputs only
-    a_src[i] = xp + (int64_t)m * xrow_u32 + (int64_t)kb0 * 64 + c * 4;
+    a_voff[i] = (uint32_t)(((int64_t)(m - m0) * xrow_u32 + c * 4) * 4);
     a_dst[i] = (uint32_t)(r * kARow4 + (((uint32_t)c ^ a4_swz(r)) << 4));
   }
-  const uint8_t* b_row[NTW];
-  const uint16_t* n_row[NTW];
+  const int nlast = (n0 + BN <= N ? n0 + BN : N) - 1;
+  const int64_t cb0 = lay.codes_off(n0), nb0 = lay.norms_off(n0);
+  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(codes + cb0), (short)0,
+      (int)(lay.codes_off(nlast) + (int64_t)(nb - 1) * lay.c_blk + (NIB ? 64 : 128) - cb0), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(norms + nb0), (short)0, (int)((lay.norms_off(nlast) + (int64_t)(nb - 1) * lay.n_blk + 1 - nb0) * 2),
+      0x00020000);
+  uint32_t b_voff[NTW], n_voff[NTW];
 #pragma unroll
   for (int j = 0; j < NTW; ++j) {
     int n = n0 + wave * 32 * NTW + j * 32 + l32;
     if (n >= N) n = N - 1;
-    b_row[j] = codes + lay.codes_off(n) + 16 * h + (int64_t)kb0 * lay.c_blk;
-    n_row[j] = norms + lay.norms_off(n) + (int64_t)kb0 * lay.n_blk;
+    b_voff[j] = (uint32_t)(lay.codes_off(n) - cb0) + 16 * h;
+    n_voff[j] = (uint32_t)((lay.norms_off(n) - nb0) * 2);
   }
   uint32_t a_off[4];  // lane's row l32, chunk 4h + t, swizzled
 #pragma unroll
@@ -511,20 +525,22 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
   // loads past the last half-block re-read it (in bounds, never used)
   auto ldb = [&](BSlot4<NIB, NTW>& sl, int kt) {
     kt = kt < nkt ? kt : nkt - 1;
-    const int bk = kt >> 1, half = kt & 1;
+    const int bk = kb0 + (kt >> 1), half = kt & 1;
+    const int sc = bk * (int)lay.c_blk + half * 32, sn = bk * (int)lay.n_blk * 2;
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
-      const uint8_t* pc = b_row[j] + bk * lay.c_blk + half * 32;
-      sl.lo[j] = *reinterpret_cast<const u32x4v*>(pc);
-      if constexpr (!NIB) sl.hi[j] = *reinterpret_cast<const u32x4v*>(pc + 64);
-      sl.nrm[j] = (uint32_t)n_row[j][bk * lay.n_blk];
+      sl.lo[j] = __builtin_bit_cast(u32x4v, __builtin_amdgcn_raw_buffer_load_b128(rc, b_voff[j], sc, 0));
+      if constexpr (!NIB)
+        sl.hi[j] = __builtin_bit_cast(u32x4v, __builtin_amdgcn_raw_buffer_load_b128(rc, b_voff[j], sc + 64, 0));
+      sl.nrm[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rn, n_voff[j], sn, 0);
     }
   };
   auto lda = [&](u32x4v (&rg)[KA], int kt) {
     kt = kt < nkt ? kt : nkt - 1;
-    const int off = (kt >> 1) * 64 + (kt & 1) * 32;
+    const int sa = (kb0 * 64 + (kt >> 1) * 64 + (kt & 1) * 32) * 4;
 #pragma unroll
-    for (int i = 0; i < KA; ++i) rg[i] = *reinterpret_cast<const u32x4v*>(a_src[i] + off);
+    for (int i = 0; i < KA; ++i)
+      rg[i] = __builtin_bit_cast(u32x4v, __builtin_amdgcn_raw_buffer_load_b128(ra, a_voff[i], sa, 0));
   };
   auto sta = [&](uint32_t buf, const u32x4v (&rg)[KA]) {
 #pragma unroll
@@ -620,6 +636,10 @@ static int launch_gemm4_t(const GemmArgs& a, hipStream_t st, int ksplit = 1) {
   const int tiles_n = (a.N + BN - 1) / BN;
   const int64_t total = (int64_t)tiles_m * tiles_n;
   if (total > INT32_MAX) return PE_ERR_DIMS;
+  // one workgroup's rows of x and columns of codes and norms are addressed by
+  // 32-bit buffer offsets
+  const int64_t w_span = a.lay.codes_off(BN - 1) + (int64_t)a.nb * a.lay.c_blk + 128;
+  if ((int64_t)BM * a.nb * 256 >= ((int64_t)1 << 31) || w_span >= ((int64_t)1 << 31)) return PE_ERR_DIMS;
   const uint8_t mb = NIB ? (uint8_t)((a.n_levels - 1) * 0x11) : (uint8_t)(a.n_levels - 1);
   // 16-byte stores need aligned rows; with a K split, aligned slab starts too
   const int vec_ok = ((uintptr_t)a.y % 16 == 0) && ((a.ldy * (int64_t)ES) % 16 == 0) &&
