@@ -204,8 +204,10 @@ __device__ __forceinline__ void dec_xform_mfma(const u32x4v (&xq)[8], uint32_t s
 
 // x: raw fp16 activations [M, K] (XRAW) or pair-f16 x_tf [M][nb][64] (else),
 // row stride ldx fp16 elements. The workgroup covers TN 16-row tiles with
-// NW = TN * KS waves: wave w works on tile w % TN over the K-slice w / TN
-// (blocks w / TN, w / TN + KS, ..), streaming it D blocks deep. XC: activation
+// NW = TN * KS waves: wave w works on tile w / KS over the K-slice w % KS
+// (blocks w % KS, w % KS + KS, ..), streaming it D blocks deep; a tile's KS
+// waves are neighbours, so they issue their first loads together (1-1.5%
+// over slices of one tile spread across the workgroup). XC: activation
 // registers per lane. SPLIT: the K blocks are divided into gridDim.y groups,
 // blockIdx.y's group only (its activations alone in LDS); each workgroup
 // writes fp32 partial sums part[blockIdx.y][M][N], and the last of the
@@ -232,7 +234,7 @@ __global__ __launch_bounds__(TN * KS * 64) void gemv_mfma_kernel(
   // LDS: [codebook table][activations, 256 B per (row, block) from xs_addr];
   // after the K loop the reduction buffer reuses the start of LDS.
 
-  const int jt = wave % TN, ks = wave / TN;
+  const int jt = wave / KS, ks = wave % KS;
   // K blocks of this workgroup: [kb0, kb0 + nbr)
   const int kb0 = SPLIT ? (int)((int64_t)nb * blockIdx.y / gridDim.y) : 0;
   const int nbr = SPLIT ? (int)((int64_t)nb * (blockIdx.y + 1) / gridDim.y) - kb0 : nb;
