@@ -442,13 +442,99 @@ __device__ __forceinline__ void store_tile4(const float16v (&acc)[TMW][NTW], voi
   }
 }
 
-template <bool NIB, int TMW, int NTW, bool MASK, int OM>
+// Grouped form (experts): the row tiles of all groups, in group order, are
+// numbered consecutively; tile t of the grid belongs to the group whose tiles
+// cover t. A wave finds it from the group offsets with a prefix sum over the
+// lanes (64 groups per step). False past the last tile.
+template <int BM>
+__device__ __forceinline__ bool group_tile(const GemmGroup& g, int t, int lane, int& e_out,
+                                           int& mt_out) {
+  int base = 0;
+  for (int q = 0; q * 64 < g.groups; ++q) {  // uniform
+    const int e = q * 64 + lane;
+    const int cnt = e < g.groups ? g.offsets[e + 1] - g.offsets[e] : 0;
+    const int tiles = (cnt + BM - 1) / BM;
+    int incl = tiles;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int v = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += v;
+    }
+    const int first = base + incl - tiles;
+    const unsigned long long hit = __ballot(tiles > 0 && t >= first && t < first + tiles);
+    if (hit) {
+      const int l = __ffsll((long long)hit) - 1;
+      e_out = __builtin_amdgcn_readfirstlane(q * 64 + l);
+      mt_out = __builtin_amdgcn_readfirstlane(t - __shfl(first, l, 64));
+      return true;
+    }
+    base += __shfl(incl, 63, 64);
+  }
+  return false;
+}
+
+// GRP 0: one matrix. GRP 1 / 2 (grouped experts, GemmGroup g): blockIdx.x is
+// a row tile of some expert (group_tile), blockIdx.y the column tile; the
+// activation rows are gathered (g.a_rows) and the expert's codes and norms
+// start at codes / norms + e * stride. GRP 1 writes fp32 rows of y at the
+// expert's pair rows; GRP 2 (SwiGLU, NTW = 2) takes gate rows n and up rows
+// I + n for the same 128 columns n of h, and writes silu(gate) * up through
+// the FWHT-128 as pair-f16 rows (the next product's activations).
+// SwiGLU epilogue of the grouped four-wave kernel: h = silu(gate) * up for
+// the tile's 128 columns (one 128-block of h) into an fp16 LDS tile [BM][128],
+// then each row through the FWHT-128 (16 lanes per row) into pair-f16 x_tf
+// layout at y + (row0 + m) * (ldy / 2) u32, block n0 / 128. Columns >= I are
+// zero.
+template <int TMW>
+__device__ __forceinline__ void swiglu_xtf_tile4(const float16v (&acc)[TMW][2], uint32_t* __restrict__ y,
+                                                 int64_t ldy, int M, int I, int64_t row0, int m0, int n0) {
+  constexpr int BM = TMW * 32;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+  __syncthreads();  // every wave is done with the ring and the table
+#pragma unroll
+  for (int i = 0; i < TMW; ++i)
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const int col = wave * 32 + 8 * gq + 4 * h;  // four consecutive columns
+      float hv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float s = acc[i][0][4 * gq + e], u = acc[i][1][4 * gq + e];
+        hv[e] = n0 + col + e < I ? s / (1.f + __expf(-s)) * u : 0.f;
+      }
+      const uint32_t addr = (uint32_t)(32 * i + l32) * 256u + (uint32_t)col * 2u;
+      lds_st64(addr, u32x2v{pack16x2(hv[0], hv[1], false), pack16x2(hv[2], hv[3], false)});
+    }
+  __syncthreads();
+  const int q = tid & 15;  // 16 groups of 16 lanes: rows tid / 16 + 16 k
+#pragma unroll
+  for (int k = 0; k < BM / 16; ++k) {
+    const int r = (tid >> 4) + 16 * k;
+    float v[8];
+    {
+      const u32x4v w = lds_ld128((uint32_t)r * 256u + (uint32_t)q * 16u);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        v[2 * c] = h2f((uint16_t)(w[c] & 0xffff));
+        v[2 * c + 1] = h2f((uint16_t)(w[c] >> 16));
+      }
+    }
+    fwht128_group16(v, q);
+    const int m = m0 + r;
+    const bool live = m < M;
+    const int64_t prow = live ? row0 + m : row0;  // no address past the expert's rows
+    store_pair_block(v, q, y + prow * (ldy / 2) + (int64_t)(n0 / 128) * 64, live);
+  }
+}
+
+template <bool NIB, int TMW, int NTW, bool MASK, int OM, int GRP>
 __global__ __launch_bounds__(256) void gemm4_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
     const float* __restrict__ ct, int n_levels, uint32_t code_mask, int tbl_entries,
     const uint32_t* __restrict__ xp, void* __restrict__ y, const uint16_t* __restrict__ bias,
     int M, int N, int nb, int64_t ldy, int tiles_m, int tiles_total, WLayout lay, int vec_ok,
-    int ybf) {
+    int ybf, GemmGroup g) {
   constexpr int NT = 256;
   constexpr int BM = TMW * 32;
   constexpr int BN = 128 * NTW;
@@ -462,12 +548,27 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
   const int h = lane >> 5, l32 = lane & 31;
   const uint32_t lane4 = (uint32_t)lane << 2;
 
-  // XCD-aware tile order: ids are dealt round-robin to 8 XCDs; give each XCD a
-  // contiguous range of logical tiles (M-tile fastest).
-  int wid = blockIdx.x;
-  if ((tiles_total & 7) == 0) wid = (wid & 7) * (tiles_total >> 3) + (wid >> 3);
-  const int tm = wid % tiles_m, tn = wid / tiles_m;
-  const int m0 = tm * BM, n0 = tn * BN;
+  static_assert(GRP != 2 || NTW == 2, "SwiGLU tiles: one gate and one up n-tile per wave");
+  int m0, n0;
+  int64_t row0 = 0;  // grouped: the expert's first pair row
+  if constexpr (GRP == 0) {
+    // XCD-aware tile order: ids are dealt round-robin to 8 XCDs; give each
+    // XCD a contiguous range of logical tiles (M-tile fastest).
+    int wid = blockIdx.x;
+    if ((tiles_total & 7) == 0) wid = (wid & 7) * (tiles_total >> 3) + (wid >> 3);
+    const int tm = wid % tiles_m, tn = wid / tiles_m;
+    m0 = tm * BM;
+    n0 = tn * BN;
+  } else {
+    int e, mt;
+    if (!group_tile<BM>(g, blockIdx.x, lane, e, mt)) return;  // uniform
+    row0 = g.offsets[e];
+    M = g.offsets[e + 1] - (int)row0;  // this expert's rows
+    m0 = mt * BM;
+    n0 = blockIdx.y * (GRP == 2 ? 128 : BN);
+    codes += (int64_t)e * g.codes_stride;
+    norms += (int64_t)e * g.norms_stride;
+  }
 
   // codebook values now, the table once the first A and B loads are issued
   // (the values' round trip overlaps theirs)
@@ -478,9 +579,9 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
   // K range of this workgroup, in pairs of 128-blocks (the loop takes four
   // half-blocks per step): gridDim.z groups; with more than one, fp32 partial
   // sums go to slab blockIdx.z [M][ldy] of y
-  const int kb0 = 2 * (int)((int64_t)(nb / 2) * blockIdx.z / gridDim.z);
-  const int nbz = 2 * (int)((int64_t)(nb / 2) * (blockIdx.z + 1) / gridDim.z) - kb0;
-  y = reinterpret_cast<char*>(y) + (int64_t)blockIdx.z * M * ldy * (OM == OM_F16 ? 2 : 4);
+  const int kb0 = GRP ? 0 : 2 * (int)((int64_t)(nb / 2) * blockIdx.z / gridDim.z);
+  const int nbz = GRP ? nb : 2 * (int)((int64_t)(nb / 2) * (blockIdx.z + 1) / gridDim.z) - kb0;
+  if constexpr (GRP == 0) y = reinterpret_cast<char*>(y) + (int64_t)blockIdx.z * M * ldy * (OM == OM_F16 ? 2 : 4);
 
   // Loads through buffer resources based at this workgroup's first row of x
   // and first column of the weights: per-lane offsets in VGPRs, the K
@@ -488,8 +589,11 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
   // loop). Every extent is below 2 GiB (host check).
   const int64_t xrow_u32 = (int64_t)nb * 64;
   const int mlast = (m0 + BM <= M ? m0 + BM : M) - 1;
-  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(xp + (int64_t)m0 * xrow_u32), (short)0, (int)((mlast - m0 + 1) * xrow_u32 * 4), 0x00020000);
+  // grouped: the whole activation matrix (rows gathered per lane)
+  const __amdgpu_buffer_rsrc_t ra =
+      GRP ? __builtin_amdgcn_make_buffer_rsrc((void*)xp, (short)0, (int)(g.a_total_rows * xrow_u32 * 4), 0x00020000)
+          : __builtin_amdgcn_make_buffer_rsrc((void*)(xp + (int64_t)m0 * xrow_u32), (short)0,
+                                              (int)((mlast - m0 + 1) * xrow_u32 * 4), 0x00020000);
   uint32_t a_voff[KA];
   uint32_t a_dst[KA];
 #pragma unroll
@@ -498,22 +602,40 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
     const int r = q >> 3, c = q & 7;
     int m = m0 + r;
     if (m >= M) m = M - 1;  // clamped rows feed discarded outputs only
-    a_voff[i] = (uint32_t)(((int64_t)(m - m0) * xrow_u32 + c * 4) * 4);
+    if constexpr (GRP) {
+      const int64_t pr = row0 + m;  // pair row
+      const int64_t src = g.a_rows ? (int64_t)g.a_rows[pr] : pr;
+      a_voff[i] = (uint32_t)((src * xrow_u32 + c * 4) * 4);
+    } else {
+      a_voff[i] = (uint32_t)(((int64_t)(m - m0) * xrow_u32 + c * 4) * 4);
+    }
     a_dst[i] = (uint32_t)(r * kARow4 + (((uint32_t)c ^ a4_swz(r)) << 4));
   }
+  // grouped: resources over the expert's whole codes and norms
   const int nlast = (n0 + BN <= N ? n0 + BN : N) - 1;
-  const int64_t cb0 = lay.codes_off(n0), nb0 = lay.norms_off(n0);
+  const int64_t cb0 = GRP ? 0 : lay.codes_off(n0), nb0 = GRP ? 0 : lay.norms_off(n0);
   const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(codes + cb0), (short)0,
-      (int)(lay.codes_off(nlast) + (int64_t)(nb - 1) * lay.c_blk + (NIB ? 64 : 128) - cb0), 0x00020000);
+      GRP ? (int)g.codes_stride
+          : (int)(lay.codes_off(nlast) + (int64_t)(nb - 1) * lay.c_blk + (NIB ? 64 : 128) - cb0), 0x00020000);
   const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(norms + nb0), (short)0, (int)((lay.norms_off(nlast) + (int64_t)(nb - 1) * lay.n_blk + 1 - nb0) * 2),
+      (void*)(norms + nb0), (short)0,
+      GRP ? (int)(g.norms_stride * 2)
+          : (int)((lay.norms_off(nlast) + (int64_t)(nb - 1) * lay.n_blk + 1 - nb0) * 2),
       0x00020000);
   uint32_t b_voff[NTW], n_voff[NTW];
 #pragma unroll
   for (int j = 0; j < NTW; ++j) {
-    int n = n0 + wave * 32 * NTW + j * 32 + l32;
-    if (n >= N) n = N - 1;
+    int n;
+    if constexpr (GRP == 2) {
+      // gate row (j = 0) or up row (j = 1) of column c of h
+      int c = n0 + wave * 32 + l32;
+      if (c >= g.I) c = g.I - 1;
+      n = j == 0 ? c : g.I + c;
+    } else {
+      n = n0 + wave * 32 * NTW + j * 32 + l32;
+      if (n >= N) n = N - 1;
+    }
     b_voff[j] = (uint32_t)(lay.codes_off(n) - cb0) + 16 * h;
     n_voff[j] = (uint32_t)((lay.norms_off(n) - nb0) * 2);
   }
@@ -607,20 +729,34 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
     // go into the buffers of A(kt - 2), A(kt - 1), read before the last one
     if constexpr (S & 1) __syncthreads();
   };
-  for (int kt = 0; kt < nkt; kt += 4) {
+  int kt = 0;
+  for (; kt + 4 <= nkt; kt += 4) {
     half_step(std::integral_constant<int, 0>{}, kt);
     half_step(std::integral_constant<int, 1>{}, kt + 1);
     half_step(std::integral_constant<int, 2>{}, kt + 2);
     half_step(std::integral_constant<int, 3>{}, kt + 3);
   }
+  if constexpr (GRP != 0) {
+    if (kt < nkt) {  // an odd block count: its last block
+      half_step(std::integral_constant<int, 0>{}, kt);
+      half_step(std::integral_constant<int, 1>{}, kt + 1);
+    }
+  }
 
-  store_tile4<TMW, NTW, OM>(acc, y, ldy, bias, M, N, m0, n0, vec_ok, ybf != 0);
+  if constexpr (GRP == 2) {
+    swiglu_xtf_tile4<TMW>(acc, reinterpret_cast<uint32_t*>(y), ldy, M, g.I, row0, m0, n0);
+  } else if constexpr (GRP == 1) {
+    store_tile4<TMW, NTW, OM>(acc, reinterpret_cast<char*>(y) + row0 * ldy * (OM == OM_F16 ? 2 : 4), ldy,
+                              bias, M, N, m0, n0, vec_ok, ybf != 0);
+  } else {
+    store_tile4<TMW, NTW, OM>(acc, y, ldy, bias, M, N, m0, n0, vec_ok, ybf != 0);
+  }
 }
 
 template <bool NIB, int TMW, int NTW, bool MASK, int OM>
 static int launch_gemm4_t(const GemmArgs& a, hipStream_t st, int ksplit = 1) {
   constexpr int BM = TMW * 32, BN = 128 * NTW;
-  auto kern = gemm4_kernel<NIB, TMW, NTW, MASK, OM>;
+  auto kern = gemm4_kernel<NIB, TMW, NTW, MASK, OM, 0>;
   const int entries = table_entries(NIB, a.n_levels);
   constexpr size_t ES = OM == OM_F16 ? 2 : 4;
   const size_t lds_loop = (size_t)entries * 256 + kA4Ring * (size_t)BM * kARow4;
@@ -647,8 +783,61 @@ static int launch_gemm4_t(const GemmArgs& a, hipStream_t st, int ksplit = 1) {
   kern<<<dim3((unsigned)total, 1, (unsigned)ksplit), dim3(256), lds, st>>>(
       a.codes, a.norms, a.ct, a.n_levels, 0x01010101u * mb, entries,
       reinterpret_cast<const uint32_t*>(a.xp), a.y, a.bias, a.M, a.N, a.nb, a.ldy, tiles_m,
-      (int)total, a.lay, vec_ok, a.ybf);
+      (int)total, a.lay, vec_ok, a.ybf, GemmGroup{});
   return launch_status();
+}
+
+// Grouped expert products on the four-wave kernel, 128 x 256 tiles: GRP 1
+// (SE_F32) fp32 rows y[pair][N]; GRP 2 (SE_SWIGLU_XTF) the transformed
+// silu(gate) * up as pair-f16 rows of I / 128 blocks.
+template <bool NIB, bool MASK, int GRP>
+static int launch_moe_gemm4_t(const MoeGemmArgs& a, hipStream_t st) {
+  constexpr int TMW = 4, NTW = 2, BM = TMW * 32, BN = 128 * NTW;
+  constexpr int OM = GRP == 1 ? OM_F32 : OM_F16;
+  auto kern = gemm4_kernel<NIB, TMW, NTW, MASK, OM, GRP>;
+  const int entries = table_entries(NIB, a.n_levels);
+  const size_t lds_loop = (size_t)entries * 256 + kA4Ring * (size_t)BM * kARow4;
+  const size_t lds_out = GRP == 1 ? (size_t)BM * (BN * 4 + 16) : (size_t)BM * 256;
+  const size_t lds = lds_loop > lds_out ? lds_loop : lds_out;
+  if (lds > 160 * 1024) return PE_ERR_DIMS;
+  static const bool attr_ok = [&] {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+  }();
+  (void)attr_ok;
+  // at least the sum over the groups of ceil(rows / BM); the surplus
+  // workgroups find no tile and leave
+  const int64_t tiles_m = a.g.groups + (a.P + BM - 1) / BM;
+  const int64_t tiles_n = GRP == 2 ? a.g.I / 128 : (a.N + BN - 1) / BN;
+  if (tiles_m > INT32_MAX || tiles_n > 65535 || tiles_n < 1) return PE_ERR_DIMS;
+  const uint8_t mb = NIB ? (uint8_t)((a.n_levels - 1) * 0x11) : (uint8_t)(a.n_levels - 1);
+  const int vec_ok = GRP == 1 && (uintptr_t)a.y % 16 == 0 && (a.ldy * 4) % 16 == 0;
+  kern<<<dim3((unsigned)tiles_m, (unsigned)tiles_n), dim3(256), lds, st>>>(
+      a.codes, a.norms, a.ct, a.n_levels, 0x01010101u * mb, entries,
+      reinterpret_cast<const uint32_t*>(a.xp), a.y, nullptr, 0, a.N, a.nb, a.ldy, 0, 0, a.lay, vec_ok, 0,
+      a.g);
+  return launch_status();
+}
+
+bool moe_gemm4_fits(const MoeGemmArgs& a, int epilogue) {
+  const int64_t lim = (int64_t)1 << 31;
+  if (epilogue == SE_SWIGLU_XTF && (a.g.I <= 0 || a.g.I % 128 || a.ldy % 128)) return false;
+  return a.nb >= 1 && a.g.groups >= 1 && a.g.codes_stride < lim && a.g.norms_stride * 2 < lim &&
+         a.g.a_total_rows * a.nb * 256 < lim && a.P < lim;
+}
+
+int moe_gemm4(bool nibble, int epilogue, const MoeGemmArgs& a, hipStream_t st) {
+  if (!a.g.offsets || !moe_gemm4_fits(a, epilogue)) return PE_ERR_DIMS;
+  const bool mask = nibble ? a.n_levels != 16 : a.n_levels != 256;
+  if (epilogue == SE_F32) {
+    if (nibble) return mask ? launch_moe_gemm4_t<true, true, 1>(a, st) : launch_moe_gemm4_t<true, false, 1>(a, st);
+    return mask ? launch_moe_gemm4_t<false, true, 1>(a, st) : launch_moe_gemm4_t<false, false, 1>(a, st);
+  }
+  if (epilogue == SE_SWIGLU_XTF) {
+    if (nibble) return mask ? launch_moe_gemm4_t<true, true, 2>(a, st) : launch_moe_gemm4_t<true, false, 2>(a, st);
+    return mask ? launch_moe_gemm4_t<false, true, 2>(a, st) : launch_moe_gemm4_t<false, false, 2>(a, st);
+  }
+  return PE_ERR_DTYPE;
 }
 
 template <bool NIB, int TMW, int TNW, int WM, int WN, int OM>

@@ -63,6 +63,34 @@ struct GemmArgs {
   int ybf = 0;  // 16-bit output (and bias) is bfloat16
 };
 
+// Grouped form of the four-wave prefill kernel (expert products): row tiles
+// of every group in group order, activation rows gathered per pair row.
+struct GemmGroup {
+  const int32_t* offsets;  // [groups + 1]: first pair row of each group
+  const int32_t* a_rows;   // activation row of each pair row (null: the pair row)
+  int64_t codes_stride;    // bytes of one group's codes
+  int64_t norms_stride;    // fp16 norms of one group
+  int64_t a_total_rows;    // rows of the activation matrix
+  int groups;
+  int I;  // SwiGLU: columns of h (gate rows 0..I-1, up rows I..2I-1)
+};
+struct MoeGemmArgs {
+  const uint8_t* codes;
+  const uint16_t* norms;
+  const float* ct;
+  int n_levels;
+  WLayout lay;
+  int nb;          // 128-blocks of K (any count)
+  const void* xp;  // pair-f16 activations [a_total_rows][nb][64]
+  void* y;         // SE_F32: fp32 [pairs][ldy]; SE_SWIGLU_XTF: pair-f16 rows of ldy halves
+  int64_t ldy;
+  int N;      // SE_F32: output columns; SE_SWIGLU_XTF: weight rows (2 I)
+  int64_t P;  // pair rows over all groups
+  GemmGroup g;
+};
+bool moe_gemm4_fits(const MoeGemmArgs& a, int epilogue);
+int moe_gemm4(bool nibble, int epilogue, const MoeGemmArgs& a, hipStream_t st);
+
 // pe_gemv.hip
 int gemv1(bool nibble, int xmode, int omode, const Gemv1Args& a, hipStream_t st);
 int gemv1_max_kp(bool nibble);

@@ -443,6 +443,12 @@ static int route_check(int64_t T, int E, int top_k, int scoring, const float* bi
   return PE_OK;
 }
 
+// Experts with at least this many rows on average (the prefill regime) run
+// on the grouped four-wave prefill kernel: 128-row tiles of 32x32x16 MFMAs,
+// each expert's weights read once per 128 rows, instead of the expert
+// kernel's passes of 64 rows on 16x16x32 MFMAs.
+constexpr int kMoeGemmMinRows = 256;
+
 struct MoeWeights {
   const void* w13_codes;
   int bits13, packed13;
@@ -533,20 +539,31 @@ static int moe_run(const void* x, int x_dtype, int64_t T, int H, int I, int E, i
   const float* wts = route ? reinterpret_cast<const float*>(ws + L.topk_w) : topk_w;
   // 2. gate/up + SwiGLU, each 128-column block of h transformed in the same
   // kernel -> htf [P, Ip] pair f16 (columns past I are zero)
-  {
-    SmallArgs a{reinterpret_cast<const uint8_t*>(W.w13_codes), W.w13_norms, W.ct13, W.n_levels13,
-                reinterpret_cast<const uint32_t*>(ws + L.xtf), sorted_token, offsets,
-                2 * (int64_t)I * row13, 2 * (int64_t)I * nb13, ws + L.htf, Ip, nullptr, (int)P, I,
-                nb13, wlayout(nib13, tiled13, nb13)};  // M: all pairs (rows per pass)
-    if (int rc = moe_grouped(nib13, SE_SWIGLU_XTF, a, E, st)) return rc;
-  }
   // 3. down -> y2 [P, H] fp32
-  {
-    SmallArgs a{reinterpret_cast<const uint8_t*>(W.w2_codes), W.w2_norms, W.ct2, W.n_levels2,
-                reinterpret_cast<const uint32_t*>(ws + L.htf), nullptr, offsets,
-                (int64_t)H * row2, (int64_t)H * nb2, ws + L.y2, H, nullptr, (int)P, H, nb2,
-                wlayout(nib2, tiled2, nb2)};
-    if (int rc = moe_grouped(nib2, SE_F32, a, E, st)) return rc;
+  const MoeGemmArgs g13{reinterpret_cast<const uint8_t*>(W.w13_codes), W.w13_norms, W.ct13, W.n_levels13,
+                        wlayout(nib13, tiled13, nb13), nb13, ws + L.xtf, ws + L.htf, Ip, 2 * I, P,
+                        GemmGroup{offsets, sorted_token, 2 * (int64_t)I * row13, 2 * (int64_t)I * nb13, T, E, I}};
+  const MoeGemmArgs g2{reinterpret_cast<const uint8_t*>(W.w2_codes), W.w2_norms, W.ct2, W.n_levels2,
+                       wlayout(nib2, tiled2, nb2), nb2, ws + L.htf, ws + L.y2, H, H, P,
+                       GemmGroup{offsets, nullptr, (int64_t)H * row2, (int64_t)H * nb2, P, E, 0}};
+  if (P >= (int64_t)kMoeGemmMinRows * E && moe_gemm4_fits(g13, SE_SWIGLU_XTF) && moe_gemm4_fits(g2, SE_F32)) {
+    if (int rc = moe_gemm4(nib13, SE_SWIGLU_XTF, g13, st)) return rc;
+    if (int rc = moe_gemm4(nib2, SE_F32, g2, st)) return rc;
+  } else {
+    {
+      SmallArgs a{reinterpret_cast<const uint8_t*>(W.w13_codes), W.w13_norms, W.ct13, W.n_levels13,
+                  reinterpret_cast<const uint32_t*>(ws + L.xtf), sorted_token, offsets,
+                  2 * (int64_t)I * row13, 2 * (int64_t)I * nb13, ws + L.htf, Ip, nullptr, (int)P, I,
+                  nb13, wlayout(nib13, tiled13, nb13)};  // M: all pairs (rows per pass)
+      if (int rc = moe_grouped(nib13, SE_SWIGLU_XTF, a, E, st)) return rc;
+    }
+    {
+      SmallArgs a{reinterpret_cast<const uint8_t*>(W.w2_codes), W.w2_norms, W.ct2, W.n_levels2,
+                  reinterpret_cast<const uint32_t*>(ws + L.htf), nullptr, offsets,
+                  (int64_t)H * row2, (int64_t)H * nb2, ws + L.y2, H, nullptr, (int)P, H, nb2,
+                  wlayout(nib2, tiled2, nb2)};
+      if (int rc = moe_grouped(nib2, SE_F32, a, E, st)) return rc;
+    }
   }
   // 4. weighted combine -> out (x's dtype)
   const int64_t work = T * (H / 4);

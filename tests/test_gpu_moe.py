@@ -70,6 +70,34 @@ def test_invalid_and_duplicate_slots(b2):
     check_close(got, want, f"moe slots q{b2}")
 
 
+@pytest.mark.parametrize("tile", [True, False])
+def test_grouped_gemm_route_empty_and_invalid(tile):
+    """The prefill regime (>= 256 rows per expert on average: the grouped
+    four-wave kernel) with most experts empty, one expert taking a single
+    row, invalid slots and a token twice on one expert."""
+    say(f"moe grouped route, empty experts tile={tile}")
+    rng = np.random.default_rng(980)
+    e, hdim, inter, t, k = 8, 256, 256, 1100, 2
+    meth, layer, (w13, w2) = _layer(rng, e, hdim, inter, 3, 4, tile)
+    x = O.seeded_normal((t, hdim), 1.0, 981)
+    ids = np.tile(np.array([[1, 6]], np.int32), (t, 1))
+    ids[0] = [3, 6]        # expert 3: one row
+    ids[5] = [6, 6]        # twice to one expert
+    ids[7, 1] = -1         # a slot without an expert
+    ids[9, 0] = e          # an id past the experts
+    wts = (np.abs(O.seeded_normal((t, k), 1.0, 982, np.float32)) + 0.1).astype(np.float32)
+
+    def given(hidden_states, gating_output, topk, renormalize):
+        return to_dev(wts), to_dev(ids)
+
+    logits = to_dev(np.zeros((t, e), np.float32))
+    y = meth.apply(layer, to_dev(x), logits, k, True, custom_routing_function=given)
+    want = O.moe_forward(x, wts, ids, w13, w2).astype(np.float32)
+    check_close(y.float().cpu().numpy(), want, "moe grouped route")
+    y2 = meth.apply(layer, to_dev(x), logits, k, True, custom_routing_function=given)
+    assert torch.equal(y, y2), "grouped route not deterministic"
+
+
 def test_many_routing_workgroups():
     say("moe T=2048 e=32 k=4")
     rng = np.random.default_rng(920)
