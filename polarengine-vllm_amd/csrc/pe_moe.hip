@@ -446,8 +446,9 @@ static int route_check(int64_t T, int E, int top_k, int scoring, const float* bi
 // Experts with at least this many rows on average (the prefill regime) run
 // on the grouped four-wave prefill kernel: 128-row tiles of 32x32x16 MFMAs,
 // each expert's weights read once per 128 rows, instead of the expert
-// kernel's passes of 64 rows on 16x16x32 MFMAs.
-constexpr int kMoeGemmMinRows = 256;
+// kernel's passes of 64 rows on 16x16x32 MFMAs (64 experts, top-8: 1024
+// tokens 351 -> 313 us, 2048 tokens 603 -> 487; at 96 rows level).
+constexpr int kMoeGemmMinRows = 128;
 
 struct MoeWeights {
   const void* w13_codes;

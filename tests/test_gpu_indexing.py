@@ -349,9 +349,10 @@ MOE_CASES = [
     (128, 64, 2048, 1408, 8, 3, 4),   # the MoE config of BASELINE (C5)
     (64, 8, 512, 384, 4, 4, 3),
     (48, 16, 512, 256, 2, 5, 6),      # int8 experts
-    (512, 8, 1024, 256, 2, 2, 8),     # ~128 rows per expert: 64-row passes
+    (400, 8, 512, 256, 2, 3, 4),      # ~100 rows per expert: 64-row passes
+    (512, 8, 1024, 256, 2, 2, 8),     # ~128 rows per expert: the grouped prefill kernel
     (40, 4, 384, 132, 3, 4, 4),       # 2I = 264 rows: w13 stays row-major
-    # at least 256 rows per expert on average: the grouped prefill kernel
+    # more rows per expert on the grouped prefill kernel
     (512, 2, 512, 256, 2, 3, 4),
     (384, 2, 512, 384, 2, 5, 4),      # int8 w13; w2 over 3 blocks (odd)
     (300, 2, 384, 256, 2, 4, 5),      # w13 over 3 blocks (odd); int8 w2

@@ -732,11 +732,12 @@ def _moe_layer(rng, e, hdim, inter, b13, b2, tile=True):
     (3, 16, 512, 384, 1, 5, 6),       # most experts empty; int8 experts
     (40, 4, 384, 132, 3, 4, 3),       # 2I = 264 rows: w13 stays row-major
     # at least 64 rows per expert on average: 64-row passes (four m-tiles)
-    (256, 4, 256, 256, 2, 3, 4),      # ~128 rows per expert, ragged
+    (200, 4, 256, 256, 2, 3, 4),      # ~100 rows per expert, ragged
     (300, 8, 384, 200, 3, 4, 6),      # I not a multiple of 128, int8 w2
     (200, 2, 256, 384, 1, 5, 4),      # int8 w13, ~100 rows per expert
-    # at least 256 rows per expert on average: the grouped prefill kernel
+    # at least 128 rows per expert on average: the grouped prefill kernel
     # (128-row tiles of every expert in one launch per product)
+    (256, 4, 256, 256, 2, 3, 4),      # ~128 rows per expert, ragged
     (1024, 4, 256, 256, 2, 3, 4),     # ~512 rows per expert, ragged
     (600, 8, 384, 256, 4, 4, 5),      # w13 over 3 blocks (odd), int8 w2
     (700, 4, 256, 384, 2, 5, 4),      # int8 w13, w2 over 3 blocks (odd)

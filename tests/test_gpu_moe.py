@@ -72,7 +72,7 @@ def test_invalid_and_duplicate_slots(b2):
 
 @pytest.mark.parametrize("tile", [True, False])
 def test_grouped_gemm_route_empty_and_invalid(tile):
-    """The prefill regime (>= 256 rows per expert on average: the grouped
+    """The prefill regime (>= 128 rows per expert on average: the grouped
     four-wave kernel) with most experts empty, one expert taking a single
     row, invalid slots and a token twice on one expert."""
     say(f"moe grouped route, empty experts tile={tile}")
