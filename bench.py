@@ -806,7 +806,7 @@ def main():
     ap.add_argument("--headline-only", action="store_true",
                     help="time only the headline call (for a rocprofv3 kernel trace whose "
                          "dispatches are exactly the headline's)")
-    ap.add_argument("--only-extra", choices=("moe", "prefill", "prefill2048", "kv", "layer",
+    ap.add_argument("--only-extra", choices=("moe", "moe2048", "prefill", "prefill2048", "kv", "layer",
                                              "decode", "e2e", "fwht", "hbm"),
                     help="time only one of the extra workloads and print its JSON (for a "
                          "rocprofv3 kernel trace of that path alone)")
@@ -844,7 +844,8 @@ def main():
         profile_traffic(dev)
         return
     if args.only_extra:
-        fn = {"moe": moe_extra, "prefill": prefill_extra, "kv": kv_extra,
+        fn = {"moe": moe_extra, "moe2048": lambda d: moe_extra(d, t=2048),
+              "prefill": prefill_extra, "kv": kv_extra,
               "prefill2048": lambda d: prefill_m2048_extra(d, trace_only=True),
               "layer": decoder_layer_extra, "decode": decode_extra, "e2e": e2e_extra,
               "fwht": fwht_extra, "hbm": hbm_extra}[args.only_extra]
