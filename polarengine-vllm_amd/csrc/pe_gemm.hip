@@ -322,13 +322,15 @@ constexpr int kARow4 = 128;
 constexpr int kA4Ring = 6;
 __device__ __forceinline__ uint32_t a4_swz(int r) { return (uint32_t)((r >> 1) & 7); }
 
-template <bool NIB, int TMW, int NTW, bool MASK>
+// ACT <= TMW: the m-tiles that hold live rows (the others' A fragments are
+// not read and their MFMAs not issued; their accumulators stay zero)
+template <bool NIB, int TMW, int NTW, bool MASK, int ACT = TMW>
 __device__ __forceinline__ void issue_frag4(Frag4<NIB, TMW, NTW>& f, uint32_t aaddr, int t,
                                             const BSlot4<NIB, NTW>& bt, uint32_t lane4,
                                             uint32_t code_mask) {
   // aaddr: this lane's row and swizzled chunk of slab t in m-tile 0
 #pragma unroll
-  for (int i = 0; i < TMW; ++i)
+  for (int i = 0; i < ACT; ++i)
     f.a[i] = __builtin_bit_cast(half8v, lds_ld128(aaddr + i * 32 * kARow4));
 #pragma unroll
   for (int j = 0; j < NTW; ++j) {
@@ -349,7 +351,7 @@ __device__ __forceinline__ void issue_frag4(Frag4<NIB, TMW, NTW>& f, uint32_t aa
   }
 }
 
-template <bool NIB, int TMW, int NTW>
+template <bool NIB, int TMW, int NTW, int ACT = TMW>
 __device__ __forceinline__ void mma_frag4(float16v (&acc)[TMW][NTW], const Frag4<NIB, TMW, NTW>& f,
                                           const BSlot4<NIB, NTW>& bt) {
 #pragma unroll
@@ -369,7 +371,7 @@ __device__ __forceinline__ void mma_frag4(float16v (&acc)[TMW][NTW], const Frag4
     // weights as the MFMA's A operand: the accumulator comes out transposed,
     // lane = output row, four consecutive output columns per register group
 #pragma unroll
-    for (int i = 0; i < TMW; ++i)
+    for (int i = 0; i < ACT; ++i)
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf, f.a[i], acc[i][j], 0, 0, 0);
   }
 }
@@ -549,6 +551,7 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
   const uint32_t lane4 = (uint32_t)lane << 2;
 
   static_assert(GRP != 2 || NTW == 2, "SwiGLU tiles: one gate and one up n-tile per wave");
+  static_assert(GRP == 0 || TMW > 2, "grouped tiles: 1, 2 or TMW live m-tiles");
   int m0, n0;
   int64_t row0 = 0;  // grouped: the expert's first pair row
   if constexpr (GRP == 0) {
@@ -697,50 +700,66 @@ __global__ __launch_bounds__(256) void gemm4_kernel(
   lda(stg[1], 5);
   __syncthreads();
 
-  Frag4<NIB, TMW, NTW> f;
-  issue_frag4<NIB, TMW, NTW, MASK>(f, abuf + a_off[0], 0, slot[0], lane4, code_mask);
-  uint32_t bcur = 0;  // ring offset (bytes) of half-block kt's A buffer
   auto ring_next = [](uint32_t b) { return b == (kA4Ring - 1) * ABUF ? 0u : b + ABUF; };
+  // the K loop, computing the first ACT m-tiles
+  auto k_loop = [&](auto ACT_) {
+    constexpr int ACT = decltype(ACT_)::value;
+    Frag4<NIB, TMW, NTW> f;
+    issue_frag4<NIB, TMW, NTW, MASK, ACT>(f, abuf + a_off[0], 0, slot[0], lane4, code_mask);
+    uint32_t bcur = 0;  // ring offset (bytes) of half-block kt's A buffer
 
-  auto half_step = [&](auto S_, int kt) {
-    constexpr int S = decltype(S_)::value;
-    const uint32_t bnext = ring_next(bcur);
-    const uint32_t bst = ring_next(ring_next(ring_next(bnext)));  // where A(kt - 2) was
-    ldb(slot[(S + 3) & 3], kt + 3);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      Frag4<NIB, TMW, NTW> fn;
-      // this slab's operands (issued one slab ago) are in: wait for them
-      // before the next slab's reads go out
-      __builtin_amdgcn_s_waitcnt(0xc07f);
-      if (t < 3) issue_frag4<NIB, TMW, NTW, MASK>(fn, abuf + bcur + a_off[t + 1], t + 1, slot[S], lane4, code_mask);
-      else issue_frag4<NIB, TMW, NTW, MASK>(fn, abuf + bnext + a_off[0], 0, slot[(S + 1) & 3], lane4, code_mask);
-      // keep the next slab's reads ahead of this slab's MFMAs
+    auto half_step = [&](auto S_, int kt) {
+      constexpr int S = decltype(S_)::value;
+      const uint32_t bnext = ring_next(bcur);
+      const uint32_t bst = ring_next(ring_next(ring_next(bnext)));  // where A(kt - 2) was
+      ldb(slot[(S + 3) & 3], kt + 3);
       __builtin_amdgcn_sched_barrier(0);
-      mma_frag4<NIB, TMW, NTW>(acc, f, slot[S]);
-      f = fn;
-    }
-    sta(abuf + bst, stg[S & 1]);  // A(kt + 4)
-    lda(stg[S & 1], kt + 6);
-    bcur = bnext;
-    // one barrier per 128-block: between two of them the waves read A(kt),
-    // A(kt + 1) and the first slab of A(kt + 2) while A(kt + 4), A(kt + 5)
-    // go into the buffers of A(kt - 2), A(kt - 1), read before the last one
-    if constexpr (S & 1) __syncthreads();
-  };
-  int kt = 0;
-  for (; kt + 4 <= nkt; kt += 4) {
-    half_step(std::integral_constant<int, 0>{}, kt);
-    half_step(std::integral_constant<int, 1>{}, kt + 1);
-    half_step(std::integral_constant<int, 2>{}, kt + 2);
-    half_step(std::integral_constant<int, 3>{}, kt + 3);
-  }
-  if constexpr (GRP != 0) {
-    if (kt < nkt) {  // an odd block count: its last block
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        Frag4<NIB, TMW, NTW> fn;
+        // this slab's operands (issued one slab ago) are in: wait for them
+        // before the next slab's reads go out
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        if (t < 3)
+          issue_frag4<NIB, TMW, NTW, MASK, ACT>(fn, abuf + bcur + a_off[t + 1], t + 1, slot[S], lane4, code_mask);
+        else
+          issue_frag4<NIB, TMW, NTW, MASK, ACT>(fn, abuf + bnext + a_off[0], 0, slot[(S + 1) & 3], lane4, code_mask);
+        // keep the next slab's reads ahead of this slab's MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+        mma_frag4<NIB, TMW, NTW, ACT>(acc, f, slot[S]);
+        f = fn;
+      }
+      sta(abuf + bst, stg[S & 1]);  // A(kt + 4)
+      lda(stg[S & 1], kt + 6);
+      bcur = bnext;
+      // one barrier per 128-block: between two of them the waves read A(kt),
+      // A(kt + 1) and the first slab of A(kt + 2) while A(kt + 4), A(kt + 5)
+      // go into the buffers of A(kt - 2), A(kt - 1), read before the last one
+      if constexpr (S & 1) __syncthreads();
+    };
+    int kt = 0;
+    for (; kt + 4 <= nkt; kt += 4) {
       half_step(std::integral_constant<int, 0>{}, kt);
       half_step(std::integral_constant<int, 1>{}, kt + 1);
+      half_step(std::integral_constant<int, 2>{}, kt + 2);
+      half_step(std::integral_constant<int, 3>{}, kt + 3);
     }
+    if constexpr (GRP != 0) {
+      if (kt < nkt) {  // an odd block count: its last block
+        half_step(std::integral_constant<int, 0>{}, kt);
+        half_step(std::integral_constant<int, 1>{}, kt + 1);
+      }
+    }
+  };
+  if constexpr (GRP != 0) {
+    // an expert's last row tile often holds a few rows: compute only the
+    // m-tiles that hold live rows (uniform: M and m0 are per workgroup)
+    const int live = M - m0;
+    if (live <= 32) k_loop(std::integral_constant<int, 1>{});
+    else if (live <= 64) k_loop(std::integral_constant<int, 2>{});
+    else k_loop(std::integral_constant<int, TMW>{});
+  } else {
+    k_loop(std::integral_constant<int, TMW>{});
   }
 
   if constexpr (GRP == 2) {
