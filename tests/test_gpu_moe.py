@@ -98,6 +98,34 @@ def test_grouped_gemm_route_empty_and_invalid(tile):
     assert torch.equal(y, y2), "grouped route not deterministic"
 
 
+@pytest.mark.parametrize("tile", [False, True])
+def test_grouped_gemm_route_partial_tiles(tile):
+    """The prefill regime with expert row counts on every side of the
+    kernel's 32- and 64-row steps (a tile computes only the 32-row m-tiles
+    that hold rows): 1, 32, 33, 64, 65 rows, and experts whose last tile
+    holds 1, 20 or 40 rows after full ones."""
+    say(f"moe grouped route, partial tiles tile={tile}")
+    rng = np.random.default_rng(990)
+    e, hdim, inter, t, k = 8, 256, 256, 600, 2
+    meth, layer, (w13, w2) = _layer(rng, e, hdim, inter, 3, 4, tile)
+    x = O.seeded_normal((t, hdim), 1.0, 991)
+    first = np.concatenate([np.full(n, ex, np.int32) for ex, n in
+                            ((0, 1), (1, 32), (2, 33), (3, 64), (4, 65), (5, 168), (6, 129))])
+    first = np.concatenate([first, np.full(t - first.size, 5, np.int32)])  # expert 5: 276 rows
+    ids = np.stack([rng.permutation(first), np.full(t, 7, np.int32)], axis=1).astype(np.int32)
+    counts = np.bincount(ids.ravel(), minlength=e)
+    assert list(counts) == [1, 32, 33, 64, 65, 276, 129, 600]
+    wts = (np.abs(O.seeded_normal((t, k), 1.0, 992, np.float32)) + 0.1).astype(np.float32)
+
+    def given(hidden_states, gating_output, topk, renormalize):
+        return to_dev(wts), to_dev(ids)
+
+    logits = to_dev(np.zeros((t, e), np.float32))
+    y = meth.apply(layer, to_dev(x), logits, k, True, custom_routing_function=given)
+    want = O.moe_forward(x, wts, ids, w13, w2).astype(np.float32)
+    check_close(y.float().cpu().numpy(), want, "moe grouped route, partial tiles")
+
+
 def test_many_routing_workgroups():
     say("moe T=2048 e=32 k=4")
     rng = np.random.default_rng(920)
