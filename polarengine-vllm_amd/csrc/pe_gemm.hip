@@ -475,13 +475,6 @@ __device__ __forceinline__ bool group_tile(const GemmGroup& g, int t, int lane, 
   return false;
 }
 
-// GRP 0: one matrix. GRP 1 / 2 (grouped experts, GemmGroup g): blockIdx.x is
-// a row tile of some expert (group_tile), blockIdx.y the column tile; the
-// activation rows are gathered (g.a_rows) and the expert's codes and norms
-// start at codes / norms + e * stride. GRP 1 writes fp32 rows of y at the
-// expert's pair rows; GRP 2 (SwiGLU, NTW = 2) takes gate rows n and up rows
-// I + n for the same 128 columns n of h, and writes silu(gate) * up through
-// the FWHT-128 as pair-f16 rows (the next product's activations).
 // SwiGLU epilogue of the grouped four-wave kernel: h = silu(gate) * up for
 // the tile's 128 columns (one 128-block of h) into an fp16 LDS tile [BM][128],
 // then each row through the FWHT-128 (16 lanes per row) into pair-f16 x_tf
@@ -530,6 +523,13 @@ __device__ __forceinline__ void swiglu_xtf_tile4(const float16v (&acc)[TMW][2], 
   }
 }
 
+// GRP 0: one matrix. GRP 1 / 2 (grouped experts, GemmGroup g): blockIdx.x is
+// a row tile of some expert (group_tile), blockIdx.y the column tile; the
+// activation rows are gathered (g.a_rows) and the expert's codes and norms
+// start at codes / norms + e * stride. GRP 1 writes fp32 rows of y at the
+// expert's pair rows; GRP 2 (SwiGLU, NTW = 2) takes gate rows n and up rows
+// I + n for the same 128 columns n of h, and writes silu(gate) * up through
+// the FWHT-128 as pair-f16 rows (the next product's activations).
 template <bool NIB, int TMW, int NTW, bool MASK, int OM, int GRP>
 __global__ __launch_bounds__(256) void gemm4_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms,
