@@ -947,6 +947,12 @@ static bool use_gemm4_short(int M, int N, int nb) {
   return (nb & 1) == 0 && tiles * 4 >= 3 * (int64_t)num_cus() && tiles <= num_cus();
 }
 
+// 128 x 128 tiles, the same number as 64 x 256 ones where M is a multiple of
+// 128: each dequantized B fragment then feeds four m-tiles instead of two,
+// for twice the A reads per MFMA (Q4 12288 x 4096 at M = 256: 41.1-41.7
+// against 42.0-42.6 us, Q3 40.4-41.4 against 41.4-42.0)
+static bool gemm4_square(int M) { return M % 128 == 0; }
+
 static bool use_gemm4(int M, int N, int nb) {
   const int64_t tiles4 = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
   return (nb & 1) == 0 && tiles4 >= num_cus() && tiles4 <= 16 * (int64_t)num_cus();
@@ -961,13 +967,18 @@ static bool use_gemm4(int M, int N, int nb) {
 // kernel's split at M = 128: 31.9 against 43.7 us on the 4096 x 12288 down
 // projection, 33.3 against 45.5 on Q4 12288 x 4096; M = 256 on the down
 // projection 47.1 against 48.5 with 128-row tiles), 128 above (M = 512: 79.1
-// against 82.4 us with 64-row ones).
-static int gemm4_split_rows(int M) { return M <= 256 ? 64 : 128; }
+// against 82.4 us with 64-row ones). At M = 256, 128 x 128 tiles instead of
+// 64 x 256 ones (the same tile count; Q3 down projection 44.6-45.1 against
+// 45.0-45.4 us); at M = 128 they measured slightly slower (31.3-31.7 against
+// 31.1-31.5 us), above M = 256 slower (M = 512: 75.9 against 72.8 us).
+static bool gemm4_split_square(int M) { return M > 128 && M <= 256 && gemm4_square(M); }
+static int gemm4_split_rows(int M) { return M <= 256 && !gemm4_split_square(M) ? 64 : 128; }
+static int gemm4_split_cols(int M) { return gemm4_split_square(M) ? 128 : 256; }
 
 static int gemm4_ksplit(int M, int N, int nb) {
   if (M <= 32 || (nb & 1) || use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb)) return 1;
-  const int rows = gemm4_split_rows(M);
-  const int64_t tiles4 = (int64_t)((M + rows - 1) / rows) * ((N + 255) / 256);
+  const int rows = gemm4_split_rows(M), cols = gemm4_split_cols(M);
+  const int64_t tiles4 = (int64_t)((M + rows - 1) / rows) * ((N + cols - 1) / cols);
   int z = (int)(num_cus() / tiles4);
   if (z > nb / 4) z = nb / 4;
   return z < 2 ? 1 : z;
@@ -1022,6 +1033,8 @@ static int launch_gemm_shape(const GemmArgs& a, hipStream_t st, void* ws, size_t
   if constexpr (OM == OM_F16) {
     if (use_gemm4_short(a.M, a.N, a.nb)) {
       const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
+      if (gemm4_square(a.M))
+        return mask ? launch_gemm4_t<NIB, 4, 1, true, OM>(a, st) : launch_gemm4_t<NIB, 4, 1, false, OM>(a, st);
       return mask ? launch_gemm4_t<NIB, 2, 2, true, OM>(a, st) : launch_gemm4_t<NIB, 2, 2, false, OM>(a, st);
     }
   }
@@ -1037,6 +1050,9 @@ static int launch_gemm_shape(const GemmArgs& a, hipStream_t st, void* ws, size_t
     const int rc = gemm4_split_rows(a.M) == 64
                        ? (mask ? launch_gemm4_t<NIB, 2, 2, true, OM_F32>(p, st, z4)
                                : launch_gemm4_t<NIB, 2, 2, false, OM_F32>(p, st, z4))
+                   : gemm4_split_cols(a.M) == 128
+                       ? (mask ? launch_gemm4_t<NIB, 4, 1, true, OM_F32>(p, st, z4)
+                               : launch_gemm4_t<NIB, 4, 1, false, OM_F32>(p, st, z4))
                        : (mask ? launch_gemm4_t<NIB, 4, 2, true, OM_F32>(p, st, z4)
                                : launch_gemm4_t<NIB, 4, 2, false, OM_F32>(p, st, z4));
     if (rc) return rc;
