@@ -953,9 +953,24 @@ static bool use_gemm4_short(int M, int N, int nb) {
 // against 42.0-42.6 us, Q3 40.4-41.4 against 41.4-42.0)
 static bool gemm4_square(int M) { return M % 128 == 0; }
 
+// 64 x 384 four-wave tiles (nibble codes, 16-bit output) where 128 x 256
+// tiles do not fill a round, 64 x 256 ones do not fit one, and the 64 x 384
+// ones fill at least three quarters of one (M = 384..512 on 12288 columns):
+// one launch in place of the eight-wave kernel (Q3 12288 x 4096 at M = 512:
+// 65.8-66.1 against 70.6-71.1 us, Q4 65.7-66.0 against 71.2-71.6; M = 384
+// 57.5-57.6 against 67.9). 128 x 256 tiles at 192 workgroups measured alike
+// at M = 512 (65.5-67.4 us).
+static bool use_gemm4_wide_short(int M, int N, int nb);
+
 static bool use_gemm4(int M, int N, int nb) {
   const int64_t tiles4 = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
   return (nb & 1) == 0 && tiles4 >= num_cus() && tiles4 <= 16 * (int64_t)num_cus();
+}
+
+static bool use_gemm4_wide_short(int M, int N, int nb) {
+  const int64_t t643 = (int64_t)((M + 63) / 64) * ((N + 383) / 384);
+  return !use_gemm4(M, N, nb) && !use_gemm4_short(M, N, nb) && (nb & 1) == 0 &&
+         t643 * 4 >= 3 * (int64_t)num_cus() && t643 <= num_cus();
 }
 
 // K split of the four-wave kernel for M > 32 whose tiles are too few for one
@@ -1029,6 +1044,12 @@ static int launch_gemm_shape(const GemmArgs& a, hipStream_t st, void* ws, size_t
         return mask ? launch_gemm4_t<NIB, 4, 3, true, OM>(a, st) : launch_gemm4_t<NIB, 4, 3, false, OM>(a, st);
     }
     return mask ? launch_gemm4_t<NIB, 4, 2, true, OM>(a, st) : launch_gemm4_t<NIB, 4, 2, false, OM>(a, st);
+  }
+  if constexpr (NIB && OM == OM_F16) {
+    if (use_gemm4_wide_short(a.M, a.N, a.nb)) {
+      const bool mask = a.n_levels != 16;
+      return mask ? launch_gemm4_t<NIB, 2, 3, true, OM>(a, st) : launch_gemm4_t<NIB, 2, 3, false, OM>(a, st);
+    }
   }
   if constexpr (OM == OM_F16) {
     if (use_gemm4_short(a.M, a.N, a.nb)) {

@@ -146,6 +146,7 @@ XTF_CASES = [
     (512, 4096, 2048, "four-wave GEMM, 128-row tiles, K split"),
     (256, 12288, 256, "four-wave GEMM, 128 x 128 tiles, one launch"),
     (320, 12288, 256, "four-wave GEMM, 64 x 256 tiles, one launch"),
+    (512, 12288, 256, "four-wave GEMM, 64 x 384 tiles (nibbles), one launch"),
     (2048, 4096, 256, "four-wave GEMM, 128 x 256 tiles"),
     (1024, 12288, 256, "four-wave GEMM, 128 x 384 tiles (nibbles) / 128 x 256 (int8)"),
     (512, 4096, 384, "eight-wave GEMM (odd block count)"),
