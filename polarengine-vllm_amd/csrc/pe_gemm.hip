@@ -953,6 +953,11 @@ static bool use_gemm4_short(int M, int N, int nb) {
 // against 42.0-42.6 us, Q3 40.4-41.4 against 41.4-42.0)
 static bool gemm4_square(int M) { return M % 128 == 0; }
 
+static bool use_gemm4(int M, int N, int nb) {
+  const int64_t tiles4 = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
+  return (nb & 1) == 0 && tiles4 >= num_cus() && tiles4 <= 16 * (int64_t)num_cus();
+}
+
 // 64 x 384 four-wave tiles (nibble codes, 16-bit output) where 128 x 256
 // tiles do not fill a round, 64 x 256 ones do not fit one, and the 64 x 384
 // ones fill at least three quarters of one (M = 384..512 on 12288 columns):
@@ -960,17 +965,22 @@ static bool gemm4_square(int M) { return M % 128 == 0; }
 // 65.8-66.1 against 70.6-71.1 us, Q4 65.7-66.0 against 71.2-71.6; M = 384
 // 57.5-57.6 against 67.9). 128 x 256 tiles at 192 workgroups measured alike
 // at M = 512 (65.5-67.4 us).
-static bool use_gemm4_wide_short(int M, int N, int nb);
-
-static bool use_gemm4(int M, int N, int nb) {
-  const int64_t tiles4 = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
-  return (nb & 1) == 0 && tiles4 >= num_cus() && tiles4 <= 16 * (int64_t)num_cus();
-}
-
 static bool use_gemm4_wide_short(int M, int N, int nb) {
   const int64_t t643 = (int64_t)((M + 63) / 64) * ((N + 383) / 384);
   return !use_gemm4(M, N, nb) && !use_gemm4_short(M, N, nb) && (nb & 1) == 0 &&
          t643 * 4 >= 3 * (int64_t)num_cus() && t643 <= num_cus();
+}
+
+// 64 x 128 four-wave tiles, one launch, in place of the K split for a short K
+// (at most 32 blocks) where they fill three quarters of a round or more (M =
+// 512 on 4096 x 4096: 39.3-39.5 against 42.3-42.9 us with the split's fp32
+// partial sums and reduction, int8 codes; on 4096 x 12288 the split stays
+// faster, 77 against 81-82 us). Only above M = 64, where the small-M kernel
+// takes the shapes that no K split applies to.
+static bool use_gemm4_narrow(int M, int N, int nb) {
+  const int64_t t21 = (int64_t)((M + 63) / 64) * ((N + 127) / 128);
+  return M > 64 && nb <= 32 && (nb & 1) == 0 && !use_gemm4(M, N, nb) && !use_gemm4_short(M, N, nb) &&
+         t21 * 4 >= 3 * (int64_t)num_cus() && t21 <= num_cus();
 }
 
 // K split of the four-wave kernel for M > 32 whose tiles are too few for one
@@ -991,7 +1001,8 @@ static int gemm4_split_rows(int M) { return M <= 256 && !gemm4_split_square(M) ?
 static int gemm4_split_cols(int M) { return gemm4_split_square(M) ? 128 : 256; }
 
 static int gemm4_ksplit(int M, int N, int nb) {
-  if (M <= 32 || (nb & 1) || use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb)) return 1;
+  if (M <= 32 || (nb & 1) || use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb) || use_gemm4_narrow(M, N, nb))
+    return 1;
   const int rows = gemm4_split_rows(M), cols = gemm4_split_cols(M);
   const int64_t tiles4 = (int64_t)((M + rows - 1) / rows) * ((N + cols - 1) / cols);
   int z = (int)(num_cus() / tiles4);
@@ -1006,7 +1017,9 @@ static int gemm4_ksplit(int M, int N, int nb) {
 // workspace, then the ordered reduction shared with the decode path. 1 = no
 // split.
 static int gemm_ksplit(int M, int N, int nb) {
-  if (use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb) || gemm4_ksplit(M, N, nb) > 1) return 1;
+  if (use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb) || use_gemm4_narrow(M, N, nb) ||
+      gemm4_ksplit(M, N, nb) > 1)
+    return 1;
   const GemmShape g = pick_gemm_tile(M, N);
   const int bm = 32 * g.tmw, bn = 32 * g.wn;
   const int64_t tiles = (int64_t)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
@@ -1057,6 +1070,12 @@ static int launch_gemm_shape(const GemmArgs& a, hipStream_t st, void* ws, size_t
       if (gemm4_square(a.M))
         return mask ? launch_gemm4_t<NIB, 4, 1, true, OM>(a, st) : launch_gemm4_t<NIB, 4, 1, false, OM>(a, st);
       return mask ? launch_gemm4_t<NIB, 2, 2, true, OM>(a, st) : launch_gemm4_t<NIB, 2, 2, false, OM>(a, st);
+    }
+  }
+  if constexpr (OM == OM_F16) {
+    if (use_gemm4_narrow(a.M, a.N, a.nb)) {
+      const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
+      return mask ? launch_gemm4_t<NIB, 2, 1, true, OM>(a, st) : launch_gemm4_t<NIB, 2, 1, false, OM>(a, st);
     }
   }
   // fp16 out (the linear entry points): split K when the tiles are few and

@@ -143,7 +143,8 @@ XTF_CASES = [
     (64, 4096, 1024, "four-wave GEMM, 64-row tiles, K split + ordered reduction"),
     (128, 4096, 1024, "four-wave GEMM, 64-row tiles, K split"),
     (256, 4096, 1024, "four-wave GEMM, 128 x 128 tiles, K split"),
-    (512, 4096, 2048, "four-wave GEMM, 128-row tiles, K split"),
+    (512, 4096, 2048, "four-wave GEMM, 64 x 128 tiles, one launch (short K)"),
+    (512, 4096, 4608, "four-wave GEMM, 128-row tiles, K split"),
     (256, 12288, 256, "four-wave GEMM, 128 x 128 tiles, one launch"),
     (320, 12288, 256, "four-wave GEMM, 64 x 256 tiles, one launch"),
     (512, 12288, 256, "four-wave GEMM, 64 x 384 tiles (nibbles), one launch"),
