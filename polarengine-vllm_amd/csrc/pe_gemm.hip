@@ -971,6 +971,15 @@ static bool use_gemm4_wide_short(int M, int N, int nb) {
          t643 * 4 >= 3 * (int64_t)num_cus() && t643 <= num_cus();
 }
 
+// 128 x 256 four-wave tiles (128 x 384 where gemm4_ntw picks them) that fill
+// three quarters of a round or more but less than one, where none of the
+// narrower one-round forms above applies: in place of the eight-wave kernel
+// (int8 6144 x 4096 at M = 1024, 192 tiles: 78.3 against 117.0 us).
+static bool use_gemm4_part(int M, int N, int nb) {
+  const int64_t tiles4 = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
+  return (nb & 1) == 0 && tiles4 * 4 >= 3 * (int64_t)num_cus() && tiles4 < num_cus();
+}
+
 // 64 x 128 four-wave tiles, one launch, in place of the K split for a short K
 // (at most 32 blocks) where they fill three quarters of a round or more (M =
 // 512 on 4096 x 4096: 39.3-39.5 against 42.3-42.9 us with the split's fp32
@@ -980,7 +989,7 @@ static bool use_gemm4_wide_short(int M, int N, int nb) {
 static bool use_gemm4_narrow(int M, int N, int nb) {
   const int64_t t21 = (int64_t)((M + 63) / 64) * ((N + 127) / 128);
   return M > 64 && nb <= 32 && (nb & 1) == 0 && !use_gemm4(M, N, nb) && !use_gemm4_short(M, N, nb) &&
-         t21 * 4 >= 3 * (int64_t)num_cus() && t21 <= num_cus();
+         !use_gemm4_part(M, N, nb) && t21 * 4 >= 3 * (int64_t)num_cus() && t21 <= num_cus();
 }
 
 // K split of the four-wave kernel for M > 32 whose tiles are too few for one
@@ -1001,7 +1010,8 @@ static int gemm4_split_rows(int M) { return M <= 256 && !gemm4_split_square(M) ?
 static int gemm4_split_cols(int M) { return gemm4_split_square(M) ? 128 : 256; }
 
 static int gemm4_ksplit(int M, int N, int nb) {
-  if (M <= 32 || (nb & 1) || use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb) || use_gemm4_narrow(M, N, nb))
+  if (M <= 32 || (nb & 1) || use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb) || use_gemm4_part(M, N, nb) ||
+      use_gemm4_narrow(M, N, nb))
     return 1;
   const int rows = gemm4_split_rows(M), cols = gemm4_split_cols(M);
   const int64_t tiles4 = (int64_t)((M + rows - 1) / rows) * ((N + cols - 1) / cols);
@@ -1017,8 +1027,8 @@ static int gemm4_ksplit(int M, int N, int nb) {
 // workspace, then the ordered reduction shared with the decode path. 1 = no
 // split.
 static int gemm_ksplit(int M, int N, int nb) {
-  if (use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb) || use_gemm4_narrow(M, N, nb) ||
-      gemm4_ksplit(M, N, nb) > 1)
+  if (use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb) || use_gemm4_part(M, N, nb) ||
+      use_gemm4_narrow(M, N, nb) || gemm4_ksplit(M, N, nb) > 1)
     return 1;
   const GemmShape g = pick_gemm_tile(M, N);
   const int bm = 32 * g.tmw, bn = 32 * g.wn;
@@ -1071,6 +1081,14 @@ static int launch_gemm_shape(const GemmArgs& a, hipStream_t st, void* ws, size_t
         return mask ? launch_gemm4_t<NIB, 4, 1, true, OM>(a, st) : launch_gemm4_t<NIB, 4, 1, false, OM>(a, st);
       return mask ? launch_gemm4_t<NIB, 2, 2, true, OM>(a, st) : launch_gemm4_t<NIB, 2, 2, false, OM>(a, st);
     }
+  }
+  if (use_gemm4_part(a.M, a.N, a.nb)) {
+    const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
+    if constexpr (NIB && OM == OM_F16) {
+      if (gemm4_ntw(NIB, a.M, a.N, OM) == 3)
+        return mask ? launch_gemm4_t<NIB, 4, 3, true, OM>(a, st) : launch_gemm4_t<NIB, 4, 3, false, OM>(a, st);
+    }
+    return mask ? launch_gemm4_t<NIB, 4, 2, true, OM>(a, st) : launch_gemm4_t<NIB, 4, 2, false, OM>(a, st);
   }
   if constexpr (OM == OM_F16) {
     if (use_gemm4_narrow(a.M, a.N, a.nb)) {
