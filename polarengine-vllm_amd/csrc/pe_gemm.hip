@@ -1005,9 +1005,13 @@ static bool use_gemm4_narrow(int M, int N, int nb) {
 // 64 x 256 ones (the same tile count; Q3 down projection 44.6-45.1 against
 // 45.0-45.4 us); at M = 128 they measured slightly slower (31.3-31.7 against
 // 31.1-31.5 us), above M = 256 slower (M = 512: 75.9 against 72.8 us).
+// Up to M = 64, 64 x 128 tiles (twice the tiles, so a smaller split and
+// fewer fp32 partial sums; Q4 12288 x 4096 at M = 64: 23.0 against 24.7 us,
+// 4096 x 12288 21.7-21.8 against 24.1-24.2, int8 6144 x 4096 18.6 against
+// 20.4).
 static bool gemm4_split_square(int M) { return M > 128 && M <= 256 && gemm4_square(M); }
 static int gemm4_split_rows(int M) { return M <= 256 && !gemm4_split_square(M) ? 64 : 128; }
-static int gemm4_split_cols(int M) { return gemm4_split_square(M) ? 128 : 256; }
+static int gemm4_split_cols(int M) { return gemm4_split_square(M) || M <= 64 ? 128 : 256; }
 
 static int gemm4_ksplit(int M, int N, int nb) {
   if (M <= 32 || (nb & 1) || use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb) || use_gemm4_part(M, N, nb) ||
@@ -1106,8 +1110,11 @@ static int launch_gemm_shape(const GemmArgs& a, hipStream_t st, void* ws, size_t
     p.bias = nullptr;
     const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
     const int rc = gemm4_split_rows(a.M) == 64
-                       ? (mask ? launch_gemm4_t<NIB, 2, 2, true, OM_F32>(p, st, z4)
-                               : launch_gemm4_t<NIB, 2, 2, false, OM_F32>(p, st, z4))
+                       ? (gemm4_split_cols(a.M) == 128
+                              ? (mask ? launch_gemm4_t<NIB, 2, 1, true, OM_F32>(p, st, z4)
+                                      : launch_gemm4_t<NIB, 2, 1, false, OM_F32>(p, st, z4))
+                              : (mask ? launch_gemm4_t<NIB, 2, 2, true, OM_F32>(p, st, z4)
+                                      : launch_gemm4_t<NIB, 2, 2, false, OM_F32>(p, st, z4)))
                    : gemm4_split_cols(a.M) == 128
                        ? (mask ? launch_gemm4_t<NIB, 4, 1, true, OM_F32>(p, st, z4)
                                : launch_gemm4_t<NIB, 4, 1, false, OM_F32>(p, st, z4))
@@ -1138,8 +1145,8 @@ int gemm(bool nibble, int omode, const GemmArgs& a, hipStream_t st, void* ws, si
 // Matmul on a pair-f16 x_tf, used by the linear entry points for M > 1: the
 // fp32 partial sums of the K split, if it applies.
 // M = 33..64 with fp16 out takes the GEMM when a K split applies (the
-// four-wave kernel's with 64-row tiles: 25.0 us at M = 64 on Q4 12288 x 4096,
-// against 31.5 us for the eight-wave kernel's split and 57 us for the
+// four-wave kernel's with 64 x 128 tiles: 23.0 us at M = 64 on Q4 12288 x
+// 4096, against 31.5 us for the eight-wave kernel's split and 57 us for the
 // small-M kernel)
 static bool mm_small(int64_t M, int N, int nb, int out_mode) {
   if (M <= 32) return true;
