@@ -1005,13 +1005,14 @@ static bool use_gemm4_narrow(int M, int N, int nb) {
 // 64 x 256 ones (the same tile count; Q3 down projection 44.6-45.1 against
 // 45.0-45.4 us); at M = 128 they measured slightly slower (31.3-31.7 against
 // 31.1-31.5 us), above M = 256 slower (M = 512: 75.9 against 72.8 us).
-// Up to M = 64, 64 x 128 tiles (twice the tiles, so a smaller split and
+// Up to M = 128, 64 x 128 tiles (twice the tiles, so a smaller split and
 // fewer fp32 partial sums; Q4 12288 x 4096 at M = 64: 23.0 against 24.7 us,
 // 4096 x 12288 21.7-21.8 against 24.1-24.2, int8 6144 x 4096 18.6 against
-// 20.4).
+// 20.4; M = 128: 4096 x 12288 30.0 against 30.6, int8 4096 x 4096 22.1
+// against 22.9; at M = 192 slower, 43.3 against 38.7).
 static bool gemm4_split_square(int M) { return M > 128 && M <= 256 && gemm4_square(M); }
 static int gemm4_split_rows(int M) { return M <= 256 && !gemm4_split_square(M) ? 64 : 128; }
-static int gemm4_split_cols(int M) { return gemm4_split_square(M) || M <= 64 ? 128 : 256; }
+static int gemm4_split_cols(int M) { return gemm4_split_square(M) || M <= 128 ? 128 : 256; }
 
 static int gemm4_ksplit(int M, int N, int nb) {
   if (M <= 32 || (nb & 1) || use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb) || use_gemm4_part(M, N, nb) ||

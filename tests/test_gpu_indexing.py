@@ -141,7 +141,8 @@ XTF_CASES = [
     (40, 200, 384, "small-M MFMA kernel (odd block count: no GEMM K split)"),
     (48, 4096, 256, "small-M MFMA kernel (two blocks: no K split)"),
     (64, 4096, 1024, "four-wave GEMM, 64 x 128 tiles, K split + ordered reduction"),
-    (128, 4096, 1024, "four-wave GEMM, 64 x 256 tiles, K split"),
+    (128, 4096, 1024, "four-wave GEMM, 64 x 128 tiles, K split"),
+    (192, 4096, 1024, "four-wave GEMM, 64 x 256 tiles, K split"),
     (256, 4096, 1024, "four-wave GEMM, 128 x 128 tiles, K split"),
     (512, 4096, 2048, "four-wave GEMM, 64 x 128 tiles, one launch (short K)"),
     (512, 4096, 4608, "four-wave GEMM, 128-row tiles, K split"),
