@@ -180,7 +180,8 @@ def test_linear_xtf_indexing_bit_exact(m, n, kp, kernel, tiled):
 
 @pytest.mark.parametrize("m,n,kp", [(1, 80, 1024), (16, 200, 4096), (48, 4096, 256),
                                     (128, 4096, 1024), (256, 12288, 256), (1024, 12288, 256),
-                                    (512, 4096, 384)])
+                                    (512, 4096, 384), (512, 12288, 256), (512, 4096, 2048),
+                                    (1024, 6144, 256)])
 def test_linear_xtf_indexing_bf16_out(m, n, kp):
     """The bf16 epilogues: y = bf16(ct16 * norm), one rounding."""
     for bits in (3, 4, 6):
