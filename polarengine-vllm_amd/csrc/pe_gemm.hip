@@ -953,6 +953,19 @@ static bool use_gemm4_short(int M, int N, int nb) {
 // against 42.0-42.6 us, Q3 40.4-41.4 against 41.4-42.0)
 static bool gemm4_square(int M) { return M % 128 == 0; }
 
+// int8 codes (no 384-column tiles) where 128 x 256 tiles leave most of their
+// last round empty: 64 x 128 tiles, whose rounds are each about 0.68 of a
+// 128 x 256 round's work rate per tile area, when their total comes out
+// lower (int8 6144 x 4096 at M = 1536, 288 tiles of 128 x 256: 142.3 against
+// 156.5 us; at M = 2048 the 128 x 256 ones stay, 164.7 against 179.1).
+static bool gemm4_int8_narrow(int M, int N) {
+  const int64_t cus = num_cus();
+  const int64_t t42 = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
+  const int64_t t21 = (int64_t)((M + 63) / 64) * ((N + 127) / 128);
+  const int64_t r42 = (t42 + cus - 1) / cus, r21 = (t21 + cus - 1) / cus;
+  return r21 * 8192 * 100 < r42 * 32768 * 68;
+}
+
 static bool use_gemm4(int M, int N, int nb) {
   const int64_t tiles4 = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
   return (nb & 1) == 0 && tiles4 >= num_cus() && tiles4 <= 16 * (int64_t)num_cus();
@@ -1070,6 +1083,10 @@ static int launch_gemm_shape(const GemmArgs& a, hipStream_t st, void* ws, size_t
     if constexpr (NIB && OM == OM_F16) {
       if (gemm4_ntw(NIB, a.M, a.N, OM) == 3)
         return mask ? launch_gemm4_t<NIB, 4, 3, true, OM>(a, st) : launch_gemm4_t<NIB, 4, 3, false, OM>(a, st);
+    }
+    if constexpr (!NIB && OM == OM_F16) {
+      if (gemm4_int8_narrow(a.M, a.N))
+        return mask ? launch_gemm4_t<NIB, 2, 1, true, OM>(a, st) : launch_gemm4_t<NIB, 2, 1, false, OM>(a, st);
     }
     return mask ? launch_gemm4_t<NIB, 4, 2, true, OM>(a, st) : launch_gemm4_t<NIB, 4, 2, false, OM>(a, st);
   }
