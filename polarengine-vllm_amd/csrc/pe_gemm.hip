@@ -947,10 +947,18 @@ static bool use_gemm4_short(int M, int N, int nb) {
   return (nb & 1) == 0 && tiles * 4 >= 3 * (int64_t)num_cus() && tiles <= num_cus();
 }
 
-// 128 x 128 tiles, the same number as 64 x 256 ones where M is a multiple of
-// 128: each dequantized B fragment then feeds four m-tiles instead of two,
-// for twice the A reads per MFMA (Q4 12288 x 4096 at M = 256: 41.1-41.7
-// against 42.0-42.6 us, Q3 40.4-41.4 against 41.4-42.0)
+// 128 x 128 tiles for 16-bit output where they fill three quarters of a round
+// or more but 128 x 256 ones do not fill one, ahead of 64 x 256 tiles: each
+// dequantized B fragment feeds four m-tiles instead of two, for twice the A
+// reads per MFMA (Q4 12288 x 4096 at M = 256: 41.1-41.7 against 42.0-42.6 us
+// for 64 x 256 tiles, Q3 40.4-41.4 against 41.4-42.0; at M = 192, a third of
+// their rows empty, 40.1 against 41.4 for 64 x 256 and 50.8 for the
+// eight-wave kernel).
+static bool use_gemm4_sq(int M, int N, int nb) {
+  const int64_t t41 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+  const int64_t t42 = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
+  return (nb & 1) == 0 && t42 < num_cus() && t41 * 4 >= 3 * (int64_t)num_cus() && t41 <= num_cus();
+}
 static bool gemm4_square(int M) { return M % 128 == 0; }
 
 // int8 codes (no 384-column tiles) where 128 x 256 tiles leave most of their
@@ -1028,8 +1036,8 @@ static int gemm4_split_rows(int M) { return M <= 256 && !gemm4_split_square(M) ?
 static int gemm4_split_cols(int M) { return gemm4_split_square(M) || M <= 128 ? 128 : 256; }
 
 static int gemm4_ksplit(int M, int N, int nb) {
-  if (M <= 32 || (nb & 1) || use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb) || use_gemm4_part(M, N, nb) ||
-      use_gemm4_narrow(M, N, nb))
+  if (M <= 32 || (nb & 1) || use_gemm4(M, N, nb) || use_gemm4_sq(M, N, nb) || use_gemm4_short(M, N, nb) ||
+      use_gemm4_part(M, N, nb) || use_gemm4_narrow(M, N, nb))
     return 1;
   const int rows = gemm4_split_rows(M), cols = gemm4_split_cols(M);
   const int64_t tiles4 = (int64_t)((M + rows - 1) / rows) * ((N + cols - 1) / cols);
@@ -1045,7 +1053,7 @@ static int gemm4_ksplit(int M, int N, int nb) {
 // workspace, then the ordered reduction shared with the decode path. 1 = no
 // split.
 static int gemm_ksplit(int M, int N, int nb) {
-  if (use_gemm4(M, N, nb) || use_gemm4_short(M, N, nb) || use_gemm4_part(M, N, nb) ||
+  if (use_gemm4(M, N, nb) || use_gemm4_sq(M, N, nb) || use_gemm4_short(M, N, nb) || use_gemm4_part(M, N, nb) ||
       use_gemm4_narrow(M, N, nb) || gemm4_ksplit(M, N, nb) > 1)
     return 1;
   const GemmShape g = pick_gemm_tile(M, N);
@@ -1097,10 +1105,12 @@ static int launch_gemm_shape(const GemmArgs& a, hipStream_t st, void* ws, size_t
     }
   }
   if constexpr (OM == OM_F16) {
+    if (use_gemm4_sq(a.M, a.N, a.nb)) {
+      const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
+      return mask ? launch_gemm4_t<NIB, 4, 1, true, OM>(a, st) : launch_gemm4_t<NIB, 4, 1, false, OM>(a, st);
+    }
     if (use_gemm4_short(a.M, a.N, a.nb)) {
       const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
-      if (gemm4_square(a.M))
-        return mask ? launch_gemm4_t<NIB, 4, 1, true, OM>(a, st) : launch_gemm4_t<NIB, 4, 1, false, OM>(a, st);
       return mask ? launch_gemm4_t<NIB, 2, 2, true, OM>(a, st) : launch_gemm4_t<NIB, 2, 2, false, OM>(a, st);
     }
   }

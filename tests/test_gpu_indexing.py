@@ -147,6 +147,7 @@ XTF_CASES = [
     (512, 4096, 2048, "four-wave GEMM, 64 x 128 tiles, one launch (short K)"),
     (512, 4096, 4608, "four-wave GEMM, 128-row tiles, K split"),
     (256, 12288, 256, "four-wave GEMM, 128 x 128 tiles, one launch"),
+    (192, 12288, 256, "four-wave GEMM, 128 x 128 tiles, a third of the rows empty"),
     (320, 12288, 256, "four-wave GEMM, 64 x 256 tiles, one launch"),
     (512, 12288, 256, "four-wave GEMM, 64 x 384 tiles (nibbles), one launch"),
     (1024, 6144, 256, "four-wave GEMM, 128 x 256 tiles for 3/4 of a round (int8) / 64 x 384 (nibbles)"),
