@@ -993,12 +993,13 @@ static bool use_gemm4_wide_short(int M, int N, int nb) {
 }
 
 // 128 x 256 four-wave tiles (128 x 384 where gemm4_ntw picks them) that fill
-// three quarters of a round or more but less than one, where none of the
-// narrower one-round forms above applies: in place of the eight-wave kernel
-// (int8 6144 x 4096 at M = 1024, 192 tiles: 78.3 against 117.0 us).
+// half a round or more but less than one, where none of the narrower
+// one-round forms above applies: in place of the eight-wave kernel (int8
+// 6144 x 4096 at M = 1024, 192 tiles: 78.3 against 117.0 us; at M = 768, 144
+// tiles: 77.7 against 115.3).
 static bool use_gemm4_part(int M, int N, int nb) {
   const int64_t tiles4 = (int64_t)((M + 127) / 128) * ((N + 255) / 256);
-  return (nb & 1) == 0 && tiles4 * 4 >= 3 * (int64_t)num_cus() && tiles4 < num_cus();
+  return (nb & 1) == 0 && tiles4 * 2 >= (int64_t)num_cus() && tiles4 < num_cus();
 }
 
 // 64 x 128 four-wave tiles, one launch, in place of the K split for a short K

@@ -152,6 +152,7 @@ XTF_CASES = [
     (512, 12288, 256, "four-wave GEMM, 64 x 384 tiles (nibbles), one launch"),
     (1024, 6144, 256, "four-wave GEMM, 128 x 256 tiles for 3/4 of a round (int8) / 64 x 384 (nibbles)"),
     (1536, 6144, 256, "four-wave GEMM, 64 x 128 tiles over 5 rounds (int8) / 128 x 384 (nibbles)"),
+    (768, 6144, 256, "four-wave GEMM, 128 x 256 tiles for 9/16 of a round (int8) / 64 x 384 (nibbles)"),
     (2048, 4096, 256, "four-wave GEMM, 128 x 256 tiles"),
     (1024, 12288, 256, "four-wave GEMM, 128 x 384 tiles (nibbles) / 128 x 256 (int8)"),
     (512, 4096, 384, "eight-wave GEMM (odd block count)"),
