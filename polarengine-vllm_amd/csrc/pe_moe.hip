@@ -213,6 +213,8 @@ __global__ __launch_bounds__(64 * kRouteWaves) void moe_route_kernel(RouteParams
 //  * transform workgroups: FWHT-128 of x into pair f16, one 128-block per
 //    16-lane group;
 //  * with the ids given (route_wgs == 0), one more workgroup buckets them.
+// With more than kFrontBucketMaxPairs pairs the bucketing is left to
+// moe_bucket_kernel, launched next (bucket_here == 0).
 // Bucketing (one workgroup): LDS histogram of the T*top_k (token, slot) pairs
 // by expert, exclusive scan, scatter -> per-expert offsets, the token of each
 // sorted pair, the sorted position of each pair (-1 for an id outside
@@ -231,6 +233,7 @@ struct FrontArgs {
   int32_t* sorted_token;  // [P]
   int32_t* pair_pos;      // [P]
   uint32_t* done;         // routing completion counter (zero; left zero)
+  int bucket_here;        // 0: moe_bucket_kernel buckets the pairs after this launch
   uint16_t* out;          // [T, H]
 };
 
@@ -331,6 +334,7 @@ __global__ __launch_bounds__(kFrontThreads) void moe_front_kernel(FrontArgs a) {
   int bid = blockIdx.x;
   if (bid < a.route_wgs) {
     route_tokens<true>(a.r, (int64_t)bid * kRouteWaves);
+    if (!a.bucket_here) return;  // uniform: the next launch buckets the ids
     // this workgroup's ids are stored once every thread's vmcnt drains
     // (stores count there on this architecture); then it is counted in
     __builtin_amdgcn_s_waitcnt(0);
@@ -358,6 +362,85 @@ __global__ __launch_bounds__(kFrontThreads) void moe_front_kernel(FrontArgs a) {
   else load8<PE_DTYPE_F16>(a.x + blk * kBlock + q * 8, v);
   fwht128_group16(v, q);
   store_pair_block(v, q, a.xtf + blk * 64, live);
+}
+
+// moe_bucket_kernel: the bucketing of moe_align_block for many pairs (P >
+// kFrontBucketMaxPairs), as a launch of its own after the routing: one
+// workgroup of 1024 threads; every pair takes its slot in its expert with an
+// LDS atomic as its id is read, the sorted token list is built in LDS
+// (dynamic, 4 bytes per pair) and written out in order, so no store is
+// scattered over memory (from one CU, the scattered stores of 16384 pairs
+// took about 8 us of the front launch's 24 at 2048 tokens). Ids outside
+// 0..E-1 (given ids only) get position -1, and the output rows of tokens
+// without one valid slot are zeroed here, as in moe_align_block.
+constexpr int kBucketThreads = 1024;
+constexpr int kBucketPerThread = 32;  // pairs per thread in registers: P <= 32768
+constexpr int kFrontBucketMaxPairs = 2048;
+
+__global__ __launch_bounds__(kBucketThreads) void moe_bucket_kernel(FrontArgs a) {
+  extern __shared__ int32_t sorted_lds[];
+  __shared__ int cnt[256];
+  __shared__ int base[257];
+  __shared__ int wtot[kBucketThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int E = a.r.E, top_k = a.r.top_k;
+  const int P = (int)(a.r.T * top_k);
+  for (int e = tid; e < E; e += kBucketThreads) cnt[e] = 0;
+  __syncthreads();
+  int ids[kBucketPerThread], rank[kBucketPerThread];
+#pragma unroll
+  for (int u = 0; u < kBucketPerThread; ++u) {
+    const int p = tid + kBucketThreads * u;
+    ids[u] = p < P ? a.r.topk_ids[p] : -1;
+  }
+#pragma unroll
+  for (int u = 0; u < kBucketPerThread; ++u) {
+    const bool ok = ids[u] >= 0 && ids[u] < E;
+    rank[u] = ok ? atomicAdd(&cnt[ids[u]], 1) : -1;
+  }
+  __syncthreads();
+  // exclusive scan over the experts, thread e holding cnt[e] (E <= 256: four waves)
+  const int v = tid < E ? cnt[tid] : 0;
+  int incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) wtot[wave] = incl;
+  __syncthreads();
+  int before = 0;
+  for (int w = 0; w < wave; ++w) before += wtot[w];
+  if (tid < E) base[tid] = before + incl - v;
+  if (tid == E - 1) base[E] = before + incl;
+  __syncthreads();
+  for (int e = tid; e <= E; e += kBucketThreads) a.offsets[e] = base[e];
+#pragma unroll
+  for (int u = 0; u < kBucketPerThread; ++u) {
+    const int p = tid + kBucketThreads * u;
+    if (p >= P) continue;
+    int pos = -1;
+    if (rank[u] >= 0) {
+      pos = base[ids[u]] + rank[u];
+      sorted_lds[pos] = p / top_k;
+    }
+    a.pair_pos[p] = pos;
+  }
+  __syncthreads();
+  const int valid = base[E];
+  for (int i = tid; i < valid; i += kBucketThreads) a.sorted_token[i] = sorted_lds[i];
+  if (a.route_wgs == 0) {  // given ids: tokens without a valid slot
+    const int64_t H = (int64_t)a.nbc * kBlock;
+    for (int64_t t = tid; t < a.r.T; t += kBucketThreads) {
+      bool any = false;
+      for (int k = 0; k < top_k; ++k) {
+        const int e = a.r.topk_ids[t * top_k + k];
+        any = any || (e >= 0 && e < E);
+      }
+      if (!any)
+        for (int64_t c = 0; c < H; ++c) a.out[t * H + c] = 0;
+    }
+  }
 }
 
 // out[t, c..c+3] = sum_k w[t, k] * y2[pos(t, k), c..c+3], k in order; 4
@@ -533,9 +616,22 @@ static int moe_run(const void* x, int x_dtype, int64_t T, int H, int I, int E, i
     f.pair_pos = pair_pos;
     f.done = reinterpret_cast<uint32_t*>(ws);  // counter block word 0
     f.out = reinterpret_cast<uint16_t*>(out);
-    const int grid = f.route_wgs + f.fwht_wgs + (route ? 0 : 1);
+    // many pairs: the bucketing in a launch of its own (moe_bucket_kernel)
+    const bool bucket_apart = P > kFrontBucketMaxPairs && P <= (int64_t)kBucketThreads * kBucketPerThread;
+    f.bucket_here = bucket_apart ? 0 : 1;
+    const int grid = f.route_wgs + f.fwht_wgs + (route || bucket_apart ? 0 : 1);
     moe_front_kernel<<<dim3((unsigned)grid), dim3(kFrontThreads), 0, st>>>(f);
     if (int rc = launch_status()) return rc;
+    if (bucket_apart) {
+      const size_t lds = (size_t)P * 4;
+      static const bool attr_ok = [] {
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(moe_bucket_kernel),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024) == hipSuccess;
+      }();
+      (void)attr_ok;
+      moe_bucket_kernel<<<dim3(1), dim3(kBucketThreads), lds, st>>>(f);
+      if (int rc = launch_status()) return rc;
+    }
   }
   const float* wts = route ? reinterpret_cast<const float*>(ws + L.topk_w) : topk_w;
   // 2. gate/up + SwiGLU, each 128-column block of h transformed in the same
