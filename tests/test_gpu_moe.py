@@ -45,11 +45,13 @@ def test_routed_equals_given_ids(tile):
     assert torch.equal(y_routed, y_given)
 
 
-@pytest.mark.parametrize("b2", [4, 6])  # w2 chunks of 256 (nibbles) and 128 (int8) columns
-def test_invalid_and_duplicate_slots(b2):
-    say(f"moe invalid/duplicate slots q{b2}")
-    rng = np.random.default_rng(910 + b2)
-    e, hdim, inter, t, k = 8, 384, 256, 12, 3
+# w2 chunks of 256 (nibbles) and 128 (int8) columns; t = 800: 2400 pairs, bucketed
+# by a launch of its own (above 2048 pairs)
+@pytest.mark.parametrize("b2,t", [(4, 12), (6, 12), (4, 800)])
+def test_invalid_and_duplicate_slots(b2, t):
+    say(f"moe invalid/duplicate slots q{b2} t={t}")
+    rng = np.random.default_rng(910 + b2 + t)
+    e, hdim, inter, k = 8, 384, 256, 3
     meth, layer, (w13, w2) = _layer(rng, e, hdim, inter, 3, b2)
     x = O.seeded_normal((t, hdim), 1.0, 911)
     ids = rng.integers(0, e, (t, k)).astype(np.int32)
