@@ -807,12 +807,12 @@ static int launch_gemm4_t(const GemmArgs& a, hipStream_t st, int ksplit = 1) {
 }
 
 // Grouped expert products on the four-wave kernel, 128 x 256 tiles: GRP 1
-// (SE_F32) fp32 rows y[pair][N]; GRP 2 (SE_SWIGLU_XTF) the transformed
-// silu(gate) * up as pair-f16 rows of I / 128 blocks.
-template <bool NIB, bool MASK, int GRP>
+// (SE_F32 / SE_F16) fp32 or 16-bit rows y[pair][N]; GRP 2 (SE_SWIGLU_XTF) the
+// transformed silu(gate) * up as pair-f16 rows of I / 128 blocks.
+template <bool NIB, bool MASK, int GRP, int OMX = OM_F32>
 static int launch_moe_gemm4_t(const MoeGemmArgs& a, hipStream_t st) {
   constexpr int TMW = 4, NTW = 2, BM = TMW * 32, BN = 128 * NTW;
-  constexpr int OM = GRP == 1 ? OM_F32 : OM_F16;
+  constexpr int OM = GRP == 1 ? OMX : OM_F16;
   auto kern = gemm4_kernel<NIB, TMW, NTW, MASK, OM, GRP>;
   const int entries = table_entries(NIB, a.n_levels);
   const size_t lds_loop = (size_t)entries * 256 + kA4Ring * (size_t)BM * kARow4;
@@ -830,11 +830,11 @@ static int launch_moe_gemm4_t(const MoeGemmArgs& a, hipStream_t st) {
   const int64_t tiles_n = GRP == 2 ? a.g.I / 128 : (a.N + BN - 1) / BN;
   if (tiles_m > INT32_MAX || tiles_n > 65535 || tiles_n < 1) return PE_ERR_DIMS;
   const uint8_t mb = NIB ? (uint8_t)((a.n_levels - 1) * 0x11) : (uint8_t)(a.n_levels - 1);
-  const int vec_ok = GRP == 1 && (uintptr_t)a.y % 16 == 0 && (a.ldy * 4) % 16 == 0;
+  const int vec_ok = GRP == 1 && (uintptr_t)a.y % 16 == 0 && (a.ldy * (OM == OM_F16 ? 2 : 4)) % 16 == 0;
   kern<<<dim3((unsigned)tiles_m, (unsigned)tiles_n), dim3(256), lds, st>>>(
       a.codes, a.norms, a.ct, a.n_levels, 0x01010101u * mb, entries,
-      reinterpret_cast<const uint32_t*>(a.xp), a.y, nullptr, 0, a.N, a.nb, a.ldy, 0, 0, a.lay, vec_ok, 0,
-      a.g);
+      reinterpret_cast<const uint32_t*>(a.xp), a.y, nullptr, 0, a.N, a.nb, a.ldy, 0, 0, a.lay, vec_ok,
+      GRP == 1 && OM == OM_F16 ? a.ybf : 0, a.g);
   return launch_status();
 }
 
@@ -851,6 +851,11 @@ int moe_gemm4(bool nibble, int epilogue, const MoeGemmArgs& a, hipStream_t st) {
   if (epilogue == SE_F32) {
     if (nibble) return mask ? launch_moe_gemm4_t<true, true, 1>(a, st) : launch_moe_gemm4_t<true, false, 1>(a, st);
     return mask ? launch_moe_gemm4_t<false, true, 1>(a, st) : launch_moe_gemm4_t<false, false, 1>(a, st);
+  }
+  if (epilogue == SE_F16) {
+    if (nibble)
+      return mask ? launch_moe_gemm4_t<true, true, 1, OM_F16>(a, st) : launch_moe_gemm4_t<true, false, 1, OM_F16>(a, st);
+    return mask ? launch_moe_gemm4_t<false, true, 1, OM_F16>(a, st) : launch_moe_gemm4_t<false, false, 1, OM_F16>(a, st);
   }
   if (epilogue == SE_SWIGLU_XTF) {
     if (nibble) return mask ? launch_moe_gemm4_t<true, true, 2>(a, st) : launch_moe_gemm4_t<true, false, 2>(a, st);

@@ -82,11 +82,12 @@ struct MoeGemmArgs {
   WLayout lay;
   int nb;          // 128-blocks of K (any count)
   const void* xp;  // pair-f16 activations [a_total_rows][nb][64]
-  void* y;         // SE_F32: fp32 [pairs][ldy]; SE_SWIGLU_XTF: pair-f16 rows of ldy halves
+  void* y;         // SE_F32 / SE_F16: [pairs][ldy]; SE_SWIGLU_XTF: pair-f16 rows of ldy halves
   int64_t ldy;
-  int N;      // SE_F32: output columns; SE_SWIGLU_XTF: weight rows (2 I)
+  int N;      // SE_F32 / SE_F16: output columns; SE_SWIGLU_XTF: weight rows (2 I)
   int64_t P;  // pair rows over all groups
   GemmGroup g;
+  int ybf = 0;  // SE_F16: the 16-bit rows are bfloat16
 };
 bool moe_gemm4_fits(const MoeGemmArgs& a, int epilogue);
 int moe_gemm4(bool nibble, int epilogue, const MoeGemmArgs& a, hipStream_t st);

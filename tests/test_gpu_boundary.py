@@ -131,15 +131,18 @@ def test_bf16_xtf_entry_and_fp32_input():
         GLOBAL_FWHT_CACHE.clear()
 
 
-def test_bf16_moe_forward():
-    say("bf16 moe")
+# t = 600: 2400 pairs, 150 rows per expert: the prefill regime (grouped GEMM,
+# bf16 expert rows for the combine) and the bucketing launch
+@pytest.mark.parametrize("t", [40, 600])
+def test_bf16_moe_forward(t):
+    say(f"bf16 moe t={t}")
     from test_gpu_kernels import _moe_layer
     rng = np.random.default_rng(630)
     meth, layer, (w13, w2) = _moe_layer(rng, 16, 512, 384, 3, 4)
-    xd, x32 = bf16_dev(O.seeded_normal((40, 512), 1.0, 631, np.float32))
-    logits = O.seeded_normal((40, 16), 1.0, 632, np.float32)
+    xd, x32 = bf16_dev(O.seeded_normal((t, 512), 1.0, 631, np.float32))
+    logits = O.seeded_normal((t, 16), 1.0, 632, np.float32)
     y = meth.apply(layer, xd, to_dev(logits), 4, True)
-    assert y.dtype == torch.bfloat16 and y.shape == (40, 512)
+    assert y.dtype == torch.bfloat16 and y.shape == (t, 512)
     w_ref, ids_ref = O.moe_route(logits, 4, True)
     want = O.moe_forward(x32, w_ref, ids_ref, w13, w2).astype(np.float32)
     check_close(_bits_to_f32(y), want, "bf16 moe")
