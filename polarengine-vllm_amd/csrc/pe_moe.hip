@@ -443,10 +443,10 @@ __global__ __launch_bounds__(kBucketThreads) void moe_bucket_kernel(FrontArgs a)
   }
 }
 
-// out[t, c..c+3] = sum_k w[t, k] * y2[pos(t, k), c..c+3], k in order; 4
-// columns per lane, the loads of eight slots issued before their sums (top-8
-// in one memory round trip). y2 rows are fp32 (YT = float) or 16-bit (YT =
-// uint16_t: bfloat16 if y2bf, else fp16).
+// out[t, c..] = sum_k w[t, k] * y2[pos(t, k), c..], k in order; 4 (fp32
+// rows) or 8 (16-bit rows) columns per lane, the loads of eight slots issued
+// before their sums (top-8 in one memory round trip). y2 rows are fp32 (YT =
+// float) or 16-bit (YT = uint16_t: bfloat16 if y2bf, else fp16).
 constexpr int kCombineBatch = 8;
 
 template <typename YT>
@@ -455,46 +455,52 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const YT* __restrict__
                                                           const int32_t* __restrict__ pair_pos,
                                                           int64_t T, int top_k, int H,
                                                           uint16_t* __restrict__ out, int ybf) {
-  const int per_row = H / 4;
+  // columns per lane: one 16-byte load of each slot's row
+  constexpr int CPL = 16 / sizeof(YT);
+  const int per_row = H / CPL;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= T * per_row) return;
   const int64_t t = i / per_row;
-  const int c = (int)(i - t * per_row) * 4;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  const int c = (int)(i - t * per_row) * CPL;
+  float acc[CPL];
+#pragma unroll
+  for (int q = 0; q < CPL; ++q) acc[q] = 0.f;
   for (int k0 = 0; k0 < top_k; k0 += kCombineBatch) {
     int pos[kCombineBatch];
     float w[kCombineBatch];
-    float4 yv[kCombineBatch];
+    uint4 yv[kCombineBatch];
 #pragma unroll
     for (int u = 0; u < kCombineBatch; ++u) {
       const int k = k0 + u;
       pos[u] = k < top_k ? pair_pos[t * top_k + k] : -1;
       w[u] = pos[u] >= 0 ? topk_w[t * top_k + k] : 0.f;
-      if constexpr (sizeof(YT) == 4) {
-        yv[u] = pos[u] >= 0 ? *reinterpret_cast<const float4*>(y2 + (int64_t)pos[u] * H + c)
-                            : make_float4(0.f, 0.f, 0.f, 0.f);
-      } else {
-        const uint2 hv =
-            pos[u] >= 0 ? *reinterpret_cast<const uint2*>(y2 + (int64_t)pos[u] * H + c) : make_uint2(0u, 0u);
-        const uint16_t h[4] = {(uint16_t)(hv.x & 0xffff), (uint16_t)(hv.x >> 16), (uint16_t)(hv.y & 0xffff),
-                               (uint16_t)(hv.y >> 16)};
-        yv[u] = y2bf ? make_float4(bf2f(h[0]), bf2f(h[1]), bf2f(h[2]), bf2f(h[3]))
-                     : make_float4(h2f(h[0]), h2f(h[1]), h2f(h[2]), h2f(h[3]));
-      }
+      yv[u] = pos[u] >= 0 ? *reinterpret_cast<const uint4*>(y2 + (int64_t)pos[u] * H + c) : make_uint4(0u, 0u, 0u, 0u);
     }
 #pragma unroll
     for (int u = 0; u < kCombineBatch; ++u) {
       if (pos[u] < 0) continue;
-      acc[0] += w[u] * yv[u].x;
-      acc[1] += w[u] * yv[u].y;
-      acc[2] += w[u] * yv[u].z;
-      acc[3] += w[u] * yv[u].w;
+      const uint32_t d[4] = {yv[u].x, yv[u].y, yv[u].z, yv[u].w};
+#pragma unroll
+      for (int q = 0; q < CPL; ++q) {
+        float v;
+        if constexpr (sizeof(YT) == 4) {
+          v = __builtin_bit_cast(float, d[q]);
+        } else {
+          const uint16_t h = (uint16_t)(d[q >> 1] >> (16 * (q & 1)));
+          v = y2bf ? bf2f(h) : h2f(h);
+        }
+        acc[q] += w[u] * v;
+      }
     }
   }
-  uint2 o;
-  o.x = pack16x2(acc[0], acc[1], ybf != 0);
-  o.y = pack16x2(acc[2], acc[3], ybf != 0);
-  *reinterpret_cast<uint2*>(out + t * H + c) = o;
+  uint32_t o[CPL / 2];
+#pragma unroll
+  for (int q = 0; q < CPL / 2; ++q) o[q] = pack16x2(acc[2 * q], acc[2 * q + 1], ybf != 0);
+  if constexpr (CPL == 8) {
+    *reinterpret_cast<uint4*>(out + t * H + c) = make_uint4(o[0], o[1], o[2], o[3]);
+  } else {
+    *reinterpret_cast<uint2*>(out + t * H + c) = make_uint2(o[0], o[1]);
+  }
 }
 
 struct MoeWs {
@@ -681,7 +687,7 @@ static int moe_run(const void* x, int x_dtype, int64_t T, int H, int I, int E, i
     }
   }
   // 4. weighted combine -> out (x's dtype)
-  const int64_t work = T * (H / 4);
+  const int64_t work = T * (H / (y2_16 ? 8 : 4));
   if (y2_16)
     moe_combine_kernel<uint16_t><<<dim3((unsigned)((work + 255) / 256)), dim3(256), 0, st>>>(
         reinterpret_cast<const uint16_t*>(ws + L.y2), xbf, wts, pair_pos, T, top_k, H,
