@@ -40,7 +40,26 @@ def _draw(n_cases=48, seed=2024):
     return cases
 
 
-@pytest.mark.parametrize("m,n,k,bits,tiled,bf16,with_bias,idx", _draw())
+def _draw_prefill(n_cases=24, seed=2025):
+    """Larger prefill shapes, where the four-wave tile forms are chosen by how
+    many tiles fill a round of CUs (128 x 128 / 256 / 384, 64 x 128 / 256 /
+    384, the K split): M 96..1536, N up to 12288 and ragged, odd block counts
+    included."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < n_cases:
+        m = int(rng.choice([96, 160, 192, 200, 320, 384, 448, 512, 640, 768, 1024, 1280, 1536]))
+        n = int(rng.choice([2048, 3072, 4096, 6144, 8192, 12288])) - int(rng.choice([0, 0, 16, 40]))
+        k = 128 * int(rng.choice([2, 3, 4, 8, 16, 32]))
+        bits = int(rng.integers(2, 9))
+        if m * n * k > 3e9:
+            continue
+        cases.append((m, n, k, bits, bool(rng.random() < 0.6), bool(rng.random() < 0.5),
+                      bool(rng.random() < 0.5), 100 + len(cases)))
+    return cases
+
+
+@pytest.mark.parametrize("m,n,k,bits,tiled,bf16,with_bias,idx", _draw() + _draw_prefill())
 def test_random_shape(m, n, k, bits, tiled, bf16, with_bias, idx):
     from polarengine_vllm import _lib
     say(f"sweep #{idx} m={m} n={n} k={k} q{bits} tiled={tiled} bf16={bf16} bias={with_bias}")
