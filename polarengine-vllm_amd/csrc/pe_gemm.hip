@@ -1090,49 +1090,43 @@ static int launch_gemm_eight(const GemmArgs& a, hipStream_t st, int ksplit) {
   }
 }
 
+// the four-wave kernel with the code mask its codebook size needs
+template <bool NIB, int TMW, int NTW, int OM>
+static int launch_gemm4_m(const GemmArgs& a, hipStream_t st, int ksplit = 1) {
+  const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
+  return mask ? launch_gemm4_t<NIB, TMW, NTW, true, OM>(a, st, ksplit)
+              : launch_gemm4_t<NIB, TMW, NTW, false, OM>(a, st, ksplit);
+}
+
 template <bool NIB, int OM>
 static int launch_gemm_shape(const GemmArgs& a, hipStream_t st, void* ws, size_t ws_bytes) {
+  // 128 x 256 or 128 x 384 tiles for one round or more (int8: 64 x 128 where
+  // those rounds cost less)
   if (use_gemm4(a.M, a.N, a.nb)) {
-    const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
     if constexpr (NIB && OM == OM_F16) {
-      if (gemm4_ntw(NIB, a.M, a.N, OM) == 3)
-        return mask ? launch_gemm4_t<NIB, 4, 3, true, OM>(a, st) : launch_gemm4_t<NIB, 4, 3, false, OM>(a, st);
+      if (gemm4_ntw(NIB, a.M, a.N, OM) == 3) return launch_gemm4_m<NIB, 4, 3, OM>(a, st);
     }
     if constexpr (!NIB && OM == OM_F16) {
-      if (gemm4_int8_narrow(a.M, a.N))
-        return mask ? launch_gemm4_t<NIB, 2, 1, true, OM>(a, st) : launch_gemm4_t<NIB, 2, 1, false, OM>(a, st);
+      if (gemm4_int8_narrow(a.M, a.N)) return launch_gemm4_m<NIB, 2, 1, OM>(a, st);
     }
-    return mask ? launch_gemm4_t<NIB, 4, 2, true, OM>(a, st) : launch_gemm4_t<NIB, 4, 2, false, OM>(a, st);
+    return launch_gemm4_m<NIB, 4, 2, OM>(a, st);
   }
+  // fewer tiles than a round: the one-round forms, widest dequantization first
   if constexpr (NIB && OM == OM_F16) {
-    if (use_gemm4_wide_short(a.M, a.N, a.nb)) {
-      const bool mask = a.n_levels != 16;
-      return mask ? launch_gemm4_t<NIB, 2, 3, true, OM>(a, st) : launch_gemm4_t<NIB, 2, 3, false, OM>(a, st);
-    }
+    if (use_gemm4_wide_short(a.M, a.N, a.nb)) return launch_gemm4_m<NIB, 2, 3, OM>(a, st);
   }
   if constexpr (OM == OM_F16) {
-    if (use_gemm4_sq(a.M, a.N, a.nb)) {
-      const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
-      return mask ? launch_gemm4_t<NIB, 4, 1, true, OM>(a, st) : launch_gemm4_t<NIB, 4, 1, false, OM>(a, st);
-    }
-    if (use_gemm4_short(a.M, a.N, a.nb)) {
-      const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
-      return mask ? launch_gemm4_t<NIB, 2, 2, true, OM>(a, st) : launch_gemm4_t<NIB, 2, 2, false, OM>(a, st);
-    }
+    if (use_gemm4_sq(a.M, a.N, a.nb)) return launch_gemm4_m<NIB, 4, 1, OM>(a, st);
+    if (use_gemm4_short(a.M, a.N, a.nb)) return launch_gemm4_m<NIB, 2, 2, OM>(a, st);
   }
   if (use_gemm4_part(a.M, a.N, a.nb)) {
-    const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
     if constexpr (NIB && OM == OM_F16) {
-      if (gemm4_ntw(NIB, a.M, a.N, OM) == 3)
-        return mask ? launch_gemm4_t<NIB, 4, 3, true, OM>(a, st) : launch_gemm4_t<NIB, 4, 3, false, OM>(a, st);
+      if (gemm4_ntw(NIB, a.M, a.N, OM) == 3) return launch_gemm4_m<NIB, 4, 3, OM>(a, st);
     }
-    return mask ? launch_gemm4_t<NIB, 4, 2, true, OM>(a, st) : launch_gemm4_t<NIB, 4, 2, false, OM>(a, st);
+    return launch_gemm4_m<NIB, 4, 2, OM>(a, st);
   }
   if constexpr (OM == OM_F16) {
-    if (use_gemm4_narrow(a.M, a.N, a.nb)) {
-      const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
-      return mask ? launch_gemm4_t<NIB, 2, 1, true, OM>(a, st) : launch_gemm4_t<NIB, 2, 1, false, OM>(a, st);
-    }
+    if (use_gemm4_narrow(a.M, a.N, a.nb)) return launch_gemm4_m<NIB, 2, 1, OM>(a, st);
   }
   // fp16 out (the linear entry points): split K when the tiles are few and
   // the workspace holds the partial sums; otherwise one launch
@@ -1142,18 +1136,11 @@ static int launch_gemm_shape(const GemmArgs& a, hipStream_t st, void* ws, size_t
     p.y = ws;
     p.ldy = a.N;
     p.bias = nullptr;
-    const bool mask = NIB ? a.n_levels != 16 : a.n_levels != 256;
-    const int rc = gemm4_split_rows(a.M) == 64
-                       ? (gemm4_split_cols(a.M) == 128
-                              ? (mask ? launch_gemm4_t<NIB, 2, 1, true, OM_F32>(p, st, z4)
-                                      : launch_gemm4_t<NIB, 2, 1, false, OM_F32>(p, st, z4))
-                              : (mask ? launch_gemm4_t<NIB, 2, 2, true, OM_F32>(p, st, z4)
-                                      : launch_gemm4_t<NIB, 2, 2, false, OM_F32>(p, st, z4)))
-                   : gemm4_split_cols(a.M) == 128
-                       ? (mask ? launch_gemm4_t<NIB, 4, 1, true, OM_F32>(p, st, z4)
-                               : launch_gemm4_t<NIB, 4, 1, false, OM_F32>(p, st, z4))
-                       : (mask ? launch_gemm4_t<NIB, 4, 2, true, OM_F32>(p, st, z4)
-                               : launch_gemm4_t<NIB, 4, 2, false, OM_F32>(p, st, z4));
+    const bool rows64 = gemm4_split_rows(a.M) == 64, cols128 = gemm4_split_cols(a.M) == 128;
+    const int rc = rows64 ? (cols128 ? launch_gemm4_m<NIB, 2, 1, OM_F32>(p, st, z4)
+                                     : launch_gemm4_m<NIB, 2, 2, OM_F32>(p, st, z4))
+                          : (cols128 ? launch_gemm4_m<NIB, 4, 1, OM_F32>(p, st, z4)
+                                     : launch_gemm4_m<NIB, 4, 2, OM_F32>(p, st, z4));
     if (rc) return rc;
     return split_reduce(reinterpret_cast<const float*>(ws), z4, a.M, a.N, a.bias, a.y, a.ldy, st,
                         a.ybf != 0);
