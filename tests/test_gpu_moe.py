@@ -8,7 +8,8 @@ finish buckets them, signalled through the workspace's counter block):
 * slots with an id outside 0..E-1 are skipped, a token without one valid
   slot is exactly zero, a token routed twice to one expert adds both slots
   (oracle.moe_forward at the north-star tolerance);
-* many routing workgroups (T = 2048: 512 of them);
+* many routing workgroups (T = 2048: 512 of them), and the pair counts at
+  the bucketing's limits (2048, 2049, 32768, 32776 pairs);
 * the workspace's counter block is zero again after every call, and a
   second call on the same workspace repeats the first bit for bit."""
 
@@ -126,6 +127,39 @@ def test_grouped_gemm_route_partial_tiles(tile):
     y = meth.apply(layer, to_dev(x), logits, k, True, custom_routing_function=given)
     want = O.moe_forward(x, wts, ids, w13, w2).astype(np.float32)
     check_close(y.float().cpu().numpy(), want, "moe grouped route, partial tiles")
+
+
+# (token, slot) pairs at the bucketing's limits: 2048 (bucketed by the routing
+# launch's last workgroup, ids held in registers), 2049 (moe_bucket_kernel),
+# 32768 (that kernel's largest), 32776 (the routing launch again, in batches)
+@pytest.mark.parametrize("t,k", [(512, 4), (683, 3), (4096, 8), (4097, 8)])
+def test_bucketing_at_pair_count_limits(t, k):
+    """Against the oracle, and bit for bit against the same call without
+    its last token: with 8 experts both stay on the grouped kernel (at least
+    128 rows per expert), every stage after the bucketing works per pair row
+    or per token, so a token's output cannot depend on which bucketing form
+    ordered the rows (the prefixes of 2049 and 32776 pairs, 2046 and 32768,
+    are bucketed by the other form)."""
+    say(f"moe bucketing limits t={t} k={k} pairs={t * k}")
+    rng = np.random.default_rng(950 + t)
+    e, hdim, inter = 8, 256, 256
+    meth, layer, (w13, w2) = _layer(rng, e, hdim, inter, 3, 4)
+    x = O.seeded_normal((t, hdim), 1.0, 951)
+    ids = rng.integers(0, e, (t, k)).astype(np.int32)
+    wts = (np.abs(O.seeded_normal((t, k), 1.0, 952, np.float32)) + 0.1).astype(np.float32)
+
+    def run(n):
+        def given(hidden_states, gating_output, topk, renormalize):
+            return to_dev(wts[:n]), to_dev(ids[:n])
+        logits = to_dev(np.zeros((n, e), np.float32))
+        return meth.apply(layer, to_dev(x[:n]), logits, k, True, custom_routing_function=given)
+
+    y = run(t)
+    want = O.moe_forward(x, wts, ids, w13, w2).astype(np.float32)
+    check_close(y.float().cpu().numpy(), want, f"moe pairs={t * k}")
+    y_prefix = run(t - 1)
+    torch.cuda.synchronize()
+    assert torch.equal(y[:-1], y_prefix), f"pairs={t * k}: rows depend on the bucketing form"
 
 
 def test_many_routing_workgroups():
